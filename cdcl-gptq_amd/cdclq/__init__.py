@@ -1,0 +1,412 @@
+"""cdclq -- MI355X-native CDCL-GPTQ per-layer quantization engine (Python host binding).
+
+Mirrors the reference crate's public engine API (tailot/CDCL-GPTQ `cdclq` 1.0.1):
+
+    engine::Config / Method / LayerStats      src/engine.rs:83-199   -> Config, Method, LayerStats
+    engine::quantize_layer(w, d_out, d_in, h, m, hkey, cfg, cache)
+                                              src/engine.rs:690-699  -> quantize_layer(...)
+    engine::PrepCache (Option<(String, Prepared)>)
+                                              src/engine.rs:220-223  -> PrepCache (owns a GPU context)
+    linalg::gram_accumulate(x, y, t, n, h)    src/linalg.rs:388      -> gram_accumulate(...)
+    linalg::upper_chol_of_inverse(h, n)       src/linalg.rs:362      -> upper_chol_of_inverse(...)
+    engine::proxy_loss                        src/engine.rs:808      -> proxy_loss(...)
+    quant::QLayer (+ dequantize, bits_*)      src/quant.rs:161-250   -> QLayer
+
+All computation runs in libcdclq_hip.so (hand-written gfx950 HIP kernels) through the C ABI in
+include/cdclq.h. There is no CPU fallback: importing this module on a machine without the built
+library, or calling it without a GPU, raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+import os
+from dataclasses import dataclass, field
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libcdclq_hip.so")
+
+OK, INVALID_ARG, NOT_PD, NON_FINITE, DEVICE, OOM = range(6)
+PHASE_GRAM, PHASE_FACTOR, PHASE_GPTQ, PHASE_REPAIR, PHASE_TARGET = range(5)
+PHASE_NAMES = ["gram", "factor", "gptq", "repair", "target"]
+
+
+class CdclqError(RuntimeError):
+    """Error raised by the engine. `code` is the cdclq_status value; the message is the
+    reference's anyhow text where the reference reports the same condition."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(msg)
+        self.code = code
+
+
+class _Config(C.Structure):
+    _fields_ = [
+        ("bits", C.c_uint32), ("skeleton_bits", C.c_uint32), ("group", C.c_uint64), ("block", C.c_uint64),
+        ("sub_block", C.c_uint64), ("cd_sweeps", C.c_uint64), ("passes", C.c_uint64), ("row_chunk", C.c_uint64),
+        ("damp", C.c_double), ("skeleton_pct", C.c_double), ("refine_frac", C.c_double), ("tol", C.c_double),
+        ("act_order", C.c_int32), ("mse_grid", C.c_int32), ("method", C.c_int32), ("refit_scales", C.c_int32),
+    ]
+
+
+class _Stats(C.Structure):
+    _fields_ = [
+        ("loss_gptq", C.c_double), ("loss_final", C.c_double), ("subblocks_total", C.c_uint64),
+        ("subblocks_refined", C.c_uint64), ("code_updates", C.c_uint64), ("skeleton_groups", C.c_uint64),
+        ("bits_codes", C.c_double), ("bits_total", C.c_double), ("secs_prepare", C.c_double),
+        ("secs_quant", C.c_double),
+    ]
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded libcdclq_hip.so (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: build it first (python -m cdclq.build or __graft_entry__.build())")
+    L = C.CDLL(LIB_PATH)
+    vp, sz, i32, u64 = C.c_void_p, C.c_size_t, C.c_int, C.c_uint64
+    cfgp, stp = C.POINTER(_Config), C.POINTER(_Stats)
+    sig = {
+        "cdclq_abi_version": ([], i32),
+        "cdclq_sizeof_config": ([], sz),
+        "cdclq_sizeof_stats": ([], sz),
+        "cdclq_default_config": ([cfgp], None),
+        "cdclq_num_groups": ([cfgp, sz], sz),
+        "cdclq_ctx_create": ([i32, C.POINTER(vp)], i32),
+        "cdclq_ctx_destroy": ([vp], None),
+        "cdclq_last_error": ([vp], C.c_char_p),
+        "cdclq_ctx_clear_cache": ([vp], i32),
+        "cdclq_quantize_layer": ([vp, vp, sz, sz, vp, vp, C.c_char_p, cfgp, sz, vp, vp, vp, vp, vp, stp], i32),
+        "cdclq_quantize_layer_device": ([vp, vp, sz, sz, vp, vp, C.c_char_p, cfgp, sz, vp, vp, vp, vp, vp, stp], i32),
+        "cdclq_gram_accumulate": ([vp, vp, vp, sz, sz, vp], i32),
+        "cdclq_gram_accumulate_device": ([vp, vp, vp, sz, sz, vp], i32),
+        "cdclq_upper_chol_of_inverse": ([vp, vp, sz, vp], i32),
+        "cdclq_upper_chol_of_inverse_device": ([vp, vp, sz, vp], i32),
+        "cdclq_proxy_loss": ([vp, vp, vp, sz, sz, vp, C.POINTER(C.c_double)], i32),
+        "cdclq_device_alloc": ([vp, sz, C.POINTER(vp)], i32),
+        "cdclq_device_free": ([vp, vp], i32),
+        "cdclq_memcpy_h2d": ([vp, vp, vp, sz], i32),
+        "cdclq_memcpy_d2h": ([vp, vp, vp, sz], i32),
+        "cdclq_memset_device": ([vp, vp, i32, sz], i32),
+        "cdclq_synth_normal_device": ([vp, u64, u64, sz, C.c_float, vp], i32),
+        "cdclq_synth_outlier_scales": ([u64, sz, C.c_double, C.c_float, vp], i32),
+        "cdclq_synth_tokens_device": ([vp, u64, u64, sz, sz, vp, vp], i32),
+        "cdclq_f64_to_f32_device": ([vp, vp, sz, vp], i32),
+        "cdclq_ctx_set_timing": ([vp, i32], i32),
+        "cdclq_ctx_reset_timing": ([vp], i32),
+        "cdclq_ctx_get_timing": ([vp, i32, C.POINTER(C.c_uint64), C.POINTER(C.c_double)], i32),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = res
+    _lib = L
+    return L
+
+
+EXPORTED_SYMBOLS = None  # filled lazily by exported_symbols()
+
+
+def exported_symbols() -> list[str]:
+    """Names of the C-ABI entry points this binding expects the library to export."""
+    return [
+        "cdclq_abi_version", "cdclq_sizeof_config", "cdclq_sizeof_stats", "cdclq_default_config",
+        "cdclq_num_groups", "cdclq_ctx_create", "cdclq_ctx_destroy", "cdclq_last_error", "cdclq_ctx_clear_cache",
+        "cdclq_quantize_layer", "cdclq_quantize_layer_device", "cdclq_gram_accumulate",
+        "cdclq_gram_accumulate_device", "cdclq_upper_chol_of_inverse", "cdclq_upper_chol_of_inverse_device",
+        "cdclq_proxy_loss", "cdclq_device_alloc", "cdclq_device_free", "cdclq_memcpy_h2d", "cdclq_memcpy_d2h",
+        "cdclq_memset_device", "cdclq_synth_normal_device", "cdclq_synth_outlier_scales", "cdclq_synth_tokens_device", "cdclq_f64_to_f32_device",
+        "cdclq_ctx_set_timing", "cdclq_ctx_reset_timing", "cdclq_ctx_get_timing",
+    ]
+
+
+class Method(enum.IntEnum):
+    """engine::Method (src/engine.rs:83-88)."""
+
+    Gptq = 0
+    Cdcl = 1
+
+
+@dataclass
+class Config:
+    """engine::Config with the reference defaults (src/engine.rs:94-167)."""
+
+    bits: int = 3
+    group: int = 128
+    block: int = 128
+    damp: float = 0.01
+    act_order: bool = True
+    skeleton_pct: float = 0.0
+    skeleton_bits: int = 8
+    mse_grid: bool = False
+    method: Method = Method.Cdcl
+    refine_frac: float = 1.0
+    sub_block: int = 64
+    cd_sweeps: int = 1
+    passes: int = 10
+    tol: float = 1e-3
+    refit_scales: bool = True
+    row_chunk: int = 0
+
+    def _c(self) -> _Config:
+        c = _Config()
+        for name, _ in _Config._fields_:
+            v = getattr(self, name)
+            setattr(c, name, int(v) if isinstance(v, (bool, enum.Enum)) else v)
+        return c
+
+
+def effective_group(cfg: Config, n: int) -> int:
+    """engine::effective_group (src/engine.rs:227-233)."""
+    return n if (cfg.group == 0 or cfg.group >= n) else cfg.group
+
+
+@dataclass
+class LayerStats:
+    """engine::LayerStats (src/engine.rs:174-199)."""
+
+    loss_gptq: float = 0.0
+    loss_final: float = 0.0
+    subblocks_total: int = 0
+    subblocks_refined: int = 0
+    code_updates: int = 0
+    skeleton_groups: int = 0
+    bits_codes: float = 0.0
+    bits_total: float = 0.0
+    secs_prepare: float = 0.0
+    secs_quant: float = 0.0
+
+
+@dataclass
+class QLayer:
+    """quant::QLayer (src/quant.rs:161-175): codes in permuted column order."""
+
+    d_out: int
+    d_in: int
+    group: int
+    perm: np.ndarray
+    gbits: np.ndarray
+    codes: np.ndarray
+    scales: np.ndarray
+    zeros: np.ndarray
+
+    def ngroups(self) -> int:
+        return int(self.gbits.size)
+
+    def dequantize(self) -> np.ndarray:
+        """QLayer::dequantize (src/quant.rs:189-202): original column order."""
+        g = self.group
+        gi = np.arange(self.d_in) // g
+        vals = self.scales[:, gi] * (self.codes.astype(np.float32) - self.zeros[:, gi])
+        out = np.zeros((self.d_out, self.d_in), np.float32)
+        out[:, self.perm.astype(np.int64)] = vals
+        return out
+
+    def bits_codes(self) -> float:
+        return float(self.gbits[np.arange(self.d_in) // self.group].astype(np.int64).sum()) / self.d_in
+
+    def bits_total(self) -> float:
+        return self.bits_codes() + 24.0 / self.group
+
+
+def _check(ctx_ptr, rc: int):
+    if rc != OK:
+        msg = lib().cdclq_last_error(ctx_ptr)
+        raise CdclqError(rc, msg.decode() if msg else f"cdclq error {rc}")
+
+
+class Context:
+    """A GPU context: HIP stream, device workspace and the one-entry factor cache."""
+
+    def __init__(self, device: int = 0):
+        L = lib()
+        p = C.c_void_p()
+        rc = L.cdclq_ctx_create(device, C.byref(p))
+        if rc != OK:
+            raise CdclqError(rc, f"cdclq_ctx_create(device={device}) failed (no usable GPU?)")
+        self.ptr = p
+        self.device = device
+
+    def close(self):
+        if getattr(self, "ptr", None) and _lib is not None:
+            _lib.cdclq_ctx_destroy(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        self.close()
+
+    def check(self, rc: int):
+        _check(self.ptr, rc)
+
+    def clear_cache(self):
+        self.check(lib().cdclq_ctx_clear_cache(self.ptr))
+
+    # ---- timing
+    def set_timing(self, on: bool):
+        self.check(lib().cdclq_ctx_set_timing(self.ptr, int(on)))
+
+    def reset_timing(self):
+        self.check(lib().cdclq_ctx_reset_timing(self.ptr))
+
+    def timing(self) -> dict:
+        out = {}
+        for i, name in enumerate(PHASE_NAMES):
+            n, ms = C.c_uint64(), C.c_double()
+            self.check(lib().cdclq_ctx_get_timing(self.ptr, i, C.byref(n), C.byref(ms)))
+            out[name] = {"launches": n.value, "ms": ms.value}
+        return out
+
+
+class PrepCache:
+    """engine::PrepCache handle: callers create it empty and pass it to every quantize_layer call
+    (src/engine.rs:220-223). It owns the GPU context holding the cached factorisation."""
+
+    def __init__(self, device: int = 0, ctx: Context | None = None):
+        self.ctx = ctx or Context(device)
+
+
+class DeviceArray:
+    """A device (HBM) buffer owned through the C ABI, with numpy-typed upload/download."""
+
+    def __init__(self, ctx: Context, shape, dtype):
+        self.ctx = ctx
+        self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = C.c_void_p()
+        ctx.check(lib().cdclq_device_alloc(ctx.ptr, self.nbytes, C.byref(p)))
+        self.ptr = p
+
+    @classmethod
+    def from_host(cls, ctx: Context, a: np.ndarray) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(ctx, a.shape, a.dtype)
+        d.upload(a)
+        return d
+
+    @property
+    def addr(self) -> int:
+        return int(self.ptr.value or 0)
+
+    def upload(self, a: np.ndarray):
+        a = np.ascontiguousarray(a, self.dtype)
+        assert a.nbytes == self.nbytes
+        self.ctx.check(lib().cdclq_memcpy_h2d(self.ctx.ptr, self.ptr, a.ctypes.data, self.nbytes))
+
+    def download(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        self.ctx.check(lib().cdclq_memcpy_d2h(self.ctx.ptr, out.ctypes.data, self.ptr, self.nbytes))
+        return out
+
+    def zero(self):
+        self.ctx.check(lib().cdclq_memset_device(self.ctx.ptr, self.ptr, 0, self.nbytes))
+
+    def free(self):
+        if getattr(self, "ptr", None) is not None and self.ptr.value and _lib is not None and self.ctx.ptr:
+            _lib.cdclq_device_free(self.ctx.ptr, self.ptr)
+        self.ptr = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, np.float32)
+
+
+def quantize_layer(w, d_out: int, d_in: int, h, m, hkey: str, cfg: Config, cache: PrepCache,
+                   nthreads: int = 24) -> tuple[QLayer, LayerStats]:
+    """engine::quantize_layer (src/engine.rs:690-799) on the GPU. `w` (d_out x d_in) and `h`
+    (d_in x d_in) are host arrays (f32); `m` is the optional cross-covariance or None.
+    `nthreads` stands in for rayon::current_num_threads() when cfg.row_chunk == 0."""
+    w = _f32(w).reshape(d_out, d_in)
+    h = _f32(h).reshape(d_in, d_in)
+    if m is not None:
+        m = _f32(m).reshape(d_in, d_in)
+    ctx = cache.ctx
+    n = d_in
+    g = effective_group(cfg, n)
+    ng = (n + g - 1) // g
+    codes = np.zeros((d_out, n), np.uint8)
+    scales = np.zeros((d_out, ng), np.float32)
+    zeros = np.zeros((d_out, ng), np.float32)
+    perm = np.zeros(n, np.uint32)
+    gbits = np.zeros(ng, np.uint8)
+    st = _Stats()
+    c = cfg._c()
+    rc = lib().cdclq_quantize_layer(ctx.ptr, w.ctypes.data, d_out, n, h.ctypes.data,
+                                    m.ctypes.data if m is not None else None, hkey.encode(), C.byref(c), nthreads,
+                                    codes.ctypes.data, scales.ctypes.data, zeros.ctypes.data, perm.ctypes.data,
+                                    gbits.ctypes.data, C.byref(st))
+    ctx.check(rc)
+    stats = LayerStats(**{f: getattr(st, f) for f, _ in _Stats._fields_})
+    return QLayer(d_out, n, g, perm, gbits, codes, scales, zeros), stats
+
+
+def quantize_layer_device(ctx: Context, w: DeviceArray, d_out: int, d_in: int, h: DeviceArray,
+                          m: DeviceArray | None, hkey: str, cfg: Config, codes: DeviceArray, scales: DeviceArray,
+                          zeros: DeviceArray, nthreads: int = 24):
+    """Device-resident variant: inputs and codes/scales/zeros stay in HBM. Returns (perm, gbits,
+    LayerStats) on the host."""
+    n = d_in
+    g = effective_group(cfg, n)
+    ng = (n + g - 1) // g
+    perm = np.zeros(n, np.uint32)
+    gbits = np.zeros(ng, np.uint8)
+    st = _Stats()
+    c = cfg._c()
+    ctx.check(lib().cdclq_quantize_layer_device(ctx.ptr, w.ptr, d_out, n, h.ptr, m.ptr if m is not None else None,
+                                                hkey.encode(), C.byref(c), nthreads, codes.ptr, scales.ptr,
+                                                zeros.ptr, perm.ctypes.data, gbits.ctypes.data, C.byref(st)))
+    return perm, gbits, LayerStats(**{f: getattr(st, f) for f, _ in _Stats._fields_})
+
+
+def gram_accumulate(x, y, t: int, n: int, h: np.ndarray, ctx: Context) -> np.ndarray:
+    """linalg::gram_accumulate (src/linalg.rs:388-418): h (f64, n x n) += x^T y, in place.
+    Pass the same array object for x and y for the symmetric Hessian."""
+    sym = y is x
+    x = _f32(x).reshape(t, n)
+    y = x if sym else _f32(y).reshape(t, n)
+    assert h.dtype == np.float64 and h.shape == (n, n) and h.flags.c_contiguous
+    ctx.check(lib().cdclq_gram_accumulate(ctx.ptr, x.ctypes.data, y.ctypes.data, t, n, h.ctypes.data))
+    return h
+
+
+def upper_chol_of_inverse(h64, n: int, ctx: Context) -> np.ndarray:
+    """linalg::upper_chol_of_inverse (src/linalg.rs:362-375)."""
+    h64 = np.ascontiguousarray(h64, np.float64).reshape(n, n)
+    u = np.zeros((n, n), np.float32)
+    ctx.check(lib().cdclq_upper_chol_of_inverse(ctx.ptr, h64.ctypes.data, n, u.ctypes.data))
+    return u
+
+
+def proxy_loss(w_t, w_hat, rows: int, n: int, h, ctx: Context) -> float:
+    """engine::proxy_loss (src/engine.rs:808-815)."""
+    w_t, w_hat, h = _f32(w_t), _f32(w_hat), _f32(h)
+    out = C.c_double()
+    ctx.check(lib().cdclq_proxy_loss(ctx.ptr, w_t.ctypes.data, w_hat.ctypes.data, rows, n, h.ctypes.data,
+                                     C.byref(out)))
+    return out.value
+
+
+def synth_outlier_scales(seed: int, n: int, frac: float, factor: float) -> np.ndarray:
+    """Channel-scale vector of the synthetic calibration inputs (see include/cdclq.h)."""
+    out = np.empty(n, np.float32)
+    rc = lib().cdclq_synth_outlier_scales(seed, n, frac, factor, out.ctypes.data)
+    if rc != OK:
+        raise CdclqError(rc, "cdclq_synth_outlier_scales failed")
+    return out
+
+
+def default_config() -> Config:
+    return Config()

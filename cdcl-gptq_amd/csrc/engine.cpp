@@ -1,0 +1,924 @@
+// Host side of the MI355X engine: the control flow of engine::quantize_layer
+// (src/engine.rs:690-799), build_prepared (:320-342) and process_chunk (:366-674), driving the
+// gfx950 kernels, plus the C-ABI entry points declared in include/cdclq.h.
+//
+// Only scalar bookkeeping runs on the host -- validation, the column permutation sort, the
+// damping mean, sub-block selection and the per-chunk convergence test -- with the reference's
+// exact f64 operation order. Every per-weight operation runs on the GPU.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "cdclq.h"
+#include "cdclq_dev.h"
+#include "kernels.h"
+
+namespace {
+
+using namespace cdclq;
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+};
+
+struct TimedRegion {
+  int phase;
+  hipEvent_t a, b;
+};
+
+double now_secs() {
+  using namespace std::chrono;
+  return duration<double>(steady_clock::now().time_since_epoch()).count();
+}
+
+// Rust's `{:e}` (LowerExp) of an f64: shortest round-trip digits, exponent without '+'/padding.
+std::string rust_lower_exp(double d) {
+  if (std::isnan(d)) return "NaN";
+  if (std::isinf(d)) return d < 0 ? "-inf" : "inf";
+  char buf[64];
+  for (int p = 0; p < 17; ++p) {
+    std::snprintf(buf, sizeof buf, "%.*e", p, d);
+    if (std::strtod(buf, nullptr) == d) break;
+  }
+  char* e = std::strchr(buf, 'e');
+  const int ex = std::atoi(e + 1);
+  *e = 0;
+  return std::string(buf) + "e" + std::to_string(ex);
+}
+
+}  // namespace
+
+struct cdclq_ctx {
+  int device = 0;
+  hipStream_t st = nullptr;
+  std::string err;
+  // workspace (grow-only)
+  DevBuf w_in, h_in, m_in, x_in, y_in, h64_in, u_out, codes_o, scales_o, zeros_o;
+  DevBuf wp, wwork, wq, ebuf, gbits_d, perm_d, deadp_d, dead_d, diag_d, colsq_d, invd, colloss_d;
+  DevBuf G, part, dlog, dcnt, active_d, sel_d, ld_d, upd_d, mp, t1, t2, a64, y64, tbuf, tpart, status_d, tiles_d,
+      proxy_p, cs_d;
+  int tiles_n = -1, tiles_sym = -1, tiles_count = 0;
+  // one-entry PrepCache (src/engine.rs:207-223): key, perm, damping and the device factors
+  bool cache_valid = false;
+  std::string cache_key;
+  std::vector<uint32_t> cache_perm;
+  size_t cache_n = 0;
+  double cache_damp = 0.0;
+  DevBuf cache_u, cache_h32;
+  // timing
+  bool timing = false;
+  std::vector<TimedRegion> pending;
+  double ms[CDCLQ_PHASE_COUNT] = {};
+  uint64_t launches[CDCLQ_PHASE_COUNT] = {};
+};
+
+namespace {
+
+int fail(cdclq_ctx* ctx, int code, const std::string& msg) {
+  ctx->err = msg;
+  return code;
+}
+
+#define HIPCK(expr)                                                                                   \
+  do {                                                                                                \
+    hipError_t e_ = (expr);                                                                           \
+    if (e_ != hipSuccess)                                                                             \
+      return fail(ctx, CDCLQ_DEVICE, std::string("HIP error '") + hipGetErrorString(e_) + "' in " #expr); \
+  } while (0)
+#define CK(expr)                       \
+  do {                                 \
+    int rc_ = (expr);                  \
+    if (rc_ != CDCLQ_OK) return rc_;   \
+  } while (0)
+
+int ensure(cdclq_ctx* ctx, DevBuf& b, size_t bytes) {
+  if (bytes == 0) bytes = 256;
+  if (b.cap >= bytes) return CDCLQ_OK;
+  if (b.p) {
+    hipError_t e = hipFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+    if (e != hipSuccess) return fail(ctx, CDCLQ_DEVICE, std::string("hipFree failed: ") + hipGetErrorString(e));
+  }
+  hipError_t e = hipMalloc(&b.p, bytes);
+  if (e != hipSuccess) {
+    b.p = nullptr;
+    (void)hipGetLastError();
+    return fail(ctx, CDCLQ_OOM, "device allocation of " + std::to_string(bytes) + " bytes failed (" +
+                                    hipGetErrorString(e) + ")");
+  }
+  b.cap = bytes;
+  return CDCLQ_OK;
+}
+
+template <class T>
+T* P(DevBuf& b) {
+  return static_cast<T*>(b.p);
+}
+
+void free_buf(DevBuf& b) {
+  if (b.p) (void)hipFree(b.p);
+  b.p = nullptr;
+  b.cap = 0;
+}
+
+struct PhaseScope {
+  cdclq_ctx* ctx;
+  int phase;
+  hipEvent_t a = nullptr;
+  PhaseScope(cdclq_ctx* c, int ph) : ctx(c), phase(ph) {
+    if (ctx->timing && hipEventCreate(&a) == hipSuccess) (void)hipEventRecord(a, ctx->st);
+  }
+  ~PhaseScope() {
+    if (!ctx->timing || !a) return;
+    hipEvent_t b = nullptr;
+    if (hipEventCreate(&b) == hipSuccess) {
+      (void)hipEventRecord(b, ctx->st);
+      ctx->pending.push_back({phase, a, b});
+    } else {
+      (void)hipEventDestroy(a);
+    }
+  }
+};
+
+void drain_timing(cdclq_ctx* ctx) {
+  for (auto& r : ctx->pending) {
+    float ms = 0.0f;
+    if (hipEventSynchronize(r.b) == hipSuccess && hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) {
+      ctx->ms[r.phase] += ms;
+      ctx->launches[r.phase] += 1;
+    }
+    (void)hipEventDestroy(r.a);
+    (void)hipEventDestroy(r.b);
+  }
+  ctx->pending.clear();
+}
+
+size_t effective_group(const cdclq_config* cfg, size_t n) {
+  return (cfg->group == 0 || cfg->group >= n) ? n : (size_t)cfg->group;
+}
+
+// src/engine.rs:240-258 (same messages)
+int validate(cdclq_ctx* ctx, const cdclq_config* cfg, size_t n) {
+  if (cfg->bits < 2 || cfg->bits > 8 || cfg->skeleton_bits < 2 || cfg->skeleton_bits > 8)
+    return fail(ctx, CDCLQ_INVALID_ARG, "bits and skeleton_bits must be in 2..=8");
+  if (cfg->block == 0 || cfg->sub_block == 0) return fail(ctx, CDCLQ_INVALID_ARG, "block and sub_block must be > 0");
+  const size_t g = effective_group(cfg, n);
+  if (g < n && cfg->block % g != 0 && g % cfg->block != 0)
+    return fail(ctx, CDCLQ_INVALID_ARG,
+                "group size " + std::to_string(g) + " must divide the block size " + std::to_string(cfg->block) +
+                    " (or be a multiple of it)");
+  if (cfg->skeleton_pct > 0.0 && g >= n) return fail(ctx, CDCLQ_INVALID_ARG, "the skeleton needs a finite group size");
+  if (!(cfg->refine_frac >= 0.0 && cfg->refine_frac <= 1.0))
+    return fail(ctx, CDCLQ_INVALID_ARG, "refine_frac must be in [0, 1]");
+  return CDCLQ_OK;
+}
+
+// Rust `sort_by(|a, b| key[b].partial_cmp(&key[a]).unwrap_or(Equal).then(a.cmp(&b)))`
+void sort_desc_index(std::vector<size_t>& idx, const std::vector<double>& key) {
+  std::stable_sort(idx.begin(), idx.end(), [&](size_t a, size_t b) {
+    const double ka = key[a], kb = key[b];
+    if (kb < ka) return true;
+    if (kb > ka) return false;
+    return a < b;
+  });
+}
+
+// U from the flipped matrix `a` (n x n f64, overwritten by L): blocked Cholesky, triangular inverse
+// of L into y, then U_ij = (f32) y[n-1-i][n-1-j] (src/linalg.rs:362-375).
+int factor(cdclq_ctx* ctx, int n, double* a, double* y, float* u) {
+  const int NB = 96;
+  hipStream_t st = ctx->st;
+  CK(ensure(ctx, ctx->status_d, 16));
+  int* status = P<int>(ctx->status_d);
+  double* pivot = reinterpret_cast<double*>(P<char>(ctx->status_d) + 8);
+  HIPCK(hipMemsetAsync(ctx->status_d.p, 0, 16, st));
+  for (int k = 0; k < n; k += NB) {
+    const int kb = std::min(NB, n - k), kend = k + kb;
+    HIPCK(chol_diag(st, n, a, k, kb, status, pivot));
+    if (kend < n) {
+      HIPCK(chol_panel(st, n, a, k, kb, status));
+      const long off = (long)kend * n + k;
+      HIPCK(gemm_chain<double>(st, n - kend, n - kend, kb, -1.0, 1, a + off, n, 1, a + off, 1, n,
+                               a + (long)kend * n + kend, n, 1, true, (double*)nullptr));
+    }
+  }
+  struct {
+    int status;
+    int pad;
+    double pivot;
+  } hs;
+  HIPCK(hipMemcpyAsync(&hs, ctx->status_d.p, 16, hipMemcpyDeviceToHost, st));
+  HIPCK(hipStreamSynchronize(st));
+  if (hs.status) {
+    return fail(ctx, CDCLQ_NOT_PD,
+                "matrix is not positive definite (pivot " + std::to_string(hs.status - 1) + " = " +
+                    rust_lower_exp(hs.pivot) + "); increase --damp or check the Hessian");
+  }
+  HIPCK(fill_zero_f64(st, y, (size_t)n * n));
+  HIPCK(trinv_diag(st, n, a, y, status));
+  if (n > NB) {
+    CK(ensure(ctx, ctx->tbuf, (size_t)NB * n * sizeof(double)));
+    CK(ensure(ctx, ctx->tpart, gemm_partials_elems(NB, n, n) * sizeof(double)));
+  }
+  for (int s = NB; s < n; s += NB) {
+    const int e = std::min(s + NB, n), w = e - s;
+    double* t = P<double>(ctx->tbuf);
+    // t = L[s:e, 0:s] Y[0:s, 0:s]; Y[s:e, 0:s] = -Y_ss t  (src/linalg.rs:307-343)
+    HIPCK(gemm_chain<double>(st, w, s, s, 1.0, 0, a + (long)s * n, n, 1, y, n, 1, t, s, 1, false,
+                             s > 256 ? P<double>(ctx->tpart) : nullptr));
+    HIPCK(gemm_chain<double>(st, w, s, w, -1.0, 0, y + (long)s * n + s, n, 1, t, s, 1, y + (long)s * n, n, 1, false,
+                             (double*)nullptr));
+  }
+  HIPCK(scatter_u(st, n, y, u));
+  return CDCLQ_OK;
+}
+
+// The G = E H[:, c0:c0+wd] GEMM of phase 2 (src/engine.rs:548, :608).
+int grad_gemm(cdclq_ctx* ctx, int rows, int n, int c0, int wd, const float* e, const float* h32) {
+  return gemm_chain<float>(ctx->st, rows, wd, n, 1.0f, 0, e, n, 1, h32 + c0, n, 1, P<float>(ctx->G), wd, 1, false,
+                           P<float>(ctx->part)) == hipSuccess
+             ? CDCLQ_OK
+             : fail(ctx, CDCLQ_DEVICE, "gradient GEMM launch failed");
+}
+
+int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, const float* h, const float* m,
+                    const char* hkey, const cdclq_config* cfg, size_t nthreads, uint8_t* codes, float* scales,
+                    float* zeros, uint32_t* perm_out, uint8_t* gbits_out, cdclq_layer_stats* stats) {
+  if (!cfg) return fail(ctx, CDCLQ_INVALID_ARG, "cfg is null");
+  if (!w || !h || !codes || !scales || !zeros || !perm_out || !gbits_out)
+    return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+  if (d_out_ == 0 || n_ == 0) return fail(ctx, CDCLQ_INVALID_ARG, "empty layer (d_out and d_in must be > 0)");
+  if (n_ > 65536 || d_out_ > (size_t)1 << 20 || d_out_ * n_ > ((size_t)1 << 31) - 1)
+    return fail(ctx, CDCLQ_INVALID_ARG, "layer too large for this build (d_in <= 65536, d_out*d_in < 2^31)");
+  CK(validate(ctx, cfg, n_));
+  const int d_out = (int)d_out_, n = (int)n_;
+  const int g = (int)effective_group(cfg, n_);
+  const int ng = (n + g - 1) / g;
+  const int bsz = (int)std::min<uint64_t>(cfg->block, (uint64_t)n);
+  const int sbw = (int)std::min<uint64_t>(cfg->sub_block, (uint64_t)n);
+  if (std::min<uint64_t>(cfg->block, n_) > 1024)
+    return fail(ctx, CDCLQ_INVALID_ARG, "block > 1024 columns is not supported by the GPU block sweep");
+  if (cfg->method == CDCLQ_METHOD_CDCL && std::min<uint64_t>(cfg->sub_block, n_) > 1024)
+    return fail(ctx, CDCLQ_INVALID_ARG, "sub_block > 1024 columns is not supported by the GPU repair sweep");
+  hipStream_t st = ctx->st;
+  HIPCK(hipSetDevice(ctx->device));
+  const double t0 = now_secs();
+
+  // ---- dead columns and column order (src/engine.rs:708-717, :271-304)
+  CK(ensure(ctx, ctx->diag_d, (size_t)n * 4));
+  HIPCK(diag_extract(st, n, h, P<float>(ctx->diag_d)));
+  std::vector<float> hd32(n);
+  HIPCK(hipMemcpyAsync(hd32.data(), ctx->diag_d.p, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+  HIPCK(hipStreamSynchronize(st));
+  std::vector<double> hdiag(n);
+  std::vector<uint8_t> dead(n);
+  for (int j = 0; j < n; ++j) {
+    hdiag[j] = (double)hd32[j];
+    dead[j] = hdiag[j] == 0.0;
+  }
+  size_t nskel = 0;
+  std::vector<uint32_t> perm;
+  perm.reserve(n);
+  std::vector<uint8_t> in_skel(n, 0);
+  if (cfg->skeleton_pct > 0.0 && g < n) {
+    const size_t full_groups = (size_t)n / g;
+    const double v = std::round(cfg->skeleton_pct / 100.0 * (double)n / (double)g);
+    const size_t want = v > 0.0 ? (size_t)v : 0;
+    const size_t capg = full_groups > 0 ? full_groups - 1 : 0;
+    nskel = std::min(want, capg);
+    if (nskel > 0) {
+      CK(ensure(ctx, ctx->dead_d, (size_t)n));
+      CK(ensure(ctx, ctx->colsq_d, (size_t)n * 8));
+      HIPCK(hipMemcpyAsync(ctx->dead_d.p, dead.data(), n, hipMemcpyHostToDevice, st));
+      HIPCK(colsq(st, d_out, n, w, P<uint8_t>(ctx->dead_d), P<double>(ctx->colsq_d)));
+      std::vector<double> cs(n);
+      HIPCK(hipMemcpyAsync(cs.data(), ctx->colsq_d.p, (size_t)n * 8, hipMemcpyDeviceToHost, st));
+      HIPCK(hipStreamSynchronize(st));
+      std::vector<double> sal(n);
+      for (int j = 0; j < n; ++j) sal[j] = hdiag[j] * cs[j];
+      std::vector<size_t> idx(n);
+      for (int j = 0; j < n; ++j) idx[j] = j;
+      sort_desc_index(idx, sal);
+      for (size_t t = 0; t < nskel * g; ++t) {
+        in_skel[idx[t]] = 1;
+        perm.push_back((uint32_t)idx[t]);
+      }
+    }
+  }
+  {
+    std::vector<size_t> rest;
+    rest.reserve(n);
+    for (int j = 0; j < n; ++j)
+      if (!in_skel[j]) rest.push_back(j);
+    if (cfg->act_order) sort_desc_index(rest, hdiag);
+    for (size_t j : rest) perm.push_back((uint32_t)j);
+  }
+
+  // ---- factor cache (src/engine.rs:718-723) and build_prepared (:320-342)
+  const std::string key = hkey ? hkey : "";
+  const bool reuse = ctx->cache_valid && ctx->cache_key == key && ctx->cache_n == n_ && ctx->cache_perm == perm;
+  CK(ensure(ctx, ctx->perm_d, (size_t)n * 4));
+  HIPCK(hipMemcpyAsync(ctx->perm_d.p, perm.data(), (size_t)n * 4, hipMemcpyHostToDevice, st));
+  if (!reuse) {
+    ctx->cache_valid = false;
+    double mean_diag = 0.0;
+    for (int i = 0; i < n; ++i) {
+      double v = hdiag[perm[i]];
+      if (v == 0.0) v = 1.0;
+      mean_diag += v;
+    }
+    mean_diag /= (double)n;
+    const double damp_val = cfg->damp * mean_diag;
+    CK(ensure(ctx, ctx->cache_h32, (size_t)n * n * 4));
+    CK(ensure(ctx, ctx->cache_u, (size_t)n * n * 4));
+    CK(ensure(ctx, ctx->a64, (size_t)n * n * 8));
+    CK(ensure(ctx, ctx->y64, (size_t)n * n * 8));
+    {
+      PhaseScope ps(ctx, CDCLQ_PHASE_FACTOR);
+      HIPCK(build_flipped(st, n, h, P<uint32_t>(ctx->perm_d), damp_val, P<double>(ctx->a64), P<float>(ctx->cache_h32)));
+      CK(factor(ctx, n, P<double>(ctx->a64), P<double>(ctx->y64), P<float>(ctx->cache_u)));
+    }
+    ctx->cache_valid = true;
+    ctx->cache_key = key;
+    ctx->cache_perm = perm;
+    ctx->cache_n = n_;
+    ctx->cache_damp = damp_val;
+  }
+  const float* U = P<float>(ctx->cache_u);
+  const float* H32 = P<float>(ctx->cache_h32);
+
+  // ---- permuted (and optionally target-adjusted) weights (src/engine.rs:726-755)
+  std::vector<uint8_t> dead_perm(n);
+  for (int j = 0; j < n; ++j) dead_perm[j] = dead[perm[j]];
+  CK(ensure(ctx, ctx->deadp_d, (size_t)n));
+  HIPCK(hipMemcpyAsync(ctx->deadp_d.p, dead_perm.data(), n, hipMemcpyHostToDevice, st));
+  const size_t wn = (size_t)d_out * n;
+  CK(ensure(ctx, ctx->wp, wn * 4));
+  float* wp = P<float>(ctx->wp);
+  HIPCK(permute_w(st, d_out, n, w, P<uint32_t>(ctx->perm_d), P<uint8_t>(ctx->deadp_d), wp));
+  if (m) {
+    PhaseScope ps(ctx, CDCLQ_PHASE_TARGET);
+    CK(ensure(ctx, ctx->mp, (size_t)n * n * 4));
+    CK(ensure(ctx, ctx->t1, wn * 4));
+    CK(ensure(ctx, ctx->t2, wn * 4));
+    float* mp = P<float>(ctx->mp);
+    HIPCK(permute_m(st, n, m, P<uint32_t>(ctx->perm_d), (float)ctx->cache_damp, mp));
+    HIPCK(gemm_chain<float>(st, d_out, n, n, 1.0f, 0, wp, n, 1, mp, n, 1, P<float>(ctx->t1), n, 1, false, nullptr));
+    HIPCK(gemm_chain<float>(st, d_out, n, n, 1.0f, 0, P<float>(ctx->t1), n, 1, U, 1, n, P<float>(ctx->t2), n, 1, false,
+                            nullptr));
+    HIPCK(gemm_chain<float>(st, d_out, n, n, 1.0f, 0, P<float>(ctx->t2), n, 1, U, n, 1, wp, n, 1, false, nullptr));
+  }
+  HIPCK(hipStreamSynchronize(st));
+  const double secs_prepare = now_secs() - t0;
+
+  // ---- per-group widths and row chunks (src/engine.rs:760, :768-770)
+  std::vector<uint8_t> gbits(ng);
+  for (int gi = 0; gi < ng; ++gi) gbits[gi] = (uint8_t)((size_t)gi < nskel ? cfg->skeleton_bits : cfg->bits);
+  CK(ensure(ctx, ctx->gbits_d, (size_t)ng));
+  HIPCK(hipMemcpyAsync(ctx->gbits_d.p, gbits.data(), ng, hipMemcpyHostToDevice, st));
+  const size_t nt = nthreads ? nthreads : 1;
+  size_t rcz;
+  if (cfg->row_chunk > 0) {
+    rcz = cfg->row_chunk;
+  } else {
+    rcz = (d_out_ + nt - 1) / nt;
+    rcz = std::min<size_t>(std::max<size_t>(rcz, 32), 256);
+  }
+  rcz = std::max<size_t>(std::min(rcz, d_out_), 1);
+  const int rc = (int)rcz;
+  const int nchunks = (d_out + rc - 1) / rc;
+
+  const double t1 = now_secs();
+  // ---- phase 1: blocked GPTQ with lazy updates (src/engine.rs:397-479)
+  CK(ensure(ctx, ctx->wwork, wn * 4));
+  CK(ensure(ctx, ctx->wq, wn * 4));
+  CK(ensure(ctx, ctx->ebuf, wn * 4));
+  CK(ensure(ctx, ctx->invd, (size_t)n * 4));
+  CK(ensure(ctx, ctx->colloss_d, (size_t)nchunks * n * 8));
+  float* wwork = P<float>(ctx->wwork);
+  float* wq = P<float>(ctx->wq);
+  float* eb = P<float>(ctx->ebuf);
+  std::vector<double> loss_gptq(nchunks, 0.0);
+  std::vector<double> colloss((size_t)nchunks * n);
+  {
+    PhaseScope ps(ctx, CDCLQ_PHASE_GPTQ);
+    HIPCK(hipMemcpyAsync(wwork, wp, wn * 4, hipMemcpyDeviceToDevice, st));
+    HIPCK(inv_diag(st, n, U, P<float>(ctx->invd)));
+    for (int i1 = 0; i1 < n; i1 += bsz) {
+      const int i2 = std::min(i1 + bsz, n), cnt = i2 - i1;
+      HIPCK(gptq_block(st, d_out, n, i1, cnt, g, ng, wwork, U, P<float>(ctx->invd), P<uint8_t>(ctx->gbits_d),
+                       cfg->mse_grid, scales, zeros, codes, wq, eb));
+      if (i2 < n)
+        HIPCK(gemm_chain<float>(st, d_out, n - i2, cnt, -1.0f, 1, eb + i1, n, 1, U + (long)i1 * n + i2, n, 1,
+                                wwork + i2, n, 1, false, nullptr));
+    }
+    HIPCK(cdclq::colloss(st, d_out, n, rc, eb, P<double>(ctx->colloss_d)));
+  }
+  HIPCK(hipMemcpyAsync(colloss.data(), ctx->colloss_d.p, colloss.size() * 8, hipMemcpyDeviceToHost, st));
+  HIPCK(hipStreamSynchronize(st));
+  for (int c = 0; c < nchunks; ++c) {
+    double s = 0.0;
+    for (int j = 0; j < n; ++j) s += colloss[(size_t)c * n + j];
+    loss_gptq[c] = s;
+  }
+
+  // ---- phase 2: conflict selection + repair (src/engine.rs:488-671)
+  const int n_sb = (n + sbw - 1) / sbw;
+  std::vector<double> ld(nchunks, 0.0);
+  std::vector<uint64_t> updates(nchunks, 0), refined(nchunks, 0);
+  const bool do_cd = cfg->refine_frac > 0.0 && cfg->cd_sweeps > 0 && cfg->passes > 0;
+  const bool do_refit = cfg->refit_scales && g <= 1024;
+  if (cfg->method == CDCLQ_METHOD_CDCL && (do_cd || do_refit)) {
+    PhaseScope ps(ctx, CDCLQ_PHASE_REPAIR);
+    std::vector<uint8_t> sel((size_t)nchunks * n_sb, 0);
+    if (do_cd) {
+      const double kf = std::ceil(cfg->refine_frac * (double)n_sb);
+      size_t kk = kf > 0.0 ? (size_t)kf : 0;
+      kk = std::min<size_t>(std::max<size_t>(kk, 1), n_sb);
+      std::vector<double> sums(n_sb);
+      std::vector<size_t> order(n_sb);
+      for (int c = 0; c < nchunks; ++c) {
+        for (int s = 0; s < n_sb; ++s) {
+          const int c0 = s * sbw, c1 = std::min((s + 1) * sbw, n);
+          double acc = 0.0;
+          for (int j = c0; j < c1; ++j) acc += colloss[(size_t)c * n + j];
+          sums[s] = acc;
+          order[s] = s;
+        }
+        sort_desc_index(order, sums);
+        for (size_t t = 0; t < kk; ++t) sel[(size_t)c * n_sb + order[t]] = 1;
+        refined[c] = kk;
+      }
+    }
+    CK(ensure(ctx, ctx->sel_d, sel.size()));
+    HIPCK(hipMemcpyAsync(ctx->sel_d.p, sel.data(), sel.size(), hipMemcpyHostToDevice, st));
+    HIPCK(sub_f32(st, wn, wp, wq, eb));  // e = W - W_hat (src/engine.rs:516-519)
+    const int wdmax = std::max(do_cd ? sbw : 1, do_refit ? g : 1);
+    CK(ensure(ctx, ctx->G, (size_t)d_out * wdmax * 4));
+    CK(ensure(ctx, ctx->part, gemm_partials_elems(d_out, wdmax, n) * 4));
+    const int cap = std::max(1, do_cd ? sbw * (int)cfg->cd_sweeps : 1);
+    CK(ensure(ctx, ctx->dlog, (size_t)d_out * cap * 8));
+    CK(ensure(ctx, ctx->dcnt, (size_t)d_out * 4));
+    CK(ensure(ctx, ctx->active_d, (size_t)nchunks));
+    CK(ensure(ctx, ctx->ld_d, (size_t)nchunks * 8));
+    CK(ensure(ctx, ctx->upd_d, (size_t)nchunks * 8));
+    HIPCK(hipMemsetAsync(ctx->ld_d.p, 0, (size_t)nchunks * 8, st));
+    std::vector<uint8_t> act(nchunks, 1);
+    HIPCK(hipMemcpyAsync(ctx->active_d.p, act.data(), nchunks, hipMemcpyHostToDevice, st));
+    std::vector<double> prev(nchunks, 0.0);
+    std::vector<uint64_t> upd(nchunks);
+    auto refit_all = [&]() -> int {
+      for (int gi = 0; gi < ng; ++gi) {
+        const int c0 = gi * g, wd = std::min(c0 + g, n) - c0;
+        CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32));
+        HIPCK(refit_group(st, d_out, n, ng, g, gi, rc, P<float>(ctx->G), H32, codes, scales, zeros, wq, eb,
+                          P<uint8_t>(ctx->active_d), P<double>(ctx->dlog), P<uint32_t>(ctx->dcnt), cap));
+        HIPCK(chunk_accum(st, d_out, rc, nchunks, cap, P<double>(ctx->dlog), P<uint32_t>(ctx->dcnt),
+                          P<uint8_t>(ctx->active_d), P<double>(ctx->ld_d), P<uint64_t>(ctx->upd_d)));
+      }
+      return CDCLQ_OK;
+    };
+    const uint64_t npass = cfg->passes > 0 ? cfg->passes : 1;
+    for (uint64_t pass = 0; pass < npass; ++pass) {
+      HIPCK(hipMemsetAsync(ctx->upd_d.p, 0, (size_t)nchunks * 8, st));
+      if (do_refit) CK(refit_all());
+      if (do_cd) {
+        for (int s = 0; s < n_sb; ++s) {
+          bool any = false;
+          for (int c = 0; c < nchunks && !any; ++c) any = act[c] && sel[(size_t)c * n_sb + s];
+          if (!any) continue;
+          const int c0 = s * sbw, wd = std::min(c0 + sbw, n) - c0;
+          CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32));
+          HIPCK(cd_subblock(st, d_out, n, ng, g, c0, wd, s, n_sb, rc, (int)cfg->cd_sweeps, P<float>(ctx->G), H32,
+                            P<uint8_t>(ctx->gbits_d), scales, zeros, codes, wq, eb, P<uint8_t>(ctx->active_d),
+                            P<uint8_t>(ctx->sel_d), P<double>(ctx->dlog), P<uint32_t>(ctx->dcnt), cap));
+          HIPCK(chunk_accum(st, d_out, rc, nchunks, cap, P<double>(ctx->dlog), P<uint32_t>(ctx->dcnt),
+                            P<uint8_t>(ctx->active_d), P<double>(ctx->ld_d), P<uint64_t>(ctx->upd_d)));
+        }
+      }
+      HIPCK(hipMemcpyAsync(ld.data(), ctx->ld_d.p, (size_t)nchunks * 8, hipMemcpyDeviceToHost, st));
+      HIPCK(hipMemcpyAsync(upd.data(), ctx->upd_d.p, (size_t)nchunks * 8, hipMemcpyDeviceToHost, st));
+      HIPCK(hipStreamSynchronize(st));
+      bool any_active = false;
+      for (int c = 0; c < nchunks; ++c) {
+        if (!act[c]) continue;
+        updates[c] += upd[c];
+        const double gain = prev[c] - ld[c];
+        prev[c] = ld[c];
+        if (upd[c] == 0 || gain < cfg->tol * (loss_gptq[c] + ld[c]))
+          act[c] = 0;  // converged (src/engine.rs:663-665)
+        else
+          any_active = true;
+      }
+      if (!any_active) break;
+      HIPCK(hipMemcpyAsync(ctx->active_d.p, act.data(), nchunks, hipMemcpyHostToDevice, st));
+    }
+    if (do_refit) {  // final refit (src/engine.rs:668-670)
+      std::fill(act.begin(), act.end(), 1);
+      HIPCK(hipMemcpyAsync(ctx->active_d.p, act.data(), nchunks, hipMemcpyHostToDevice, st));
+      HIPCK(hipMemsetAsync(ctx->upd_d.p, 0, (size_t)nchunks * 8, st));
+      CK(refit_all());
+      HIPCK(hipMemcpyAsync(ld.data(), ctx->ld_d.p, (size_t)nchunks * 8, hipMemcpyDeviceToHost, st));
+      HIPCK(hipMemcpyAsync(upd.data(), ctx->upd_d.p, (size_t)nchunks * 8, hipMemcpyDeviceToHost, st));
+      HIPCK(hipStreamSynchronize(st));
+      for (int c = 0; c < nchunks; ++c) updates[c] += upd[c];
+    }
+  }
+  HIPCK(hipStreamSynchronize(st));
+  const double secs_quant = now_secs() - t1;
+
+  std::memcpy(perm_out, perm.data(), (size_t)n * 4);
+  std::memcpy(gbits_out, gbits.data(), (size_t)ng);
+  if (stats) {
+    cdclq_layer_stats s{};
+    for (int c = 0; c < nchunks; ++c) {
+      s.loss_gptq += loss_gptq[c];
+      s.loss_final += loss_gptq[c] + ld[c];
+      s.subblocks_total += (uint64_t)n_sb;
+      s.subblocks_refined += refined[c];
+      s.code_updates += updates[c];
+    }
+    s.skeleton_groups = nskel;
+    size_t row_bits = 0;
+    for (int j = 0; j < n; ++j) row_bits += gbits[j / g];
+    s.bits_codes = (double)row_bits / (double)n;
+    s.bits_total = s.bits_codes + 24.0 / (double)g;
+    s.secs_prepare = secs_prepare;
+    s.secs_quant = secs_quant;
+    *stats = s;
+  }
+  return CDCLQ_OK;
+}
+
+int gram_device(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h) {
+  if (!x || !y || !h) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+  if (n == 0 || t == 0) return CDCLQ_OK;
+  if (n > 65536 || t > ((size_t)1 << 31) - 4096)
+    return fail(ctx, CDCLQ_INVALID_ARG, "gram_accumulate: n <= 65536 and t < 2^31 in this build");
+  HIPCK(hipSetDevice(ctx->device));
+  const bool sym = (x == y);
+  if (ctx->tiles_n != (int)n || ctx->tiles_sym != (int)sym) {
+    std::vector<int2> v = gram_tiles((int)n, sym);
+    CK(ensure(ctx, ctx->tiles_d, v.size() * sizeof(int2)));
+    HIPCK(hipMemcpy(ctx->tiles_d.p, v.data(), v.size() * sizeof(int2), hipMemcpyHostToDevice));
+    ctx->tiles_n = (int)n;
+    ctx->tiles_sym = (int)sym;
+    ctx->tiles_count = (int)v.size();
+  }
+  {
+    PhaseScope ps(ctx, CDCLQ_PHASE_GRAM);
+    HIPCK(gram_accumulate(ctx->st, (int)t, (int)n, x, y, h, sym, P<int2>(ctx->tiles_d), ctx->tiles_count));
+  }
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
+int uchol_device(cdclq_ctx* ctx, const double* h, size_t n_, float* u) {
+  if (!h || !u) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+  if (n_ == 0) return CDCLQ_OK;
+  if (n_ > 65536) return fail(ctx, CDCLQ_INVALID_ARG, "n > 65536 is not supported in this build");
+  HIPCK(hipSetDevice(ctx->device));
+  const int n = (int)n_;
+  CK(ensure(ctx, ctx->a64, (size_t)n * n * 8));
+  CK(ensure(ctx, ctx->y64, (size_t)n * n * 8));
+  {
+    PhaseScope ps(ctx, CDCLQ_PHASE_FACTOR);
+    HIPCK(build_flipped_f64(ctx->st, n, h, P<double>(ctx->a64)));
+    CK(factor(ctx, n, P<double>(ctx->a64), P<double>(ctx->y64), u));
+  }
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+extern "C" {
+
+int cdclq_abi_version(void) { return CDCLQ_ABI_VERSION; }
+size_t cdclq_sizeof_config(void) { return sizeof(cdclq_config); }
+size_t cdclq_sizeof_stats(void) { return sizeof(cdclq_layer_stats); }
+
+void cdclq_default_config(cdclq_config* c) {
+  if (!c) return;
+  std::memset(c, 0, sizeof(*c));
+  c->bits = 3;
+  c->group = 128;
+  c->block = 128;
+  c->damp = 0.01;
+  c->act_order = 1;
+  c->skeleton_pct = 0.0;
+  c->skeleton_bits = 8;
+  c->mse_grid = 0;
+  c->method = CDCLQ_METHOD_CDCL;
+  c->refine_frac = 1.0;
+  c->sub_block = 64;
+  c->cd_sweeps = 1;
+  c->passes = 10;
+  c->tol = 1e-3;
+  c->refit_scales = 1;
+  c->row_chunk = 0;
+}
+
+size_t cdclq_num_groups(const cdclq_config* cfg, size_t d_in) {
+  if (!cfg || d_in == 0) return 0;
+  const size_t g = effective_group(cfg, d_in);
+  return (d_in + g - 1) / g;
+}
+
+int cdclq_ctx_create(int device, cdclq_ctx** out) {
+  if (!out) return CDCLQ_INVALID_ARG;
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return CDCLQ_DEVICE;
+  if (hipSetDevice(device) != hipSuccess) return CDCLQ_DEVICE;
+  cdclq_ctx* ctx = new (std::nothrow) cdclq_ctx();
+  if (!ctx) return CDCLQ_OOM;
+  ctx->device = device;
+  if (hipStreamCreateWithFlags(&ctx->st, hipStreamNonBlocking) != hipSuccess) {
+    delete ctx;
+    return CDCLQ_DEVICE;
+  }
+  *out = ctx;
+  return CDCLQ_OK;
+}
+
+void cdclq_ctx_destroy(cdclq_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->st);
+  drain_timing(ctx);
+  DevBuf* bufs[] = {&ctx->w_in, &ctx->h_in, &ctx->m_in, &ctx->x_in, &ctx->y_in, &ctx->h64_in, &ctx->u_out,
+                    &ctx->codes_o, &ctx->scales_o, &ctx->zeros_o, &ctx->wp, &ctx->wwork, &ctx->wq, &ctx->ebuf,
+                    &ctx->gbits_d, &ctx->perm_d, &ctx->deadp_d, &ctx->dead_d, &ctx->diag_d, &ctx->colsq_d,
+                    &ctx->invd, &ctx->colloss_d, &ctx->G, &ctx->part, &ctx->dlog, &ctx->dcnt, &ctx->active_d,
+                    &ctx->sel_d, &ctx->ld_d, &ctx->upd_d, &ctx->mp, &ctx->t1, &ctx->t2, &ctx->a64, &ctx->y64,
+                    &ctx->tbuf, &ctx->tpart, &ctx->status_d, &ctx->tiles_d, &ctx->proxy_p, &ctx->cs_d,
+                    &ctx->cache_u, &ctx->cache_h32};
+  for (DevBuf* b : bufs) free_buf(*b);
+  (void)hipStreamDestroy(ctx->st);
+  delete ctx;
+}
+
+const char* cdclq_last_error(const cdclq_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+int cdclq_ctx_clear_cache(cdclq_ctx* ctx) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->cache_valid = false;
+  ctx->cache_key.clear();
+  ctx->cache_perm.clear();
+  return CDCLQ_OK;
+}
+
+int cdclq_quantize_layer_device(cdclq_ctx* ctx, const float* w, size_t d_out, size_t d_in, const float* h,
+                                const float* m, const char* hkey, const cdclq_config* cfg, size_t nthreads,
+                                uint8_t* codes, float* scales, float* zeros, uint32_t* perm, uint8_t* gbits,
+                                cdclq_layer_stats* stats) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  return quantize_device(ctx, w, d_out, d_in, h, m, hkey, cfg, nthreads, codes, scales, zeros, perm, gbits, stats);
+}
+
+int cdclq_quantize_layer(cdclq_ctx* ctx, const float* w, size_t d_out, size_t d_in, const float* h, const float* m,
+                         const char* hkey, const cdclq_config* cfg, size_t nthreads, uint8_t* codes, float* scales,
+                         float* zeros, uint32_t* perm, uint8_t* gbits, cdclq_layer_stats* stats) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  if (!cfg) return fail(ctx, CDCLQ_INVALID_ARG, "cfg is null");
+  if (!w || !h || !codes || !scales || !zeros || !perm || !gbits)
+    return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+  if (d_out == 0 || d_in == 0) return fail(ctx, CDCLQ_INVALID_ARG, "empty layer (d_out and d_in must be > 0)");
+  CK(validate(ctx, cfg, d_in));
+  HIPCK(hipSetDevice(ctx->device));
+  const size_t ng = cdclq_num_groups(cfg, d_in);
+  const size_t wn = d_out * d_in, hn = d_in * d_in;
+  CK(ensure(ctx, ctx->w_in, wn * 4));
+  CK(ensure(ctx, ctx->h_in, hn * 4));
+  CK(ensure(ctx, ctx->codes_o, wn));
+  CK(ensure(ctx, ctx->scales_o, d_out * ng * 4));
+  CK(ensure(ctx, ctx->zeros_o, d_out * ng * 4));
+  HIPCK(hipMemcpyAsync(ctx->w_in.p, w, wn * 4, hipMemcpyHostToDevice, ctx->st));
+  HIPCK(hipMemcpyAsync(ctx->h_in.p, h, hn * 4, hipMemcpyHostToDevice, ctx->st));
+  if (m) {
+    CK(ensure(ctx, ctx->m_in, hn * 4));
+    HIPCK(hipMemcpyAsync(ctx->m_in.p, m, hn * 4, hipMemcpyHostToDevice, ctx->st));
+  }
+  CK(quantize_device(ctx, P<float>(ctx->w_in), d_out, d_in, P<float>(ctx->h_in), m ? P<float>(ctx->m_in) : nullptr,
+                     hkey, cfg, nthreads, P<uint8_t>(ctx->codes_o), P<float>(ctx->scales_o), P<float>(ctx->zeros_o),
+                     perm, gbits, stats));
+  HIPCK(hipMemcpyAsync(codes, ctx->codes_o.p, wn, hipMemcpyDeviceToHost, ctx->st));
+  HIPCK(hipMemcpyAsync(scales, ctx->scales_o.p, d_out * ng * 4, hipMemcpyDeviceToHost, ctx->st));
+  HIPCK(hipMemcpyAsync(zeros, ctx->zeros_o.p, d_out * ng * 4, hipMemcpyDeviceToHost, ctx->st));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
+int cdclq_gram_accumulate_device(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  return gram_device(ctx, x, y, t, n, h);
+}
+
+int cdclq_gram_accumulate(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  if (!x || !y || !h) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+  if (n == 0 || t == 0) return CDCLQ_OK;
+  HIPCK(hipSetDevice(ctx->device));
+  const bool sym = (x == y);
+  CK(ensure(ctx, ctx->x_in, t * n * 4));
+  CK(ensure(ctx, ctx->h64_in, n * n * 8));
+  HIPCK(hipMemcpyAsync(ctx->x_in.p, x, t * n * 4, hipMemcpyHostToDevice, ctx->st));
+  if (!sym) {
+    CK(ensure(ctx, ctx->y_in, t * n * 4));
+    HIPCK(hipMemcpyAsync(ctx->y_in.p, y, t * n * 4, hipMemcpyHostToDevice, ctx->st));
+  }
+  HIPCK(hipMemcpyAsync(ctx->h64_in.p, h, n * n * 8, hipMemcpyHostToDevice, ctx->st));
+  CK(gram_device(ctx, P<float>(ctx->x_in), sym ? P<float>(ctx->x_in) : P<float>(ctx->y_in), t, n,
+                 P<double>(ctx->h64_in)));
+  HIPCK(hipMemcpyAsync(h, ctx->h64_in.p, n * n * 8, hipMemcpyDeviceToHost, ctx->st));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
+int cdclq_upper_chol_of_inverse_device(cdclq_ctx* ctx, const double* h, size_t n, float* u) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  return uchol_device(ctx, h, n, u);
+}
+
+int cdclq_upper_chol_of_inverse(cdclq_ctx* ctx, const double* h, size_t n, float* u) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  if (!h || !u) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+  if (n == 0) return CDCLQ_OK;
+  HIPCK(hipSetDevice(ctx->device));
+  CK(ensure(ctx, ctx->h64_in, n * n * 8));
+  CK(ensure(ctx, ctx->u_out, n * n * 4));
+  HIPCK(hipMemcpyAsync(ctx->h64_in.p, h, n * n * 8, hipMemcpyHostToDevice, ctx->st));
+  CK(uchol_device(ctx, P<double>(ctx->h64_in), n, P<float>(ctx->u_out)));
+  HIPCK(hipMemcpyAsync(u, ctx->u_out.p, n * n * 4, hipMemcpyDeviceToHost, ctx->st));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
+int cdclq_proxy_loss(cdclq_ctx* ctx, const float* w_t, const float* w_hat, size_t rows, size_t n, const float* h,
+                     double* out) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  if (!w_t || !w_hat || !h || !out) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+  *out = 0.0;
+  if (rows == 0 || n == 0) return CDCLQ_OK;
+  HIPCK(hipSetDevice(ctx->device));
+  const size_t wn = rows * n;
+  CK(ensure(ctx, ctx->w_in, wn * 4));
+  CK(ensure(ctx, ctx->t1, wn * 4));
+  CK(ensure(ctx, ctx->t2, wn * 4));
+  CK(ensure(ctx, ctx->h_in, n * n * 4));
+  HIPCK(hipMemcpyAsync(ctx->w_in.p, w_t, wn * 4, hipMemcpyHostToDevice, ctx->st));
+  HIPCK(hipMemcpyAsync(ctx->t2.p, w_hat, wn * 4, hipMemcpyHostToDevice, ctx->st));
+  HIPCK(hipMemcpyAsync(ctx->h_in.p, h, n * n * 4, hipMemcpyHostToDevice, ctx->st));
+  HIPCK(sub_f32(ctx->st, wn, P<float>(ctx->w_in), P<float>(ctx->t2), P<float>(ctx->t1)));  // e
+  HIPCK(gemm_chain<float>(ctx->st, (int)rows, (int)n, (int)n, 1.0f, 0, P<float>(ctx->t1), (long)n, 1,
+                          P<float>(ctx->h_in), (long)n, 1, P<float>(ctx->t2), (long)n, 1, false, nullptr));
+  const int nb = 1024;
+  CK(ensure(ctx, ctx->proxy_p, nb * 8));
+  HIPCK(proxy_reduce(ctx->st, wn, P<float>(ctx->t1), P<float>(ctx->t2), P<double>(ctx->proxy_p), nb));
+  std::vector<double> part(nb);
+  HIPCK(hipMemcpyAsync(part.data(), ctx->proxy_p.p, nb * 8, hipMemcpyDeviceToHost, ctx->st));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  double s = 0.0;
+  for (double v : part) s += v;
+  *out = s;
+  return CDCLQ_OK;
+}
+
+int cdclq_device_alloc(cdclq_ctx* ctx, size_t bytes, void** ptr) {
+  if (!ctx || !ptr) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  HIPCK(hipSetDevice(ctx->device));
+  *ptr = nullptr;
+  hipError_t e = hipMalloc(ptr, bytes ? bytes : 256);
+  if (e != hipSuccess) {
+    *ptr = nullptr;
+    (void)hipGetLastError();
+    return fail(ctx, CDCLQ_OOM, "device allocation of " + std::to_string(bytes) + " bytes failed");
+  }
+  return CDCLQ_OK;
+}
+
+int cdclq_device_free(cdclq_ctx* ctx, void* ptr) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  if (!ptr) return CDCLQ_OK;
+  HIPCK(hipSetDevice(ctx->device));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  HIPCK(hipFree(ptr));
+  return CDCLQ_OK;
+}
+
+int cdclq_memcpy_h2d(cdclq_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  HIPCK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->st));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
+int cdclq_memcpy_d2h(cdclq_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  HIPCK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->st));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
+int cdclq_memset_device(cdclq_ctx* ctx, void* dst, int value, size_t bytes) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  HIPCK(hipMemsetAsync(dst, value, bytes, ctx->st));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
+int cdclq_synth_normal_device(cdclq_ctx* ctx, uint64_t seed, uint64_t offset, size_t count, float sigma, float* out) {
+  if (!ctx || (!out && count)) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  HIPCK(synth_normal(ctx->st, seed, offset, count, sigma, out));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
+int cdclq_synth_outlier_scales(uint64_t seed, size_t n, double frac, float factor, float* scales) {
+  if (!scales && n) return CDCLQ_INVALID_ARG;
+  size_t k = (size_t)std::round(frac * (double)n);
+  if (k > n) k = n;
+  std::vector<size_t> idx(n);
+  for (size_t j = 0; j < n; ++j) {
+    idx[j] = j;
+    scales[j] = 1.0f;
+  }
+  for (size_t i = 0; i < k; ++i) {
+    const size_t j = i + (size_t)(mix64(seed + (i + 1) * 0x9E3779B97F4A7C15ULL) % (uint64_t)(n - i));
+    std::swap(idx[i], idx[j]);
+  }
+  for (size_t i = 0; i < k; ++i) scales[idx[i]] = factor;
+  return CDCLQ_OK;
+}
+
+int cdclq_synth_tokens_device(cdclq_ctx* ctx, uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale,
+                              float* x) {
+  if (!ctx || (!x && t && n)) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  const float* cs = nullptr;
+  if (ch_scale) {
+    CK(ensure(ctx, ctx->cs_d, n * 4));
+    HIPCK(hipMemcpyAsync(ctx->cs_d.p, ch_scale, n * 4, hipMemcpyHostToDevice, ctx->st));
+    cs = P<float>(ctx->cs_d);
+  }
+  HIPCK(synth_tokens(ctx->st, seed, row0, t, n, cs, x));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
+int cdclq_f64_to_f32_device(cdclq_ctx* ctx, const double* h64, size_t count, float* h32) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  HIPCK(f64_to_f32(ctx->st, count, h64, h32));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
+int cdclq_ctx_set_timing(cdclq_ctx* ctx, int enable) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->timing = enable != 0;
+  return CDCLQ_OK;
+}
+
+int cdclq_ctx_reset_timing(cdclq_ctx* ctx) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  drain_timing(ctx);
+  for (int i = 0; i < CDCLQ_PHASE_COUNT; ++i) {
+    ctx->ms[i] = 0.0;
+    ctx->launches[i] = 0;
+  }
+  return CDCLQ_OK;
+}
+
+int cdclq_ctx_get_timing(cdclq_ctx* ctx, int phase, uint64_t* launches, double* ms) {
+  if (!ctx || phase < 0 || phase >= CDCLQ_PHASE_COUNT) return CDCLQ_INVALID_ARG;
+  drain_timing(ctx);
+  if (launches) *launches = ctx->launches[phase];
+  if (ms) *ms = ctx->ms[phase];
+  return CDCLQ_OK;
+}
+
+}  // extern "C"

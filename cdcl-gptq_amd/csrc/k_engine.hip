@@ -1,0 +1,605 @@
+// Per-row sweep kernels of the quantization engine (src/engine.rs:366-674) and small helpers.
+//
+// Rows are independent in both phases (src/engine.rs:9-15), so every sweep kernel gives one
+// 64-lane wavefront to one row: the row's columns of the current block / group / sub-block live in
+// VGPRs spread over the lanes, the column loop runs in wave-uniform control flow, the value of the
+// current column is broadcast with v_readlane, and updates of the not-yet-visited columns are
+// lane-parallel. Each element therefore sees exactly the reference's sequence of roundings.
+#include <algorithm>
+
+#include "cdclq_dev.h"
+#include "kernels.h"
+
+namespace cdclq {
+namespace {
+
+inline unsigned nblk(long count) { return (unsigned)((count + 255) / 256); }
+
+__device__ __forceinline__ int readlane_i(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+
+// ---------------------------------------------------------------- preparation helpers
+__global__ __launch_bounds__(256) void k_diag_extract(int n, const float* __restrict__ h, float* __restrict__ d) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j < n) d[j] = h[(long)j * n + j];
+}
+
+// wp[r][j] = w0[r][perm[j]], where w0 has dead columns zeroed (src/engine.rs:708-716, :726-731).
+__global__ __launch_bounds__(256) void k_permute_w(int d_out, int n, const float* __restrict__ w,
+                                                   const uint32_t* __restrict__ perm,
+                                                   const uint8_t* __restrict__ dead_perm, float* __restrict__ wp) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)d_out * n) return;
+  const int r = (int)(idx / n), j = (int)(idx % n);
+  wp[idx] = dead_perm[j] ? 0.0f : w[(long)r * n + perm[j]];
+}
+
+// mp = perm(M) with the f32 ridge on the diagonal (src/engine.rs:739-746).
+__global__ __launch_bounds__(256) void k_permute_m(int n, const float* __restrict__ m,
+                                                   const uint32_t* __restrict__ perm, float damp32,
+                                                   float* __restrict__ mp) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)n * n) return;
+  const int i = (int)(idx / n), j = (int)(idx % n);
+  float v = m[(long)perm[i] * n + perm[j]];
+  if (i == j) v += damp32;
+  mp[idx] = v;
+}
+
+// colsq[j] = sum_r (f64 w0_rj)^2 in row order (src/engine.rs:279-285).
+__global__ __launch_bounds__(256) void k_colsq(int d_out, int n, const float* __restrict__ w,
+                                               const uint8_t* __restrict__ dead, double* __restrict__ out) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= n) return;
+  double s = 0.0;
+  if (!dead[j])
+    for (int r = 0; r < d_out; ++r) {
+      const double v = (double)w[(long)r * n + j];
+      s = s + v * v;
+    }
+  out[j] = s;
+}
+
+__global__ __launch_bounds__(256) void k_inv_diag(int n, const float* __restrict__ u, float* __restrict__ invd) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j < n) invd[j] = 1.0f / u[(long)j * n + j];
+}
+
+// ---------------------------------------------------------------- phase 1 (src/engine.rs:397-473)
+// One block [i1, i1+cnt) for all rows; NPL = values per lane (cnt <= 64*NPL).
+template <int NPL>
+__global__ __launch_bounds__(256) void k_gptq_block(int rows, int n, int i1, int cnt, int g, int ng,
+                                                    const float* __restrict__ w, const float* __restrict__ u,
+                                                    const float* __restrict__ invd, const uint8_t* __restrict__ gbits,
+                                                    int mse, float* __restrict__ scales, float* __restrict__ zeros,
+                                                    uint8_t* __restrict__ codes, float* __restrict__ wq,
+                                                    float* __restrict__ err) {
+  const int lane = threadIdx.x & 63;
+  const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (r >= rows) return;
+  const int i2 = i1 + cnt;
+  const float* wr = w + (long)r * n;
+  float x[NPL], mq[NPL], mwq[NPL], me[NPL];
+#pragma unroll
+  for (int s = 0; s < NPL; ++s) {
+    const int c = s * 64 + lane;
+    x[s] = (c < cnt) ? wr[i1 + c] : 0.0f;
+    mq[s] = 0.0f;
+    mwq[s] = 0.0f;
+    me[s] = 0.0f;
+  }
+  // A block that starts inside a group (block < group) continues with the stored grid.
+  float sc = 0.0f, zr = 0.0f, maxq = 0.0f;
+  if (i1 % g != 0) {
+    const int gi = i1 / g;
+    sc = scales[(long)r * ng + gi];
+    zr = zeros[(long)r * ng + gi];
+    maxq = (float)((1u << gbits[gi]) - 1u);
+  }
+#pragma unroll
+  for (int s = 0; s < NPL; ++s) {
+    for (int ii = 0; ii < 64; ++ii) {
+      const int i = s * 64 + ii;
+      if (i >= cnt) break;
+      const int j = i1 + i;
+      if (j % g == 0) {
+        // group grid from the weights current at this column (src/engine.rs:410-423):
+        // columns < i2 from the in-block values, columns >= i2 from the full-width buffer.
+        const int gi = j / g;
+        const int gend = min(j + g, n);
+        maxq = (float)((1u << gbits[gi]) - 1u);
+        float lmin = INFINITY, lmax = -INFINITY;
+#pragma unroll
+        for (int s2 = 0; s2 < NPL; ++s2) {
+          const int col = i1 + s2 * 64 + lane;
+          if (col < i2 && col >= j && col < gend) {
+            lmin = rs_minf(lmin, x[s2]);
+            lmax = rs_maxf(lmax, x[s2]);
+          }
+        }
+        for (int col = i2 + lane; col < gend; col += 64) {
+          const float v = wr[col];
+          lmin = rs_minf(lmin, v);
+          lmax = rs_maxf(lmax, v);
+        }
+        float xmin = rs_minf(0.0f, wave_min(lmin));
+        float xmax = rs_maxf(0.0f, wave_max(lmax));
+        if (xmin == 0.0f && xmax == 0.0f) {
+          xmin = -1.0f;
+          xmax = 1.0f;
+        }
+        grid_mk(xmin, xmax, maxq, &sc, &zr);
+        if (mse) {
+          // 24 clip ratios, one per lane; each lane runs its candidate's sequential error sum over
+          // the group in column order (src/quant.rs:65-81), then the first minimum wins.
+          const int cand = lane < 24 ? lane : 0;
+          const float p = 1.0f - 0.02f * (float)cand;
+          float cs, cz;
+          grid_mk(p * xmin, p * xmax, maxq, &cs, &cz);
+          float errs = 0.0f;
+#pragma unroll
+          for (int s2 = 0; s2 < NPL; ++s2) {
+            for (int jj = 0; jj < 64; ++jj) {
+              const int col = i1 + s2 * 64 + jj;
+              if (col >= i2 || col >= gend) break;
+              if (col < j) continue;
+              const float v = readlane(x[s2], jj);
+              float qq;
+              const float d = quant_dq(v, cs, cz, maxq, &qq);
+              const float ee = d - v;
+              errs = errs + ee * ee;
+            }
+          }
+          for (int col = i2 > j ? i2 : j; col < gend; ++col) {
+            const float v = wr[col];
+            float qq;
+            const float d = quant_dq(v, cs, cz, maxq, &qq);
+            const float ee = d - v;
+            errs = errs + ee * ee;
+          }
+          float be = (lane < 24 && errs == errs) ? errs : INFINITY;
+          int bc = (lane < 24) ? lane : (1 << 20);
+#pragma unroll
+          for (int o = 32; o > 0; o >>= 1) {
+            const float oe = __shfl_xor(be, o, 64);
+            const int oc = __shfl_xor(bc, o, 64);
+            if (oe < be || (oe == be && oc < bc)) {
+              be = oe;
+              bc = oc;
+            }
+          }
+          bc = readlane_i(bc, 0);
+          sc = readlane(cs, bc);
+          zr = readlane(cz, bc);
+        }
+        if (lane == 0) {
+          scales[(long)r * ng + gi] = sc;
+          zeros[(long)r * ng + gi] = zr;
+        }
+      }
+      const float xv = readlane(x[s], ii);
+      float q;
+      const float dq = quant_dq(xv, sc, zr, maxq, &q);
+      const float e = (xv - dq) * invd[j];
+      if (lane == ii) {
+        mq[s] = q;
+        mwq[s] = dq;
+        me[s] = e;
+      }
+      const float* urow = u + (long)j * n + i1;
+#pragma unroll
+      for (int s2 = s; s2 < NPL; ++s2) {
+        const int c = s2 * 64 + lane;
+        if (c > i && c < cnt) x[s2] = x[s2] - e * urow[c];
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < NPL; ++s) {
+    const int c = s * 64 + lane;
+    if (c < cnt) {
+      const long o = (long)r * n + i1 + c;
+      codes[o] = code_of(mq[s]);
+      wq[o] = mwq[s];
+      err[o] = me[s];
+    }
+  }
+}
+
+// colloss[chunk][j] = sum over the chunk's rows, in row order, of (f64)(eps*eps) (src/engine.rs:438).
+__global__ __launch_bounds__(256) void k_colloss(int rows, int n, int rc, const float* __restrict__ err,
+                                                 double* __restrict__ out) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  const int c = blockIdx.y;
+  if (j >= n) return;
+  const int r0 = c * rc, r1 = min(rows, r0 + rc);
+  double s = 0.0;
+  for (int r = r0; r < r1; ++r) {
+    const float e = err[(long)r * n + j];
+    s = s + (double)(e * e);
+  }
+  out[(long)c * n + j] = s;
+}
+
+__global__ __launch_bounds__(256) void k_sub(long count, const float* __restrict__ a, const float* __restrict__ b,
+                                             float* __restrict__ o) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx < count) o[idx] = a[idx] - b[idx];
+}
+
+// ---------------------------------------------------------------- phase 2 (src/engine.rs:534-670)
+// Closed-form f16 scale refit of group gi for every row of an active chunk (src/engine.rs:543-587).
+// G = E H[:, group] (rows x wd) comes from the chain GEMM. hu = uu H_CC is chained here per lane.
+template <int NPL>
+__global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, int gi, int rc,
+                                               const float* __restrict__ G, const float* __restrict__ h32,
+                                               const uint8_t* __restrict__ codes, float* __restrict__ scales,
+                                               const float* __restrict__ zeros, float* __restrict__ wq,
+                                               float* __restrict__ e, const uint8_t* __restrict__ active,
+                                               double* __restrict__ dlog, uint32_t* __restrict__ dcnt, int cap) {
+  const int lane = threadIdx.x & 63;
+  const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (r >= rows) return;
+  if (!active[r / rc]) {
+    if (lane == 0) dcnt[r] = 0;
+    return;
+  }
+  const int c0 = gi * g, wd = min(c0 + g, n) - c0;
+  const float z = zeros[(long)r * ng + gi];
+  const float s_old = scales[(long)r * ng + gi];
+  float uu[NPL], gg[NPL], cvh[NPL], acc[NPL];
+#pragma unroll
+  for (int s = 0; s < NPL; ++s) {
+    const int k = s * 64 + lane;
+    uu[s] = (k < wd) ? (float)codes[(long)r * n + c0 + k] - z : 0.0f;
+    gg[s] = (k < wd) ? G[(long)r * wd + k] : 0.0f;
+    cvh[s] = 0.0f;
+    acc[s] = 0.0f;
+  }
+  // hu[k2] = sum_k uu[k] * H[c0+k][c0+k2] (sgemm at src/engine.rs:560, KC-panelled)
+#pragma unroll
+  for (int s1 = 0; s1 < NPL; ++s1) {
+    for (int kk = 0; kk < 64; ++kk) {
+      const int k = s1 * 64 + kk;
+      if (k >= wd) break;
+      const float uk = readlane(uu[s1], kk);
+      const float* hrow = h32 + (long)(c0 + k) * n + c0;
+#pragma unroll
+      for (int s2 = 0; s2 < NPL; ++s2) {
+        const int k2 = s2 * 64 + lane;
+        if (k2 < wd) acc[s2] = __builtin_fmaf(uk, hrow[k2], acc[s2]);
+      }
+      if (((k + 1) % CDCLQ_KC) == 0 || k + 1 == wd) {
+#pragma unroll
+        for (int s2 = 0; s2 < NPL; ++s2) {
+          cvh[s2] = __builtin_fmaf(1.0f, acc[s2], cvh[s2]);
+          acc[s2] = 0.0f;
+        }
+      }
+    }
+  }
+  float num = 0.0f, den = 0.0f;
+#pragma unroll
+  for (int s1 = 0; s1 < NPL; ++s1) {
+    for (int kk = 0; kk < 64; ++kk) {
+      const int k = s1 * 64 + kk;
+      if (k >= wd) break;
+      const float uk = readlane(uu[s1], kk);
+      num = num + uk * readlane(gg[s1], kk);
+      den = den + uk * readlane(cvh[s1], kk);
+    }
+  }
+  uint32_t moved = 0;
+  if (den > 1e-30f) {
+    const float s_new = rs_maxf(round_f16(s_old + num / den), CDCLQ_F16_MIN_NORMAL);
+    const float d = s_new - s_old;
+    const float dl32 = (-2.0f * d) * num + (d * d) * den;
+    if ((double)dl32 < 0.0) {
+      if (lane == 0) {
+        scales[(long)r * ng + gi] = s_new;
+        dlog[(long)r * cap] = (double)dl32;
+      }
+#pragma unroll
+      for (int s = 0; s < NPL; ++s) {
+        const int k = s * 64 + lane;
+        if (k < wd) {
+          const long o = (long)r * n + c0 + k;
+          const float ndq = s_new * uu[s];
+          e[o] = e[o] + (wq[o] - ndq);
+          wq[o] = ndq;
+        }
+      }
+      moved = 1;
+    }
+  }
+  if (lane == 0) dcnt[r] = moved;
+}
+
+// Coordinate-descent sweeps over sub-block [c0, c0+wd) (src/engine.rs:600-658).
+template <int NPL>
+__global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
+                                            int sweeps, const float* __restrict__ G, const float* __restrict__ h32,
+                                            const uint8_t* __restrict__ gbits, const float* __restrict__ scales,
+                                            const float* __restrict__ zeros, uint8_t* __restrict__ codes,
+                                            float* __restrict__ wq, float* __restrict__ e,
+                                            const uint8_t* __restrict__ active, const uint8_t* __restrict__ sel,
+                                            double* __restrict__ dlog, uint32_t* __restrict__ dcnt, int cap) {
+  const int lane = threadIdx.x & 63;
+  const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (r >= rows) return;
+  const int chunk = r / rc;
+  if (!active[chunk] || !sel[(long)chunk * nsb + sb]) {
+    if (lane == 0) dcnt[r] = 0;
+    return;
+  }
+  float gg[NPL], mwq[NPL], me[NPL];
+  int mc[NPL];
+#pragma unroll
+  for (int s = 0; s < NPL; ++s) {
+    const int k = s * 64 + lane;
+    const long o = (long)r * n + c0 + k;
+    gg[s] = (k < wd) ? G[(long)r * wd + k] : 0.0f;
+    mwq[s] = (k < wd) ? wq[o] : 0.0f;
+    me[s] = (k < wd) ? e[o] : 0.0f;
+    mc[s] = (k < wd) ? (int)codes[o] : 0;
+  }
+  uint32_t moves = 0;
+  double* dl = dlog + (long)r * cap;
+  for (int sw = 0; sw < sweeps; ++sw) {
+    int changed = 0;
+#pragma unroll
+    for (int s = 0; s < NPL; ++s) {
+      for (int ii = 0; ii < 64; ++ii) {
+        const int jj = s * 64 + ii;
+        if (jj >= wd) break;
+        const int j = c0 + jj;
+        const int gi = j / g;
+        const float maxq = (float)((1u << gbits[gi]) - 1u);
+        const float sc = scales[(long)r * ng + gi];
+        const float z = zeros[(long)r * ng + gi];
+        const float hjj = h32[(long)j * n + j];
+        const float cur = readlane(mwq[s], ii);
+        const float gj = readlane(gg[s], ii);
+        const int code = readlane_i(mc[s], ii);
+        const float target = cur + gj / hjj;
+        float q;
+        const float newdq = quant_dq(target, sc, z, maxq, &q);
+        const int qc = (int)code_of(q);
+        if (qc != code) {
+          const float de = cur - newdq;
+          const float d32 = (2.0f * de) * gj + (de * de) * hjj;
+          if (lane == 0) dl[moves] = (double)d32;
+          ++moves;
+          const float* hrow = h32 + (long)j * n + c0;
+#pragma unroll
+          for (int s2 = 0; s2 < NPL; ++s2) {
+            const int k = s2 * 64 + lane;
+            if (k < wd) gg[s2] = gg[s2] + de * hrow[k];
+          }
+          if (lane == ii) {
+            mwq[s] = newdq;
+            mc[s] = qc;
+            me[s] = me[s] + de;
+          }
+          changed = 1;
+        }
+      }
+    }
+    if (!changed) break;
+  }
+#pragma unroll
+  for (int s = 0; s < NPL; ++s) {
+    const int k = s * 64 + lane;
+    if (k < wd) {
+      const long o = (long)r * n + c0 + k;
+      wq[o] = mwq[s];
+      e[o] = me[s];
+      codes[o] = (uint8_t)mc[s];
+    }
+  }
+  if (lane == 0) dcnt[r] = moves;
+}
+
+// Per-chunk loss bookkeeping in the reference's order: rows ascending, each row's accepted
+// deltas in the order they were made (src/engine.rs:583, :640).
+__global__ __launch_bounds__(64) void k_chunk_accum(int rows, int rc, int nchunks, int cap,
+                                                    const double* __restrict__ dlog,
+                                                    const uint32_t* __restrict__ dcnt,
+                                                    const uint8_t* __restrict__ active, double* __restrict__ ld,
+                                                    uint64_t* __restrict__ upd) {
+  const int c = blockIdx.x * 64 + threadIdx.x;
+  if (c >= nchunks || !active[c]) return;
+  double acc = ld[c];
+  uint64_t u = upd[c];
+  const int r1 = min(rows, (c + 1) * rc);
+  for (int r = c * rc; r < r1; ++r) {
+    const uint32_t k = dcnt[r];
+    const double* p = dlog + (long)r * cap;
+    for (uint32_t q = 0; q < k; ++q) acc = acc + p[q];
+    u += k;
+  }
+  ld[c] = acc;
+  upd[c] = u;
+}
+
+// ---------------------------------------------------------------- synthetic inputs
+__global__ __launch_bounds__(256) void k_synth_normal(uint64_t seed, uint64_t offset, long count, float sigma,
+                                                      float* __restrict__ out) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx < count) out[idx] = synth_normal_at(seed, offset + (uint64_t)idx) * sigma;
+}
+
+__global__ __launch_bounds__(256) void k_synth_tokens(uint64_t seed, uint64_t row0, long t, int n,
+                                                      const float* __restrict__ cs, float* __restrict__ x) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= t * (long)n) return;
+  const long r = idx / n;
+  const int j = (int)(idx % n);
+  x[idx] = synth_normal_at(seed, (row0 + (uint64_t)r) * (uint64_t)n + (uint64_t)j) * (cs ? cs[j] : 1.0f);
+}
+
+__global__ __launch_bounds__(256) void k_f64_to_f32(long count, const double* __restrict__ a, float* __restrict__ b) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx < count) b[idx] = (float)a[idx];
+}
+
+// Block partial sums of (f64)e * (f64)eh for proxy_loss (src/engine.rs:814).
+__global__ __launch_bounds__(256) void k_proxy_reduce(long count, const float* __restrict__ e,
+                                                      const float* __restrict__ eh, double* __restrict__ partial) {
+  __shared__ double red[256];
+  double s = 0.0;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < count; i += (long)gridDim.x * 256)
+    s += (double)e[i] * (double)eh[i];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
+}
+
+}  // namespace
+
+hipError_t diag_extract(hipStream_t st, int n, const float* h, float* diag) {
+  hipLaunchKernelGGL(k_diag_extract, dim3(nblk(n)), dim3(256), 0, st, n, h, diag);
+  return hipGetLastError();
+}
+hipError_t permute_w(hipStream_t st, int d_out, int n, const float* w, const uint32_t* perm, const uint8_t* dead_perm,
+                     float* wp) {
+  hipLaunchKernelGGL(k_permute_w, dim3(nblk((long)d_out * n)), dim3(256), 0, st, d_out, n, w, perm, dead_perm, wp);
+  return hipGetLastError();
+}
+hipError_t permute_m(hipStream_t st, int n, const float* m, const uint32_t* perm, float damp32, float* mp) {
+  hipLaunchKernelGGL(k_permute_m, dim3(nblk((long)n * n)), dim3(256), 0, st, n, m, perm, damp32, mp);
+  return hipGetLastError();
+}
+hipError_t colsq(hipStream_t st, int d_out, int n, const float* w, const uint8_t* dead, double* out) {
+  hipLaunchKernelGGL(k_colsq, dim3(nblk(n)), dim3(256), 0, st, d_out, n, w, dead, out);
+  return hipGetLastError();
+}
+hipError_t inv_diag(hipStream_t st, int n, const float* u, float* invd) {
+  hipLaunchKernelGGL(k_inv_diag, dim3(nblk(n)), dim3(256), 0, st, n, u, invd);
+  return hipGetLastError();
+}
+
+static int npl_for(int cnt) {
+  if (cnt <= 64) return 1;
+  if (cnt <= 128) return 2;
+  if (cnt <= 256) return 4;
+  if (cnt <= 512) return 8;
+  if (cnt <= 1024) return 16;
+  return 0;
+}
+
+hipError_t gptq_block(hipStream_t st, int rows, int n, int i1, int cnt, int g, int ng, float* w, const float* u,
+                      const float* invd, const uint8_t* gbits, int mse, float* scales, float* zeros, uint8_t* codes,
+                      float* wq, float* err) {
+  const dim3 grid((rows + 3) / 4), blk(256);
+#define GPTQ_CASE(N)                                                                                                   \
+  case N:                                                                                                              \
+    hipLaunchKernelGGL(k_gptq_block<N>, grid, blk, 0, st, rows, n, i1, cnt, g, ng, w, u, invd, gbits, mse, scales,    \
+                       zeros, codes, wq, err);                                                                         \
+    break;
+  switch (npl_for(cnt)) {
+    GPTQ_CASE(1)
+    GPTQ_CASE(2)
+    GPTQ_CASE(4)
+    GPTQ_CASE(8)
+    GPTQ_CASE(16)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef GPTQ_CASE
+  return hipGetLastError();
+}
+
+hipError_t colloss(hipStream_t st, int rows, int n, int rc, const float* err, double* out) {
+  const int nchunks = (rows + rc - 1) / rc;
+  hipLaunchKernelGGL(k_colloss, dim3(nblk(n), nchunks), dim3(256), 0, st, rows, n, rc, err, out);
+  return hipGetLastError();
+}
+
+hipError_t sub_f32(hipStream_t st, size_t count, const float* a, const float* b, float* out) {
+  hipLaunchKernelGGL(k_sub, dim3(nblk((long)count)), dim3(256), 0, st, (long)count, a, b, out);
+  return hipGetLastError();
+}
+
+hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, int rc, const float* G, const float* h32,
+                       const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
+                       const uint8_t* active, double* dlog, uint32_t* dcnt, int cap) {
+  const int wd = std::min(gi * g + g, n) - gi * g;
+  const dim3 grid((rows + 3) / 4), blk(256);
+#define REFIT_CASE(N)                                                                                                  \
+  case N:                                                                                                              \
+    hipLaunchKernelGGL(k_refit<N>, grid, blk, 0, st, rows, n, ng, g, gi, rc, G, h32, codes, scales, zeros, wq, e,      \
+                       active, dlog, dcnt, cap);                                                                       \
+    break;
+  switch (npl_for(wd)) {
+    REFIT_CASE(1)
+    REFIT_CASE(2)
+    REFIT_CASE(4)
+    REFIT_CASE(8)
+    REFIT_CASE(16)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef REFIT_CASE
+  return hipGetLastError();
+}
+
+hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
+                       int sweeps, const float* G, const float* h32, const uint8_t* gbits, const float* scales,
+                       const float* zeros, uint8_t* codes, float* wq, float* e, const uint8_t* active,
+                       const uint8_t* sel, double* dlog, uint32_t* dcnt, int cap) {
+  const dim3 grid((rows + 3) / 4), blk(256);
+#define CD_CASE(N)                                                                                                     \
+  case N:                                                                                                              \
+    hipLaunchKernelGGL(k_cd<N>, grid, blk, 0, st, rows, n, ng, g, c0, wd, sb, nsb, rc, sweeps, G, h32, gbits, scales,  \
+                       zeros, codes, wq, e, active, sel, dlog, dcnt, cap);                                             \
+    break;
+  switch (npl_for(wd)) {
+    CD_CASE(1)
+    CD_CASE(2)
+    CD_CASE(4)
+    CD_CASE(8)
+    CD_CASE(16)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef CD_CASE
+  return hipGetLastError();
+}
+
+hipError_t chunk_accum(hipStream_t st, int rows, int rc, int nchunks, int cap, const double* dlog, const uint32_t* dcnt,
+                       const uint8_t* active, double* ld, uint64_t* upd) {
+  hipLaunchKernelGGL(k_chunk_accum, dim3((nchunks + 63) / 64), dim3(64), 0, st, rows, rc, nchunks, cap, dlog, dcnt,
+                     active, ld, upd);
+  return hipGetLastError();
+}
+
+hipError_t synth_normal(hipStream_t st, uint64_t seed, uint64_t offset, size_t count, float sigma, float* out) {
+  if (!count) return hipSuccess;
+  hipLaunchKernelGGL(k_synth_normal, dim3(nblk((long)count)), dim3(256), 0, st, seed, offset, (long)count, sigma, out);
+  return hipGetLastError();
+}
+
+hipError_t synth_tokens(hipStream_t st, uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale,
+                        float* x) {
+  if (!t || !n) return hipSuccess;
+  hipLaunchKernelGGL(k_synth_tokens, dim3(nblk((long)(t * n))), dim3(256), 0, st, seed, row0, (long)t, (int)n, ch_scale,
+                     x);
+  return hipGetLastError();
+}
+
+hipError_t f64_to_f32(hipStream_t st, size_t count, const double* a, float* b) {
+  if (!count) return hipSuccess;
+  hipLaunchKernelGGL(k_f64_to_f32, dim3(nblk((long)count)), dim3(256), 0, st, (long)count, a, b);
+  return hipGetLastError();
+}
+
+hipError_t proxy_reduce(hipStream_t st, size_t count, const float* e, const float* eh, double* partial, int nblocks) {
+  hipLaunchKernelGGL(k_proxy_reduce, dim3(nblocks), dim3(256), 0, st, (long)count, e, eh, partial);
+  return hipGetLastError();
+}
+
+}  // namespace cdclq

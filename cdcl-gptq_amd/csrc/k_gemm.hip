@@ -1,0 +1,289 @@
+// Bit-exact chain GEMMs for gfx950.
+//
+// The reference computes every GEMM through matrixmultiply 0.3.8 (src/linalg.rs:56-184). Its FMA
+// micro-kernels give each C element one sequential fused-multiply-add chain over k, restarted at
+// every KC = 256 panel, and fold the panel results in order: C = fma(alpha, chain_p, C'), with
+// C' = beta*C for the first panel (C unread when beta == 0) and C afterwards. These kernels keep
+// exactly that per-element operation sequence -- which makes them bit-identical to the
+// reference -- and are free in everything else: tile shapes, thread mapping, and running the
+// panels of one element in parallel (the ordered fold then happens in k_combine).
+#include "cdclq_dev.h"
+#include "kernels.h"
+
+namespace cdclq {
+namespace {
+
+constexpr int BM = 64, BN = 64, KT = 16;
+
+__device__ __forceinline__ float fma_t(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+__device__ __forceinline__ double fma_t(double a, double b, double c) { return __builtin_fma(a, b, c); }
+
+// 64x64 output tile per 256-thread workgroup, 4x4 per thread, k staged through LDS in steps of
+// KT (KT divides KC, so panel ends coincide with stage ends).
+template <typename T, bool SPLIT, bool LOWER>
+__global__ __launch_bounds__(256) void k_gemm(int m, int n, int k, T alpha, int beta_one, const T* __restrict__ A,
+                                              long rsa, long csa, const T* __restrict__ B, long rsb, long csb,
+                                              T* __restrict__ C, long rsc, long csc, T* __restrict__ P) {
+  __shared__ T As[KT][BM + 4];
+  __shared__ T Bs[KT][BN + 4];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int i0 = blockIdx.y * BM, j0 = blockIdx.x * BN;
+  if (LOWER && j0 > i0 + BM - 1) return;  // tile strictly above the diagonal
+  int kbeg = 0, kend = k;
+  if (SPLIT) {
+    kbeg = blockIdx.z * CDCLQ_KC;
+    kend = min(k, kbeg + CDCLQ_KC);
+  }
+  T acc[4][4], cv[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      acc[a][b] = T(0);
+      cv[a][b] = T(0);
+    }
+  if (!SPLIT && beta_one) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int gi = i0 + ty * 4 + a, gj = j0 + tx * 4 + b;
+        if (gi < m && gj < n) cv[a][b] = C[(long)gi * rsc + (long)gj * csc];
+      }
+  }
+  for (int k0 = kbeg; k0 < kend; k0 += KT) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = tid + 256 * q;
+      int ii, kk;
+      if (csa == 1) {
+        kk = e & (KT - 1);
+        ii = e >> 4;
+      } else {
+        ii = e & (BM - 1);
+        kk = e >> 6;
+      }
+      const int gi = i0 + ii, gk = k0 + kk;
+      As[kk][ii] = (gi < m && gk < kend) ? A[(long)gi * rsa + (long)gk * csa] : T(0);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = tid + 256 * q;
+      int jj, kk;
+      if (csb == 1) {
+        jj = e & (BN - 1);
+        kk = e >> 6;
+      } else {
+        kk = e & (KT - 1);
+        jj = e >> 4;
+      }
+      const int gj = j0 + jj, gk = k0 + kk;
+      Bs[kk][jj] = (gj < n && gk < kend) ? B[(long)gk * rsb + (long)gj * csb] : T(0);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) {
+      T av[4], bv[4];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) av[a] = As[kk][ty * 4 + a];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) bv[b] = Bs[kk][tx * 4 + b];
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = fma_t(av[a], bv[b], acc[a][b]);
+    }
+    __syncthreads();
+    if (!SPLIT) {
+      const int kn = k0 + KT;
+      if ((kn % CDCLQ_KC) == 0 || kn >= kend) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            cv[a][b] = fma_t(alpha, acc[a][b], cv[a][b]);
+            acc[a][b] = T(0);
+          }
+      }
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int gi = i0 + ty * 4 + a, gj = j0 + tx * 4 + b;
+      if (gi < m && gj < n) {
+        if (SPLIT)
+          P[((long)blockIdx.z * m + gi) * n + gj] = acc[a][b];
+        else
+          C[(long)gi * rsc + (long)gj * csc] = cv[a][b];
+      }
+    }
+}
+
+// Ordered fold of per-panel chains: C = fma(alpha, P_p, C') for p = 0, 1, ... (see file header).
+template <typename T>
+__global__ __launch_bounds__(256) void k_combine(int m, int n, int np, T alpha, int beta_one, const T* __restrict__ P,
+                                                 T* __restrict__ C, long rsc, long csc) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)m * n) return;
+  const int i = (int)(idx / n), j = (int)(idx % n);
+  T* c = C + (long)i * rsc + (long)j * csc;
+  T cv = beta_one ? *c : T(0);
+  for (int p = 0; p < np; ++p) cv = fma_t(alpha, P[((long)p * m + i) * n + j], cv);
+  *c = cv;
+}
+
+// ---- Gram accumulation (src/linalg.rs:388-418): per 2048-token chunk, tmp = X^T Y with the
+// panel-chained order above (alpha 1, beta 0), then H += (f64)tmp in chunk order. With Y == X the
+// chain of element (j, i) is the chain of (i, j) with the factors of every fma swapped, i.e. the
+// same bits, so only tiles with ti <= tj are computed and mirrored; each side keeps its own f64
+// accumulator because the incoming H need not be symmetric.
+template <bool SYM>
+__global__ __launch_bounds__(256) void k_gram(int t, int n, const float* __restrict__ X, const float* __restrict__ Y,
+                                              double* __restrict__ H, const int2* __restrict__ tiles) {
+  __shared__ float Xs[KT][BM + 4];
+  __shared__ float Ys[KT][BN + 4];
+  const int2 tl = tiles[blockIdx.x];
+  const int i0 = tl.x * BM, j0 = tl.y * BN;
+  const bool mirror = SYM && (tl.x != tl.y);
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  double hA[4][4], hB[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int gi = i0 + ty * 4 + a, gj = j0 + tx * 4 + b;
+      const bool ok = gi < n && gj < n;
+      hA[a][b] = ok ? H[(long)gi * n + gj] : 0.0;
+      hB[a][b] = (ok && mirror) ? H[(long)gj * n + gi] : 0.0;
+    }
+  for (int c0 = 0; c0 < t; c0 += 2048) {
+    const int cend = min(t, c0 + 2048);
+    float acc[4][4], tmp[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        acc[a][b] = 0.0f;
+        tmp[a][b] = 0.0f;
+      }
+    for (int k0 = c0; k0 < cend; k0 += KT) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = tid + 256 * q;
+        const int kk = e >> 6, jj = e & 63;
+        const int tk = k0 + kk;
+        Xs[kk][jj] = (tk < cend && i0 + jj < n) ? X[(long)tk * n + i0 + jj] : 0.0f;
+        Ys[kk][jj] = (tk < cend && j0 + jj < n) ? Y[(long)tk * n + j0 + jj] : 0.0f;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk) {
+        float av[4], bv[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a) av[a] = Xs[kk][ty * 4 + a];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) bv[b] = Ys[kk][tx * 4 + b];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) acc[a][b] = __builtin_fmaf(av[a], bv[b], acc[a][b]);
+      }
+      __syncthreads();
+      const int kn = k0 + KT;
+      if ((kn % CDCLQ_KC) == 0 || kn >= cend) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            tmp[a][b] = __builtin_fmaf(1.0f, acc[a][b], tmp[a][b]);
+            acc[a][b] = 0.0f;
+          }
+      }
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        hA[a][b] += (double)tmp[a][b];
+        if (mirror) hB[a][b] += (double)tmp[a][b];
+      }
+  }
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int gi = i0 + ty * 4 + a, gj = j0 + tx * 4 + b;
+      if (gi < n && gj < n) {
+        H[(long)gi * n + gj] = hA[a][b];
+        if (mirror) H[(long)gj * n + gi] = hB[a][b];
+      }
+    }
+}
+
+}  // namespace
+
+size_t gemm_partials_elems(int m, int n, int k) {
+  const size_t np = (size_t)((k + CDCLQ_KC - 1) / CDCLQ_KC);
+  return np * (size_t)m * (size_t)n;
+}
+
+template <typename T>
+hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, int beta_one, const T* A, long rsa, long csa,
+                      const T* B, long rsb, long csb, T* C, long rsc, long csc, bool lower, T* partials) {
+  if (m <= 0 || n <= 0) return hipSuccess;
+  if (k <= 0) {
+    // k == 0: C = beta * C (src/linalg.rs:82-91); beta in {0, 1}
+    if (!beta_one) {
+      hipLaunchKernelGGL((k_combine<T>), dim3((unsigned)(((long)m * n + 255) / 256)), dim3(256), 0, st, m, n, 0, alpha,
+                         0, (const T*)nullptr, C, rsc, csc);
+    }
+    return hipGetLastError();
+  }
+  const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM, 1);
+  const int np = (k + CDCLQ_KC - 1) / CDCLQ_KC;
+  if (np > 1 && partials != nullptr && !lower) {
+    dim3 g3 = grid;
+    g3.z = np;
+    hipLaunchKernelGGL((k_gemm<T, true, false>), g3, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa, B, rsb,
+                       csb, C, rsc, csc, partials);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_combine<T>), dim3((unsigned)(((long)m * n + 255) / 256)), dim3(256), 0, st, m, n, np, alpha,
+                       beta_one, (const T*)partials, C, rsc, csc);
+    return hipGetLastError();
+  }
+  if (lower)
+    hipLaunchKernelGGL((k_gemm<T, false, true>), grid, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa, B,
+                       rsb, csb, C, rsc, csc, (T*)nullptr);
+  else
+    hipLaunchKernelGGL((k_gemm<T, false, false>), grid, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa, B,
+                       rsb, csb, C, rsc, csc, (T*)nullptr);
+  return hipGetLastError();
+}
+
+template hipError_t gemm_chain<float>(hipStream_t, int, int, int, float, int, const float*, long, long, const float*,
+                                      long, long, float*, long, long, bool, float*);
+template hipError_t gemm_chain<double>(hipStream_t, int, int, int, double, int, const double*, long, long,
+                                       const double*, long, long, double*, long, long, bool, double*);
+
+std::vector<int2> gram_tiles(int n, bool sym) {
+  const int nt = (n + BM - 1) / BM;
+  std::vector<int2> v;
+  for (int i = 0; i < nt; ++i)
+    for (int j = sym ? i : 0; j < nt; ++j) v.push_back(make_int2(i, j));
+  return v;
+}
+
+hipError_t gram_accumulate(hipStream_t st, int t, int n, const float* X, const float* Y, double* H, bool sym,
+                           const int2* tiles, int ntiles) {
+  if (n <= 0 || t <= 0 || ntiles <= 0) return hipSuccess;
+  if (sym)
+    hipLaunchKernelGGL((k_gram<true>), dim3(ntiles), dim3(256), 0, st, t, n, X, Y, H, tiles);
+  else
+    hipLaunchKernelGGL((k_gram<false>), dim3(ntiles), dim3(256), 0, st, t, n, X, Y, H, tiles);
+  return hipGetLastError();
+}
+
+}  // namespace cdclq

@@ -1,0 +1,65 @@
+// Host-side launchers of the gfx950 kernels (one translation unit per kernel family).
+// All launchers enqueue on `st` and return hipGetLastError() of the launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <vector>
+
+namespace cdclq {
+
+// ---- k_gemm.hip: bit-exact chain GEMMs (matrixmultiply 0.3.8 order, see k_gemm.hip)
+// C = alpha * A * B + beta * C, alpha in {+1,-1}, beta in {0,1}. `lower` computes only tiles that
+// intersect the lower triangle (i >= j) of C. When k spans several KC panels and `partials` is
+// non-null, panels run in parallel into partials[npanel][m][n] and are combined in panel order.
+template <typename T>
+hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, int beta_one, const T* A, long rsa, long csa,
+                      const T* B, long rsb, long csb, T* C, long rsc, long csc, bool lower, T* partials);
+size_t gemm_partials_elems(int m, int n, int k);
+
+// H (n x n, f64) += X^T Y over 2048-token chunks; X, Y token-major (t x n). sym: Y == X.
+// `tiles` lists the 64x64 output tiles (gram_tiles), uploaded by the caller.
+std::vector<int2> gram_tiles(int n, bool sym);
+hipError_t gram_accumulate(hipStream_t st, int t, int n, const float* X, const float* Y, double* H, bool sym,
+                           const int2* tiles, int ntiles);
+
+// ---- k_factor.hip: damping, Cholesky, triangular inverse, U
+hipError_t build_flipped(hipStream_t st, int n, const float* h, const uint32_t* perm, double damp_val, double* a,
+                         float* h32);
+hipError_t build_flipped_f64(hipStream_t st, int n, const double* h, double* a);
+hipError_t chol_diag(hipStream_t st, int n, double* a, int k, int kb, int* status, double* pivot);
+hipError_t chol_panel(hipStream_t st, int n, double* a, int k, int kb, const int* status);
+hipError_t trinv_diag(hipStream_t st, int n, const double* l, double* y, const int* status);
+hipError_t scatter_u(hipStream_t st, int n, const double* y, float* u);
+hipError_t fill_zero_f64(hipStream_t st, double* p, size_t count);
+
+// ---- k_engine.hip: phase 1 / phase 2 sweeps and helpers
+hipError_t permute_w(hipStream_t st, int d_out, int n, const float* w, const uint32_t* perm, const uint8_t* dead_perm,
+                     float* wp);
+hipError_t permute_m(hipStream_t st, int n, const float* m, const uint32_t* perm, float damp32, float* mp);
+hipError_t diag_extract(hipStream_t st, int n, const float* h, float* diag);
+hipError_t colsq(hipStream_t st, int d_out, int n, const float* w, const uint8_t* dead, double* out);
+hipError_t inv_diag(hipStream_t st, int n, const float* u, float* invd);
+hipError_t gptq_block(hipStream_t st, int rows, int n, int i1, int cnt, int g, int ng, float* w, const float* u,
+                      const float* invd, const uint8_t* gbits, int mse, float* scales, float* zeros, uint8_t* codes,
+                      float* wq, float* err);
+hipError_t colloss(hipStream_t st, int rows, int n, int rc, const float* err, double* out);
+hipError_t sub_f32(hipStream_t st, size_t count, const float* a, const float* b, float* out);
+hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, int rc, const float* G, const float* h32,
+                       const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
+                       const uint8_t* active, double* dlog, uint32_t* dcnt, int cap);
+hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
+                       int sweeps, const float* G, const float* h32, const uint8_t* gbits, const float* scales,
+                       const float* zeros, uint8_t* codes, float* wq, float* e, const uint8_t* active,
+                       const uint8_t* sel, double* dlog, uint32_t* dcnt, int cap);
+hipError_t chunk_accum(hipStream_t st, int rows, int rc, int nchunks, int cap, const double* dlog, const uint32_t* dcnt,
+                       const uint8_t* active, double* ld, uint64_t* upd);
+hipError_t synth_normal(hipStream_t st, uint64_t seed, uint64_t offset, size_t count, float sigma, float* out);
+hipError_t synth_tokens(hipStream_t st, uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale,
+                        float* x);
+hipError_t f64_to_f32(hipStream_t st, size_t count, const double* a, float* b);
+hipError_t proxy_reduce(hipStream_t st, size_t count, const float* e, const float* eh, double* partial, int nblocks);
+
+}  // namespace cdclq

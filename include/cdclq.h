@@ -1,0 +1,170 @@
+/*
+ * cdclq.h -- C ABI of the MI355X-native (gfx950) CDCL-GPTQ per-layer quantization engine.
+ *
+ * Drop-in boundary for the reference Rust crate `cdclq` 1.0.1 (tailot/CDCL-GPTQ): each entry
+ * point below names the reference function it replaces (path:line in that crate). Plain
+ * pointers and sizes only; no GPU runtime types appear in any signature.
+ *
+ * Conventions
+ *  - Matrices are row-major. `*_device` entry points take pointers to device (HBM) memory of the
+ *    context's GPU; the others take host memory and stage it through the device themselves.
+ *  - Every call is synchronous (returns after the device work finished), like the reference.
+ *  - Status codes: CDCLQ_OK on success; on failure cdclq_last_error(ctx) holds the message. For
+ *    conditions the reference reports with anyhow::bail! the text is the reference's text.
+ *  - A context is thread-compatible, not thread-safe: one context per host thread and GPU.
+ *    It owns the device workspace and the one-entry factor cache (PrepCache).
+ *  - No call aborts the process.
+ */
+#ifndef CDCLQ_H
+#define CDCLQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CDCLQ_ABI_VERSION 1
+
+typedef enum cdclq_status {
+  CDCLQ_OK = 0,
+  CDCLQ_INVALID_ARG = 1, /* src/engine.rs:240-258 validate(), shape/size errors */
+  CDCLQ_NOT_PD = 2,      /* src/linalg.rs:215-219 non-positive / non-finite pivot */
+  CDCLQ_NON_FINITE = 3,  /* reserved: non-finite input scan (src/io.rs:205-212) */
+  CDCLQ_DEVICE = 4,      /* HIP runtime error */
+  CDCLQ_OOM = 5          /* device allocation failed */
+} cdclq_status;
+
+/* engine::Method (src/engine.rs:83-88) */
+typedef enum cdclq_method { CDCLQ_METHOD_GPTQ = 0, CDCLQ_METHOD_CDCL = 1 } cdclq_method;
+
+/* engine::Config (src/engine.rs:94-144); defaults via cdclq_default_config
+ * (src/engine.rs:146-167). Booleans are 0/1. */
+typedef struct cdclq_config {
+  uint32_t bits;          /* 2..=8 */
+  uint32_t skeleton_bits; /* 2..=8 */
+  uint64_t group;         /* 0 = one group per row */
+  uint64_t block;
+  uint64_t sub_block;
+  uint64_t cd_sweeps;
+  uint64_t passes;
+  uint64_t row_chunk; /* 0 = automatic from nthreads (src/engine.rs:768-770) */
+  double damp;
+  double skeleton_pct;
+  double refine_frac;
+  double tol;
+  int32_t act_order;
+  int32_t mse_grid;
+  int32_t method; /* cdclq_method */
+  int32_t refit_scales;
+} cdclq_config;
+
+/* engine::LayerStats (src/engine.rs:174-199) */
+typedef struct cdclq_layer_stats {
+  double loss_gptq;
+  double loss_final;
+  uint64_t subblocks_total;
+  uint64_t subblocks_refined;
+  uint64_t code_updates;
+  uint64_t skeleton_groups;
+  double bits_codes;
+  double bits_total;
+  double secs_prepare;
+  double secs_quant;
+} cdclq_layer_stats;
+
+typedef struct cdclq_ctx cdclq_ctx;
+
+int cdclq_abi_version(void);
+size_t cdclq_sizeof_config(void);
+size_t cdclq_sizeof_stats(void);
+
+/* Config::default() (src/engine.rs:146-167) */
+void cdclq_default_config(cdclq_config* cfg);
+
+/* Number of groups for a layer of width d_in: ceil(d_in / effective_group)
+ * (src/engine.rs:227-233, :705). */
+size_t cdclq_num_groups(const cdclq_config* cfg, size_t d_in);
+
+/* Context on GPU `device`: owns a HIP stream, the device workspace and the PrepCache
+ * (src/engine.rs:220-223, created as `None` by every reference caller). */
+int cdclq_ctx_create(int device, cdclq_ctx** out);
+void cdclq_ctx_destroy(cdclq_ctx* ctx);
+/* Message of the last failed call on ctx ("" if none). Valid until the next call on ctx. */
+const char* cdclq_last_error(const cdclq_ctx* ctx);
+/* Drops the cached factorisation (`*cache = None`, src/engine.rs:720). */
+int cdclq_ctx_clear_cache(cdclq_ctx* ctx);
+
+/*
+ * engine::quantize_layer (src/engine.rs:690-799).
+ *   w      d_out x d_in f32, original column order
+ *   h      d_in x d_in f32 calibration Hessian
+ *   m      optional d_in x d_in cross-covariance (NULL = symmetric target)
+ *   hkey   Hessian identity for the factor cache (src/engine.rs:718)
+ *   nthreads  stands in for rayon::current_num_threads() when cfg->row_chunk == 0
+ * Outputs (caller-allocated): codes[d_out*d_in] u8 in permuted column order, scales[d_out*ng],
+ * zeros[d_out*ng] (f32, f16-exact / integer-valued), perm[d_in] (perm[j] = original column at
+ * permuted position j), gbits[ng], stats (may be NULL). ng = cdclq_num_groups(cfg, d_in).
+ */
+int cdclq_quantize_layer(cdclq_ctx* ctx, const float* w, size_t d_out, size_t d_in, const float* h, const float* m,
+                         const char* hkey, const cdclq_config* cfg, size_t nthreads, uint8_t* codes, float* scales,
+                         float* zeros, uint32_t* perm, uint8_t* gbits, cdclq_layer_stats* stats);
+/* Same contract; w, h, m, codes, scales, zeros are device pointers; perm, gbits, stats host. */
+int cdclq_quantize_layer_device(cdclq_ctx* ctx, const float* w, size_t d_out, size_t d_in, const float* h,
+                                const float* m, const char* hkey, const cdclq_config* cfg, size_t nthreads,
+                                uint8_t* codes, float* scales, float* zeros, uint32_t* perm, uint8_t* gbits,
+                                cdclq_layer_stats* stats);
+
+/* linalg::gram_accumulate (src/linalg.rs:388-418): h (n x n, f64) += x^T y, x and y token-major
+ * t x n f32. y == x selects the symmetric Hessian path. */
+int cdclq_gram_accumulate(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h);
+int cdclq_gram_accumulate_device(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h);
+
+/* linalg::upper_chol_of_inverse (src/linalg.rs:362-375): u (n x n f32, upper) with
+ * h^-1 = u^T u. h is not modified. */
+int cdclq_upper_chol_of_inverse(cdclq_ctx* ctx, const double* h, size_t n, float* u);
+int cdclq_upper_chol_of_inverse_device(cdclq_ctx* ctx, const double* h, size_t n, float* u);
+
+/* engine::proxy_loss (src/engine.rs:808-815): sum_rows e H e^T with e = w_t - w_hat. */
+int cdclq_proxy_loss(cdclq_ctx* ctx, const float* w_t, const float* w_hat, size_t rows, size_t n, const float* h,
+                     double* out);
+
+/* ---- Device memory staging for callers without their own GPU runtime binding. ---- */
+int cdclq_device_alloc(cdclq_ctx* ctx, size_t bytes, void** ptr);
+int cdclq_device_free(cdclq_ctx* ctx, void* ptr);
+int cdclq_memcpy_h2d(cdclq_ctx* ctx, void* dst, const void* src, size_t bytes);
+int cdclq_memcpy_d2h(cdclq_ctx* ctx, void* dst, const void* src, size_t bytes);
+int cdclq_memset_device(cdclq_ctx* ctx, void* dst, int value, size_t bytes);
+
+/* ---- Synthetic calibration inputs generated in HBM (benchmark harness support; no reference
+ * counterpart -- the reference's bench generator is src/bench.rs:41-97). Counter-based:
+ * value i of stream `seed` = Box-Muller(splitmix64 draws 2i, 2i+1), identical on host and device. */
+int cdclq_synth_normal_device(cdclq_ctx* ctx, uint64_t seed, uint64_t offset, size_t count, float sigma, float* out);
+/* Host array of n channel scales: exactly round(frac * n) channels (seeded partial Fisher-Yates on
+ * the same counter stream) get `factor`, the rest 1. */
+int cdclq_synth_outlier_scales(uint64_t seed, size_t n, double frac, float factor, float* scales);
+/* x[r][j] = normal(seed, (row0 + r) * n + j) * ch_scale[j]; ch_scale is a host array of n. */
+int cdclq_synth_tokens_device(cdclq_ctx* ctx, uint64_t seed, uint64_t row0, size_t t, size_t n,
+                              const float* ch_scale, float* x);
+/* h32[i] = (float)h64[i] (the cast at src/bench.rs:177). */
+int cdclq_f64_to_f32_device(cdclq_ctx* ctx, const double* h64, size_t count, float* h32);
+
+/* ---- Per-phase device timing (HIP events on the context's stream), for the harness. ---- */
+enum {
+  CDCLQ_PHASE_GRAM = 0,     /* H-accumulation kernels */
+  CDCLQ_PHASE_FACTOR = 1,   /* permute/damp + Cholesky + triangular inverse -> U */
+  CDCLQ_PHASE_GPTQ = 2,     /* phase 1: block sweeps + lazy GEMM */
+  CDCLQ_PHASE_REPAIR = 3,   /* phase 2: refit + coordinate descent */
+  CDCLQ_PHASE_TARGET = 4,   /* asymmetric target GEMMs */
+  CDCLQ_PHASE_COUNT = 5
+};
+int cdclq_ctx_set_timing(cdclq_ctx* ctx, int enable);
+int cdclq_ctx_reset_timing(cdclq_ctx* ctx);
+/* Accumulated device milliseconds and number of timed launches of `phase` since the reset. */
+int cdclq_ctx_get_timing(cdclq_ctx* ctx, int phase, uint64_t* launches, double* ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

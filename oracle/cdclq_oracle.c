@@ -1,0 +1,1186 @@
+/*
+ * CPU oracle: plain-C restatement of the reference engine (tailot/CDCL-GPTQ).
+ * TEST INFRASTRUCTURE ONLY -- see cdclq_oracle.h for what may load it and what pins it.
+ *
+ * Build: oracle/Makefile (gcc -O3 -fopenmp -ffp-contract=off -mfma -fno-math-errno).
+ * -ffp-contract=off is load-bearing: Rust never fuses a*b+c, so neither may this file, except
+ * where the reference's matrixmultiply kernels fuse (explicit fmaf/fma calls below).
+ */
+#include "cdclq_oracle.h"
+
+#include <math.h>
+#include <omp.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+#define F16_MIN_NORMAL 6.103515625e-5f /* src/quant.rs:20 */
+#define KC 256                         /* matrixmultiply 0.3.8 S_KC / D_KC */
+
+static int g_mut = 0;
+void orc_set_mutation(int id) { g_mut = id; }
+void orc_set_threads(int nthreads) {
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+}
+
+size_t orc_sizeof_config(void) { return sizeof(orc_config); }
+size_t orc_sizeof_stats(void) { return sizeof(orc_layer_stats); }
+
+/* src/engine.rs:146-167 */
+void orc_default_config(orc_config* c) {
+  memset(c, 0, sizeof(*c));
+  c->bits = 3;
+  c->group = 128;
+  c->block = 128;
+  c->damp = 0.01;
+  c->act_order = 1;
+  c->skeleton_pct = 0.0;
+  c->skeleton_bits = 8;
+  c->mse_grid = 0;
+  c->method = 1;
+  c->refine_frac = 1.0;
+  c->sub_block = 64;
+  c->cd_sweeps = 1;
+  c->passes = 10;
+  c->tol = 1e-3;
+  c->refit_scales = 1;
+  c->row_chunk = 0;
+}
+
+static double now_secs(void) {
+  struct timespec ts;
+  clock_gettime(CLOCK_MONOTONIC, &ts);
+  return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+static void* xcalloc(size_t n, size_t sz) {
+  void* p = calloc(n ? n : 1, sz);
+  if (!p) {
+    fprintf(stderr, "oracle: out of memory (%zu x %zu)\n", n, sz);
+    abort();
+  }
+  return p;
+}
+
+/* Rust f32::min / f32::max: a NaN argument yields the other one. */
+static inline float rs_minf(float a, float b) { return (b < a) ? b : (a != a ? b : a); }
+static inline float rs_maxf(float a, float b) { return (b > a) ? b : (a != a ? b : a); }
+/* Rust f32::clamp(min, max) */
+static inline float rs_clampf(float x, float lo, float hi) {
+  if (x < lo) x = lo;
+  if (x > hi) x = hi;
+  return x;
+}
+
+/* ------------------------------------------------------------------ f16 (src/quant.rs:24-26) */
+/* IEEE binary16 round-to-nearest-even, as `half` 2.4.1 f16::from_f32 (hardware F16C or its
+ * software fallback; both are RNE). */
+static uint16_t f32_to_f16_bits(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  uint32_t sign = (u >> 16) & 0x8000u;
+  uint32_t exp = (u >> 23) & 0xffu;
+  uint32_t man = u & 0x7fffffu;
+  if (exp == 0xffu) return (uint16_t)(man ? (sign | 0x7e00u | (man >> 13)) : (sign | 0x7c00u));
+  int e = (int)exp - 127 + 15;
+  if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (e <= 0) {
+    if (e < -10) return (uint16_t)sign;
+    man |= 0x800000u;
+    int shift = 14 - e;
+    uint32_t hm = man >> shift;
+    uint32_t rem = man & ((1u << shift) - 1u);
+    uint32_t halfway = 1u << (shift - 1);
+    if (rem > halfway || (rem == halfway && (hm & 1u))) hm++;
+    return (uint16_t)(sign | hm);
+  }
+  uint32_t hm = man >> 13;
+  uint32_t rem = man & 0x1fffu;
+  uint32_t h = sign | ((uint32_t)e << 10) | hm;
+  if (rem > 0x1000u || (rem == 0x1000u && (hm & 1u))) h++;
+  return (uint16_t)h;
+}
+
+static float f16_bits_to_f32(uint16_t h) {
+  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  uint32_t exp = ((uint32_t)h >> 10) & 0x1fu;
+  uint32_t man = (uint32_t)h & 0x3ffu;
+  uint32_t u;
+  if (exp == 0) {
+    if (man == 0) {
+      u = sign;
+    } else {
+      int e = -1;
+      do {
+        man <<= 1;
+        e++;
+      } while (!(man & 0x400u));
+      man &= 0x3ffu;
+      u = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+    }
+  } else if (exp == 0x1f) {
+    u = sign | 0x7f800000u | (man << 13);
+  } else {
+    u = sign | ((exp - 15 + 127) << 23) | (man << 13);
+  }
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+float orc_round_f16(float x) {
+  if (g_mut == 3) return x; /* planted: scale not rounded to f16 */
+  return f16_bits_to_f32(f32_to_f16_bits(x));
+}
+
+void orc_round_f16_array(const float* x, float* y, size_t n) {
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i) y[i] = f16_bits_to_f32(f32_to_f16_bits(x[i]));
+}
+
+/* ------------------------------------------------------------------ grid (src/quant.rs:40-95) */
+float orc_quant_code(float x, float scale, float zero, float maxq, uint8_t* code) {
+  float q = rs_clampf(roundf(x / scale) + zero, 0.0f, maxq);
+  if (code) *code = (q == q) ? (uint8_t)q : 0; /* `q as u8` (saturating; NaN -> 0) */
+  return scale * (q - zero);
+}
+
+static void grid_mk(float lo, float hi, float maxq, float* s, float* z) {
+  float scale = orc_round_f16((hi - lo) / maxq);
+  if (scale < F16_MIN_NORMAL) scale = F16_MIN_NORMAL;
+  *s = scale;
+  *z = rs_clampf(roundf(-lo / scale), 0.0f, maxq);
+}
+
+void orc_find_params(const float* vals, size_t len, uint32_t bits, int mse, float* s_out, float* z_out) {
+  float maxq = (float)((1u << bits) - 1u);
+  float xmin = 0.0f, xmax = 0.0f;
+  for (size_t k = 0; k < len; ++k) {
+    xmin = rs_minf(xmin, vals[k]);
+    xmax = rs_maxf(xmax, vals[k]);
+  }
+  if (xmin == 0.0f && xmax == 0.0f) {
+    xmin = -1.0f;
+    xmax = 1.0f;
+  }
+  float bs, bz;
+  grid_mk(xmin, xmax, maxq, &bs, &bz);
+  if (mse) {
+    float best_err = INFINITY;
+    for (int i = 0; i < 24; ++i) {
+      float p = 1.0f - 0.02f * (float)i;
+      float s, z;
+      grid_mk(p * xmin, p * xmax, maxq, &s, &z);
+      float err = 0.0f;
+      for (size_t k = 0; k < len; ++k) {
+        float d = orc_quant_code(vals[k], s, z, maxq, NULL);
+        float e = d - vals[k];
+        err += e * e;
+      }
+      if (err < best_err) {
+        best_err = err;
+        bs = s;
+        bz = z;
+      }
+    }
+  }
+  *s_out = bs;
+  *z_out = bz;
+}
+
+/* ------------------------------------------------------------------ GEMM (src/linalg.rs:56-184) */
+/* matrixmultiply 0.3.8 semantics, restated: for every C element, for each KC-wide panel of k in
+ * order, acc = chain of fma(a_ik, b_kj, acc) from 0 in k order; C = fma(alpha, acc, C') where C' is
+ * beta*C for the first panel (0 when beta == 0; C is not read) and C afterwards. The split of C
+ * across threads (pgemm_*) never changes this per-element order. */
+#define MB 16
+#define NBF 256
+
+#define DEFINE_GEMM(NAME, T, FMA)                                                                                     \
+  static void NAME##_tile(size_t i0, size_t mb, size_t j0, size_t nb, size_t k, T alpha, const T* a, ptrdiff_t rsa,  \
+                          ptrdiff_t csa, const T* b, ptrdiff_t rsb, ptrdiff_t csb, T beta, T* c, ptrdiff_t rsc,       \
+                          ptrdiff_t csc, T* bp, T* cv, T* acc) {                                                      \
+    for (size_t i = 0; i < mb; ++i)                                                                                   \
+      for (size_t j = 0; j < nb; ++j)                                                                                 \
+        cv[i * NBF + j] = (beta == (T)0) ? (T)0 : beta * c[(ptrdiff_t)(i0 + i) * rsc + (ptrdiff_t)(j0 + j) * csc];    \
+    for (size_t k0 = 0; k0 < k; k0 += KC) {                                                                           \
+      size_t kc = (k - k0 < KC) ? (k - k0) : KC;                                                                      \
+      for (size_t kk = 0; kk < kc; ++kk) {                                                                            \
+        const T* brow = b + (ptrdiff_t)(k0 + kk) * rsb + (ptrdiff_t)j0 * csb;                                         \
+        T* dst = bp + kk * NBF;                                                                                       \
+        if (csb == 1)                                                                                                 \
+          memcpy(dst, brow, nb * sizeof(T));                                                                          \
+        else                                                                                                          \
+          for (size_t j = 0; j < nb; ++j) dst[j] = brow[(ptrdiff_t)j * csb];                                          \
+      }                                                                                                               \
+      for (size_t i = 0; i < mb; ++i) {                                                                               \
+        const T* arow = a + (ptrdiff_t)(i0 + i) * rsa + (ptrdiff_t)k0 * csa;                                          \
+        for (size_t j = 0; j < nb; ++j) acc[j] = (T)0;                                                                \
+        for (size_t kk = 0; kk < kc; ++kk) {                                                                          \
+          const T av = arow[(ptrdiff_t)kk * csa];                                                                     \
+          const T* bk = bp + kk * NBF;                                                                                \
+          for (size_t j = 0; j < nb; ++j) acc[j] = FMA(av, bk[j], acc[j]);                                           \
+        }                                                                                                             \
+        T* cr = cv + i * NBF;                                                                                         \
+        for (size_t j = 0; j < nb; ++j) cr[j] = FMA(alpha, acc[j], cr[j]);                                           \
+      }                                                                                                               \
+    }                                                                                                                 \
+    for (size_t i = 0; i < mb; ++i)                                                                                   \
+      for (size_t j = 0; j < nb; ++j) c[(ptrdiff_t)(i0 + i) * rsc + (ptrdiff_t)(j0 + j) * csc] = cv[i * NBF + j];    \
+  }                                                                                                                   \
+  static void NAME##_impl(int par, size_t m, size_t k, size_t n, T alpha, const T* a, ptrdiff_t rsa, ptrdiff_t csa,   \
+                          const T* b, ptrdiff_t rsb, ptrdiff_t csb, T beta, T* c, ptrdiff_t rsc, ptrdiff_t csc) {     \
+    if (m == 0 || n == 0) return;                                                                                     \
+    if (k == 0) {                                                                                                     \
+      if (beta != (T)1)                                                                                               \
+        for (size_t i = 0; i < m; ++i)                                                                                \
+          for (size_t j = 0; j < n; ++j) {                                                                            \
+            T* p = c + (ptrdiff_t)i * rsc + (ptrdiff_t)j * csc;                                                       \
+            *p = (beta == (T)0) ? (T)0 : *p * beta;                                                                   \
+          }                                                                                                           \
+      return;                                                                                                         \
+    }                                                                                                                 \
+    size_t nti = (m + MB - 1) / MB, ntj = (n + NBF - 1) / NBF;                                                        \
+    size_t ntiles = nti * ntj;                                                                                        \
+    int dopar = par && ((double)m * (double)n * (double)k >= 2097152.0) && ntiles > 1;                               \
+    _Pragma("omp parallel if(dopar)") {                                                                               \
+      T* bp = (T*)xcalloc((size_t)KC * NBF, sizeof(T));                                                               \
+      T* cv = (T*)xcalloc((size_t)MB * NBF, sizeof(T));                                                               \
+      T* acc = (T*)xcalloc(NBF, sizeof(T));                                                                           \
+      _Pragma("omp for schedule(dynamic)") for (size_t t = 0; t < ntiles; ++t) {                                      \
+        size_t ti = t / ntj, tj = t % ntj;                                                                            \
+        size_t i0 = ti * MB, j0 = tj * NBF;                                                                           \
+        size_t mb = (m - i0 < MB) ? m - i0 : MB;                                                                      \
+        size_t nb = (n - j0 < NBF) ? n - j0 : NBF;                                                                    \
+        NAME##_tile(i0, mb, j0, nb, k, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc, bp, cv, acc);              \
+      }                                                                                                               \
+      free(bp);                                                                                                       \
+      free(cv);                                                                                                       \
+      free(acc);                                                                                                      \
+    }                                                                                                                 \
+  }
+
+DEFINE_GEMM(sg, float, fmaf)
+DEFINE_GEMM(dg, double, fma)
+
+/* single-thread wrappers = src/linalg.rs:98-99; parallel = pgemm_f32/f64 (src/linalg.rs:183-184) */
+static void sgemm1(size_t m, size_t k, size_t n, float alpha, const float* a, ptrdiff_t rsa, ptrdiff_t csa,
+                   const float* b, ptrdiff_t rsb, ptrdiff_t csb, float beta, float* c, ptrdiff_t rsc, ptrdiff_t csc) {
+  sg_impl(0, m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc);
+}
+static void pgemm_f32(size_t m, size_t k, size_t n, float alpha, const float* a, ptrdiff_t rsa, ptrdiff_t csa,
+                      const float* b, ptrdiff_t rsb, ptrdiff_t csb, float beta, float* c, ptrdiff_t rsc,
+                      ptrdiff_t csc) {
+  sg_impl(1, m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc);
+}
+static void pgemm_f64(size_t m, size_t k, size_t n, double alpha, const double* a, ptrdiff_t rsa, ptrdiff_t csa,
+                      const double* b, ptrdiff_t rsb, ptrdiff_t csb, double beta, double* c, ptrdiff_t rsc,
+                      ptrdiff_t csc) {
+  dg_impl(1, m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc);
+}
+
+void orc_sgemm(size_t m, size_t k, size_t n, float alpha, const float* a, ptrdiff_t rsa, ptrdiff_t csa, const float* b,
+               ptrdiff_t rsb, ptrdiff_t csb, float beta, float* c, ptrdiff_t rsc, ptrdiff_t csc) {
+  pgemm_f32(m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc);
+}
+void orc_dgemm(size_t m, size_t k, size_t n, double alpha, const double* a, ptrdiff_t rsa, ptrdiff_t csa, const double* b,
+               ptrdiff_t rsb, ptrdiff_t csb, double beta, double* c, ptrdiff_t rsc, ptrdiff_t csc) {
+  pgemm_f64(m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc);
+}
+
+/* ------------------------------------------------------------------ Rust `{:e}` for the pivot message */
+static void rust_lower_exp(double d, char* out, size_t len) {
+  /* shortest round-trip digits, then Rust's exponent style ("1.5e-5", "-2e0") */
+  if (d != d) {
+    snprintf(out, len, "NaN");
+    return;
+  }
+  if (isinf(d)) {
+    snprintf(out, len, d < 0 ? "-inf" : "inf");
+    return;
+  }
+  char buf[64];
+  int p;
+  for (p = 0; p < 17; ++p) {
+    snprintf(buf, sizeof buf, "%.*e", p, d);
+    if (strtod(buf, NULL) == d) break;
+  }
+  char* e = strchr(buf, 'e');
+  int ex = atoi(e + 1);
+  *e = 0;
+  snprintf(out, len, "%.40se%d", buf, ex);
+}
+
+/* ------------------------------------------------------------------ Cholesky (src/linalg.rs:200-276) */
+int orc_cholesky_lower(double* a, size_t n, char* err, size_t errlen) {
+  const size_t NBc = 96;
+  size_t k = 0;
+  double* pt = NULL; /* panel transposed (kb x rows_below) for the trailing update */
+  while (k < n) {
+    size_t kb = (n - k < NBc) ? n - k : NBc;
+    size_t kend = k + kb;
+    for (size_t j = k; j < kend; ++j) {
+      double d = a[j * n + j];
+      for (size_t t = k; t < j; ++t) {
+        double v = a[j * n + t];
+        d -= v * v;
+      }
+      if (!(d > 0.0) || !isfinite(d)) {
+        if (err && errlen) {
+          char num[64];
+          rust_lower_exp(d, num, sizeof num);
+          snprintf(err, errlen,
+                   "matrix is not positive definite (pivot %zu = %s); increase --damp or check the Hessian", j, num);
+        }
+        free(pt);
+        return ORC_NOT_PD;
+      }
+      d = sqrt(d);
+      a[j * n + j] = d;
+      for (size_t i = j + 1; i < kend; ++i) {
+        double s = a[i * n + j];
+        for (size_t t = k; t < j; ++t) s -= a[i * n + t] * a[j * n + t];
+        a[i * n + j] = s / d;
+      }
+    }
+    if (kend < n) {
+      size_t rb = n - kend;
+#pragma omp parallel for schedule(static)
+      for (size_t i = kend; i < n; ++i) {
+        double* row = a + i * n;
+        for (size_t j = k; j < kend; ++j) {
+          double s = row[j];
+          for (size_t t = k; t < j; ++t) s -= row[t] * a[j * n + t];
+          row[j] = s / a[j * n + j];
+        }
+      }
+      /* trailing update, lower triangle only: A[i][j] = fma(-1, chain_t P[i][t] P[j][t], A[i][j]) */
+      free(pt);
+      pt = (double*)xcalloc(kb * rb, sizeof(double));
+      for (size_t i = 0; i < rb; ++i)
+        for (size_t t = 0; t < kb; ++t) pt[t * rb + i] = a[(kend + i) * n + k + t];
+      size_t kb_eff = (g_mut == 5 && kend + kb >= n) ? kb - 1 : kb; /* planted: drop one term */
+#pragma omp parallel
+      {
+        double* acc = (double*)xcalloc(rb, sizeof(double));
+#pragma omp for schedule(dynamic, 8)
+        for (size_t i = 0; i < rb; ++i) {
+          size_t ncol = i + 1;
+          for (size_t j = 0; j < ncol; ++j) acc[j] = 0.0;
+          for (size_t t = 0; t < kb_eff; ++t) {
+            const double av = pt[t * rb + i];
+            const double* bt = pt + t * rb;
+            for (size_t j = 0; j < ncol; ++j) acc[j] = fma(av, bt[j], acc[j]);
+          }
+          double* crow = a + (kend + i) * n + kend;
+          for (size_t j = 0; j < ncol; ++j) crow[j] = fma(-1.0, acc[j], crow[j]);
+        }
+        free(acc);
+      }
+    }
+    k = kend;
+  }
+  free(pt);
+  return ORC_OK;
+}
+
+/* ------------------------------------------------------------------ triangular inverse (src/linalg.rs:284-347) */
+void orc_tri_inverse_lower(const double* l, size_t n, double* y) {
+  const size_t NBc = 96;
+  memset(y, 0, n * n * sizeof(double));
+  size_t s = 0;
+  while (s < n) {
+    size_t e = (s + NBc < n) ? s + NBc : n;
+    size_t w = e - s;
+    double* yii = (double*)xcalloc(w * w, sizeof(double));
+    for (size_t c = 0; c < w; ++c) {
+      yii[c * w + c] = 1.0 / l[(s + c) * n + (s + c)];
+      for (size_t i = c + 1; i < w; ++i) {
+        double acc = 0.0;
+        size_t tstart = (g_mut == 8) ? c + 1 : c; /* planted: off-by-one */
+        for (size_t t = tstart; t < i; ++t) acc += l[(s + i) * n + (s + t)] * yii[t * w + c];
+        yii[i * w + c] = -acc / l[(s + i) * n + (s + i)];
+      }
+    }
+    for (size_t i = 0; i < w; ++i)
+      for (size_t j = 0; j <= i; ++j) y[(s + i) * n + (s + j)] = yii[i * w + j];
+    if (s > 0) {
+      double* t = (double*)xcalloc(w * s, sizeof(double));
+      pgemm_f64(w, s, s, 1.0, l + s * n, (ptrdiff_t)n, 1, y, (ptrdiff_t)n, 1, 0.0, t, (ptrdiff_t)s, 1);
+      pgemm_f64(w, w, s, -1.0, yii, (ptrdiff_t)w, 1, t, (ptrdiff_t)s, 1, 0.0, y + s * n, (ptrdiff_t)n, 1);
+      free(t);
+    }
+    free(yii);
+    s = e;
+  }
+}
+
+/* ------------------------------------------------------------------ U (src/linalg.rs:362-375) */
+int orc_upper_chol_of_inverse(const double* h, size_t n, float* u, char* err, size_t errlen) {
+  size_t nn = n * n;
+  double* a = (double*)xcalloc(nn, sizeof(double));
+  for (size_t i = 0; i < nn; ++i) a[i] = h[nn - 1 - i]; /* h.reverse(): flips both axes */
+  int rc = orc_cholesky_lower(a, n, err, errlen);
+  if (rc != ORC_OK) {
+    free(a);
+    return rc;
+  }
+  double* y = (double*)xcalloc(nn, sizeof(double));
+  orc_tri_inverse_lower(a, n, y);
+  free(a);
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i) {
+    float* row = u + i * n;
+    for (size_t j = 0; j < i; ++j) row[j] = 0.0f;
+    for (size_t j = i; j < n; ++j) row[j] = (float)y[(n - 1 - i) * n + (n - 1 - j)];
+  }
+  free(y);
+  return ORC_OK;
+}
+
+/* ------------------------------------------------------------------ Gram (src/linalg.rs:388-418) */
+void orc_gram_accumulate(const float* x, const float* y, size_t t, size_t n, double* h) {
+  const size_t TC = 2048;
+  float* tmp = (float*)xcalloc(n * n, sizeof(float));
+  size_t t0 = 0;
+  while (t0 < t) {
+    size_t tc = (t - t0 < TC) ? t - t0 : TC;
+    if (g_mut == 7 && tc < TC) break; /* planted: drop the ragged last chunk */
+    pgemm_f32(n, tc, n, 1.0f, x + t0 * n, 1, (ptrdiff_t)n, y + t0 * n, (ptrdiff_t)n, 1, 0.0f, tmp, (ptrdiff_t)n, 1);
+#pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < n * n; ++i) h[i] += (double)tmp[i];
+    t0 += tc;
+  }
+  free(tmp);
+}
+
+/* ------------------------------------------------------------------ engine (src/engine.rs) */
+struct orc_cache {
+  int valid;
+  char* hkey;
+  size_t n;
+  uint32_t* perm;
+  float* h32;
+  float* u;
+  double damp_val;
+};
+
+orc_cache* orc_cache_new(void) { return (orc_cache*)xcalloc(1, sizeof(orc_cache)); }
+
+static void cache_clear(orc_cache* c) {
+  free(c->hkey);
+  free(c->perm);
+  free(c->h32);
+  free(c->u);
+  c->hkey = NULL;
+  c->perm = NULL;
+  c->h32 = NULL;
+  c->u = NULL;
+  c->valid = 0;
+}
+
+void orc_cache_free(orc_cache* c) {
+  if (!c) return;
+  cache_clear(c);
+  free(c);
+}
+
+/* src/engine.rs:227-233 */
+static size_t effective_group(const orc_config* cfg, size_t n) { return (cfg->group == 0 || cfg->group >= n) ? n : cfg->group; }
+
+size_t orc_num_groups(const orc_config* cfg, size_t n) {
+  size_t g = effective_group(cfg, n);
+  return (n + g - 1) / g;
+}
+
+/* src/engine.rs:240-258 */
+static int validate(const orc_config* cfg, size_t n, char* err, size_t errlen) {
+  if (cfg->bits < 2 || cfg->bits > 8 || cfg->skeleton_bits < 2 || cfg->skeleton_bits > 8) {
+    snprintf(err, errlen, "bits and skeleton_bits must be in 2..=8");
+    return ORC_INVALID_ARG;
+  }
+  if (cfg->block == 0 || cfg->sub_block == 0) {
+    snprintf(err, errlen, "block and sub_block must be > 0");
+    return ORC_INVALID_ARG;
+  }
+  size_t g = effective_group(cfg, n);
+  if (g < n && cfg->block % g != 0 && g % cfg->block != 0) {
+    snprintf(err, errlen, "group size %zu must divide the block size %zu (or be a multiple of it)", g,
+             (size_t)cfg->block);
+    return ORC_INVALID_ARG;
+  }
+  if (cfg->skeleton_pct > 0.0 && g >= n) {
+    snprintf(err, errlen, "the skeleton needs a finite group size");
+    return ORC_INVALID_ARG;
+  }
+  if (!(cfg->refine_frac >= 0.0 && cfg->refine_frac <= 1.0)) {
+    snprintf(err, errlen, "refine_frac must be in [0, 1]");
+    return ORC_INVALID_ARG;
+  }
+  return ORC_OK;
+}
+
+/* stable merge sort of indices with a comparator (Rust sort_by is stable) */
+typedef int (*idx_cmp)(size_t a, size_t b, const void* ctx);
+static void merge_sort_idx(size_t* v, size_t len, idx_cmp cmp, const void* ctx) {
+  if (len < 2) return;
+  size_t* tmp = (size_t*)xcalloc(len, sizeof(size_t));
+  for (size_t width = 1; width < len; width *= 2) {
+    for (size_t lo = 0; lo < len; lo += 2 * width) {
+      size_t mid = (lo + width < len) ? lo + width : len;
+      size_t hi = (lo + 2 * width < len) ? lo + 2 * width : len;
+      size_t i = lo, j = mid, k = lo;
+      while (i < mid && j < hi) tmp[k++] = (cmp(v[j], v[i], ctx) < 0) ? v[j++] : v[i++];
+      while (i < mid) tmp[k++] = v[i++];
+      while (j < hi) tmp[k++] = v[j++];
+    }
+    memcpy(v, tmp, len * sizeof(size_t));
+  }
+  free(tmp);
+}
+
+/* b.partial_cmp(a) (descending), NaN -> Equal, then a.cmp(b) */
+static int desc_then_index(double ka, double kb, size_t a, size_t b) {
+  if (kb < ka) return -1;
+  if (kb > ka) return 1;
+  return (a < b) ? -1 : (a > b ? 1 : 0);
+}
+
+typedef struct {
+  const double* hdiag;
+  const double* colsq;
+} perm_ctx;
+
+static int cmp_saliency(size_t a, size_t b, const void* c) {
+  const perm_ctx* p = (const perm_ctx*)c;
+  return desc_then_index(p->hdiag[a] * p->colsq[a], p->hdiag[b] * p->colsq[b], a, b);
+}
+static int cmp_hdiag(size_t a, size_t b, const void* c) {
+  const perm_ctx* p = (const perm_ctx*)c;
+  return desc_then_index(p->hdiag[a], p->hdiag[b], a, b);
+}
+
+/* src/engine.rs:271-304 */
+static size_t compute_perm(const double* hdiag, const float* w, size_t d_out, size_t n, size_t g, const orc_config* cfg,
+                           uint32_t* perm) {
+  size_t nskel = 0, np = 0;
+  unsigned char* in_skel = (unsigned char*)xcalloc(n, 1);
+  if (cfg->skeleton_pct > 0.0 && g < n) {
+    size_t full_groups = n / g;
+    double v = round(cfg->skeleton_pct / 100.0 * (double)n / (double)g);
+    size_t want = (v > 0.0) ? (size_t)v : 0;
+    size_t cap = full_groups > 0 ? full_groups - 1 : 0;
+    nskel = want < cap ? want : cap;
+    if (nskel > 0) {
+      double* colsq = (double*)xcalloc(n, sizeof(double));
+      for (size_t r = 0; r < d_out; ++r) {
+        const float* row = w + r * n;
+        for (size_t j = 0; j < n; ++j) colsq[j] += (double)row[j] * (double)row[j];
+      }
+      size_t* idx = (size_t*)xcalloc(n, sizeof(size_t));
+      for (size_t j = 0; j < n; ++j) idx[j] = j;
+      perm_ctx pc = {hdiag, colsq};
+      merge_sort_idx(idx, n, cmp_saliency, &pc);
+      for (size_t t = 0; t < nskel * g; ++t) {
+        in_skel[idx[t]] = 1;
+        perm[np++] = (uint32_t)idx[t];
+      }
+      free(idx);
+      free(colsq);
+    }
+  }
+  size_t* rest = (size_t*)xcalloc(n, sizeof(size_t));
+  size_t nr = 0;
+  for (size_t j = 0; j < n; ++j)
+    if (!in_skel[j]) rest[nr++] = j;
+  if (cfg->act_order) {
+    perm_ctx pc = {hdiag, NULL};
+    merge_sort_idx(rest, nr, cmp_hdiag, &pc);
+  }
+  for (size_t t = 0; t < nr; ++t) perm[np++] = (uint32_t)rest[t];
+  free(rest);
+  free(in_skel);
+  return nskel;
+}
+
+/* src/engine.rs:320-342. Fills cache on success. */
+static int build_prepared(const float* h, size_t n, const uint32_t* perm, const orc_config* cfg, orc_cache* cache,
+                          char* err, size_t errlen) {
+  size_t nn = n * n;
+  double* hp = (double*)xcalloc(nn, sizeof(double));
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i) {
+    size_t pi = perm[i];
+    for (size_t j = 0; j < n; ++j) hp[i * n + j] = (double)h[pi * n + perm[j]];
+  }
+  for (size_t i = 0; i < n; ++i)
+    if (hp[i * n + i] == 0.0) hp[i * n + i] = 1.0;
+  double mean_diag = 0.0;
+  for (size_t i = 0; i < n; ++i) mean_diag += hp[i * n + i];
+  mean_diag /= (double)n;
+  double damp_val = cfg->damp * mean_diag;
+  for (size_t i = 0; i < n; ++i) hp[i * n + i] += damp_val;
+  float* h32 = (float*)xcalloc(nn, sizeof(float));
+  for (size_t i = 0; i < nn; ++i) h32[i] = (float)hp[i];
+  if (g_mut == 6) /* planted: phase-2 metric left undamped */
+    for (size_t i = 0; i < n; ++i) h32[i * n + i] = (float)(hp[i * n + i] - damp_val);
+  float* u = (float*)xcalloc(nn, sizeof(float));
+  int rc = orc_upper_chol_of_inverse(hp, n, u, err, errlen);
+  free(hp);
+  if (rc != ORC_OK) {
+    free(h32);
+    free(u);
+    return rc;
+  }
+  cache->perm = (uint32_t*)xcalloc(n, sizeof(uint32_t));
+  memcpy(cache->perm, perm, n * sizeof(uint32_t));
+  cache->h32 = h32;
+  cache->u = u;
+  cache->damp_val = damp_val;
+  cache->n = n;
+  return ORC_OK;
+}
+
+typedef struct {
+  double loss_gptq, loss_final;
+  size_t sb_total, sb_refined, updates;
+} chunk_stats;
+
+typedef struct {
+  double sum;
+  size_t s;
+} sb_entry;
+
+/* Hessian-optimal scale refit, the `refit_all` closure (src/engine.rs:534-589). */
+static size_t refit_all(size_t rows, size_t n, size_t ng, size_t g, const float* h, const uint8_t* codes, float* scales,
+                        const float* zeros, float* wq, float* e, float* gs, float* hcc, float* uu, float* hu,
+                        double* loss_delta) {
+  size_t changed = 0;
+  for (size_t gi = 0; gi < ng; ++gi) {
+    size_t c0 = gi * g;
+    size_t c1 = (c0 + g < n) ? c0 + g : n;
+    size_t wd = c1 - c0;
+    sgemm1(rows, n, wd, 1.0f, e, (ptrdiff_t)n, 1, h + c0, (ptrdiff_t)n, 1, 0.0f, gs, (ptrdiff_t)wd, 1);
+    for (size_t a = 0; a < wd; ++a) memcpy(hcc + a * wd, h + (c0 + a) * n + c0, wd * sizeof(float));
+    for (size_t r = 0; r < rows; ++r) {
+      float z = zeros[r * ng + gi];
+      for (size_t k = 0; k < wd; ++k) uu[r * wd + k] = (float)codes[r * n + c0 + k] - z;
+    }
+    sgemm1(rows, wd, wd, 1.0f, uu, (ptrdiff_t)wd, 1, hcc, (ptrdiff_t)wd, 1, 0.0f, hu, (ptrdiff_t)wd, 1);
+    for (size_t r = 0; r < rows; ++r) {
+      const float* ur = uu + r * wd;
+      const float* gr = gs + r * wd;
+      const float* hr = hu + r * wd;
+      float num = 0.0f, den = 0.0f;
+      for (size_t k = 0; k < wd; ++k) num += ur[k] * gr[k];
+      for (size_t k = 0; k < wd; ++k) den += ur[k] * hr[k];
+      if (!(den > 1e-30f)) continue;
+      float s_old = scales[r * ng + gi];
+      float s_new = rs_maxf(orc_round_f16(s_old + num / den), F16_MIN_NORMAL);
+      float d = s_new - s_old;
+      float dl32 = (-2.0f * d) * num + (d * d) * den;
+      double dl = (double)dl32;
+      if (dl < 0.0) {
+        scales[r * ng + gi] = s_new;
+        for (size_t k = 0; k < wd; ++k) {
+          size_t j = c0 + k;
+          float ndq = s_new * ur[k];
+          e[r * n + j] += wq[r * n + j] - ndq;
+          wq[r * n + j] = ndq;
+        }
+        *loss_delta += dl;
+        changed++;
+      }
+    }
+  }
+  return changed;
+}
+
+/* src/engine.rs:366-674 */
+static void process_chunk(const float* wt, size_t rows, size_t n, size_t ng, size_t g, const float* u, const float* h,
+                          const uint8_t* gbits, const orc_config* cfg, uint8_t* codes, float* scales, float* zeros,
+                          chunk_stats* out) {
+  size_t bsz = cfg->block;
+  size_t bmin = bsz < n ? bsz : n;
+  float* w = (float*)xcalloc(rows * n, sizeof(float));
+  memcpy(w, wt, rows * n * sizeof(float));
+  float* wq = (float*)xcalloc(rows * n, sizeof(float));
+  double* colloss = (double*)xcalloc(n, sizeof(double));
+  float* w1 = (float*)xcalloc(rows * bmin, sizeof(float));
+  float* err1 = (float*)xcalloc(rows * bmin, sizeof(float));
+  float* tmp = (float*)xcalloc(g < n ? g : n, sizeof(float));
+
+  /* ---- phase 1: blocked GPTQ with lazy batch updates (src/engine.rs:397-473) */
+  size_t i1 = 0;
+  while (i1 < n) {
+    size_t i2 = (i1 + bsz < n) ? i1 + bsz : n;
+    size_t cnt = i2 - i1;
+    for (size_t r = 0; r < rows; ++r) memcpy(w1 + r * cnt, w + r * n + i1, cnt * sizeof(float));
+    for (size_t i = 0; i < cnt; ++i) {
+      size_t j = i1 + i;
+      if (j % g == 0) {
+        size_t gi = j / g;
+        uint32_t bits = gbits[gi];
+        size_t gend = (j + g < n) ? j + g : n;
+        for (size_t r = 0; r < rows; ++r) {
+          for (size_t col = j; col < gend; ++col)
+            tmp[col - j] = (col < i2) ? w1[r * cnt + (col - i1)] : w[r * n + col];
+          float s, z;
+          orc_find_params(tmp, gend - j, bits, cfg->mse_grid, &s, &z);
+          scales[r * ng + gi] = s;
+          zeros[r * ng + gi] = z;
+        }
+      }
+      size_t gi = j / g;
+      float maxq = (float)((1u << gbits[gi]) - 1u);
+      float inv_d = 1.0f / u[j * n + j];
+      const float* urow = u + j * n + j + 1;
+      size_t ulen = i2 - j - 1;
+      double cl = 0.0;
+      for (size_t r = 0; r < rows; ++r) {
+        float wv = w1[r * cnt + i];
+        uint8_t c;
+        float dq = orc_quant_code(wv, scales[r * ng + gi], zeros[r * ng + gi], maxq, &c);
+        codes[r * n + j] = c;
+        wq[r * n + j] = dq;
+        float e = (wv - dq) * inv_d;
+        cl += (double)(e * e);
+        err1[r * cnt + i] = e;
+        if (ulen) {
+          float* row = w1 + r * cnt + i + 1;
+          if (g_mut == 1)
+            for (size_t k = 0; k < ulen; ++k) row[k] += e * urow[k]; /* planted: sign error */
+          else
+            for (size_t k = 0; k < ulen; ++k) row[k] -= e * urow[k];
+        }
+      }
+      colloss[j] = cl;
+    }
+    if (i2 < n) {
+      if (g_mut == 2) /* planted: U transposed in the lazy update */
+        sgemm1(rows, cnt, n - i2, -1.0f, err1, (ptrdiff_t)cnt, 1, u + i2 * n + i1, 1, (ptrdiff_t)n, 1.0f, w + i2,
+               (ptrdiff_t)n, 1);
+      else
+        sgemm1(rows, cnt, n - i2, -1.0f, err1, (ptrdiff_t)cnt, 1, u + i1 * n + i2, (ptrdiff_t)n, 1, 1.0f, w + i2,
+               (ptrdiff_t)n, 1);
+    }
+    i1 = i2;
+  }
+  free(w1);
+  free(err1);
+  free(w);
+  free(tmp);
+
+  double loss_gptq = 0.0;
+  for (size_t j = 0; j < n; ++j) loss_gptq += colloss[j];
+  size_t sbw = cfg->sub_block;
+  size_t n_sb = (n + sbw - 1) / sbw;
+  double loss_delta = 0.0;
+  size_t refined = 0, updates = 0;
+
+  /* ---- phase 2 (src/engine.rs:489-671) */
+  int do_cd = cfg->refine_frac > 0.0 && cfg->cd_sweeps > 0 && cfg->passes > 0;
+  int do_refit = cfg->refit_scales && g <= 1024;
+  if (cfg->method == 1 && (do_cd || do_refit)) {
+    size_t* sel = NULL;
+    size_t nsel = 0;
+    if (do_cd) {
+      sb_entry* sbl = (sb_entry*)xcalloc(n_sb, sizeof(sb_entry));
+      size_t* order = (size_t*)xcalloc(n_sb, sizeof(size_t));
+      double* sums = (double*)xcalloc(n_sb, sizeof(double));
+      for (size_t s = 0; s < n_sb; ++s) {
+        size_t c0 = s * sbw, c1 = ((s + 1) * sbw < n) ? (s + 1) * sbw : n;
+        double acc = 0.0;
+        for (size_t c = c0; c < c1; ++c) acc += colloss[c];
+        sums[s] = acc;
+        order[s] = s;
+      }
+      perm_ctx pc = {sums, NULL};
+      merge_sort_idx(order, n_sb, cmp_hdiag, &pc);
+      double kf = ceil(cfg->refine_frac * (double)n_sb);
+      size_t k = (kf > 0.0) ? (size_t)kf : 0;
+      if (k < 1) k = 1;
+      if (k > n_sb) k = n_sb;
+      sel = (size_t*)xcalloc(k, sizeof(size_t));
+      unsigned char* mark = (unsigned char*)xcalloc(n_sb, 1);
+      for (size_t t = 0; t < k; ++t) mark[order[t]] = 1;
+      for (size_t s = 0; s < n_sb; ++s)
+        if (mark[s]) sel[nsel++] = s;
+      refined = nsel;
+      free(mark);
+      free(sbl);
+      free(order);
+      free(sums);
+    }
+    float* e = (float*)xcalloc(rows * n, sizeof(float));
+    for (size_t i = 0; i < rows * n; ++i) e[i] = wt[i] - wq[i];
+    size_t gcap = g < 1024 ? g : 1024;
+    float* gs = (float*)xcalloc(rows * (sbw > gcap ? sbw : gcap), sizeof(float));
+    float* hss = (float*)xcalloc(sbw * sbw, sizeof(float));
+    float* uu = (float*)xcalloc(do_refit ? rows * gcap : 1, sizeof(float));
+    float* hu = (float*)xcalloc(do_refit ? rows * gcap : 1, sizeof(float));
+    float* hcc = (float*)xcalloc(do_refit ? gcap * gcap : 1, sizeof(float));
+
+    double prev_delta = 0.0;
+    size_t npass = cfg->passes > 0 ? cfg->passes : 1;
+    for (size_t pass = 0; pass < npass; ++pass) {
+      size_t pass_updates = 0;
+      if (do_refit) pass_updates += refit_all(rows, n, ng, g, h, codes, scales, zeros, wq, e, gs, hcc, uu, hu, &loss_delta);
+      if (do_cd) {
+        for (size_t si = 0; si < nsel; ++si) {
+          size_t s = sel[si];
+          size_t c0 = s * sbw;
+          size_t c1 = ((s + 1) * sbw < n) ? (s + 1) * sbw : n;
+          size_t wd = c1 - c0;
+          sgemm1(rows, n, wd, 1.0f, e, (ptrdiff_t)n, 1, h + c0, (ptrdiff_t)n, 1, 0.0f, gs, (ptrdiff_t)wd, 1);
+          for (size_t a = 0; a < wd; ++a) memcpy(hss + a * wd, h + (c0 + a) * n + c0, wd * sizeof(float));
+          for (size_t r = 0; r < rows; ++r) {
+            float* gsr = gs + r * wd;
+            for (size_t sw = 0; sw < cfg->cd_sweeps; ++sw) {
+              int changed = 0;
+              for (size_t jj = 0; jj < wd; ++jj) {
+                size_t j = c0 + jj;
+                size_t gi = j / g;
+                float maxq = (float)((1u << gbits[gi]) - 1u);
+                float sc = scales[r * ng + gi];
+                float z = zeros[r * ng + gi];
+                float hjj = hss[jj * wd + jj];
+                float cur = wq[r * n + j];
+                float target = cur + gsr[jj] / hjj;
+                float q = rs_clampf(roundf(target / sc) + z, 0.0f, maxq);
+                float newdq = sc * (q - z);
+                uint8_t qc = (q == q) ? (uint8_t)q : 0;
+                if (qc != codes[r * n + j]) {
+                  float de = cur - newdq;
+                  float d32 = (2.0f * de) * gsr[jj] + (de * de) * hjj;
+                  if (g_mut == 4) d32 = -d32; /* planted: wrong sign of the closed-form delta */
+                  loss_delta += (double)d32;
+                  const float* hrow = hss + jj * wd;
+                  for (size_t k = 0; k < wd; ++k) gsr[k] += de * hrow[k];
+                  wq[r * n + j] = newdq;
+                  codes[r * n + j] = qc;
+                  e[r * n + j] += de;
+                  pass_updates++;
+                  changed = 1;
+                }
+              }
+              if (!changed) break;
+            }
+          }
+        }
+      }
+      updates += pass_updates;
+      double gain = prev_delta - loss_delta;
+      prev_delta = loss_delta;
+      if (pass_updates == 0 || gain < cfg->tol * (loss_gptq + loss_delta)) break;
+    }
+    if (do_refit) updates += refit_all(rows, n, ng, g, h, codes, scales, zeros, wq, e, gs, hcc, uu, hu, &loss_delta);
+    free(e);
+    free(gs);
+    free(hss);
+    free(uu);
+    free(hu);
+    free(hcc);
+    free(sel);
+  }
+  free(wq);
+  free(colloss);
+  out->loss_gptq = loss_gptq;
+  out->loss_final = loss_gptq + loss_delta;
+  out->sb_total = n_sb;
+  out->sb_refined = refined;
+  out->updates = updates;
+}
+
+/* src/engine.rs:690-799 */
+int orc_quantize_layer(const float* w, size_t d_out, size_t d_in, const float* h, const float* m, const char* hkey,
+                       const orc_config* cfg, size_t nthreads, orc_cache* cache, uint8_t* codes, float* scales,
+                       float* zeros, uint32_t* perm_out, uint8_t* gbits_out, orc_layer_stats* st, char* err,
+                       size_t errlen) {
+  size_t n = d_in;
+  char dummy[8];
+  if (!err || !errlen) {
+    err = dummy;
+    errlen = sizeof dummy;
+  }
+  err[0] = 0;
+  if (n == 0 || d_out == 0) {
+    snprintf(err, errlen, "empty layer (d_out and d_in must be > 0)");
+    return ORC_INVALID_ARG;
+  }
+  int rc = validate(cfg, n, err, errlen);
+  if (rc) return rc;
+  size_t g = effective_group(cfg, n);
+  size_t ng = (n + g - 1) / g;
+  double t0 = now_secs();
+
+  double* hdiag = (double*)xcalloc(n, sizeof(double));
+  for (size_t j = 0; j < n; ++j) hdiag[j] = (double)h[j * n + j];
+  float* w0 = (float*)xcalloc(d_out * n, sizeof(float));
+  memcpy(w0, w, d_out * n * sizeof(float));
+  for (size_t j = 0; j < n; ++j)
+    if (hdiag[j] == 0.0)
+      for (size_t r = 0; r < d_out; ++r) w0[r * n + j] = 0.0f;
+  uint32_t* perm = (uint32_t*)xcalloc(n, sizeof(uint32_t));
+  size_t nskel = compute_perm(hdiag, w0, d_out, n, g, cfg, perm);
+  free(hdiag);
+  int reuse = cache->valid && cache->n == n && strcmp(cache->hkey, hkey ? hkey : "") == 0 &&
+              memcmp(cache->perm, perm, n * sizeof(uint32_t)) == 0;
+  if (!reuse) {
+    cache_clear(cache);
+    rc = build_prepared(h, n, perm, cfg, cache, err, errlen);
+    if (rc) {
+      free(w0);
+      free(perm);
+      return rc;
+    }
+    cache->hkey = strdup(hkey ? hkey : "");
+    cache->valid = 1;
+  }
+  const float* U = cache->u;
+  const float* H32 = cache->h32;
+
+  float* wp = (float*)xcalloc(d_out * n, sizeof(float));
+#pragma omp parallel for schedule(static)
+  for (size_t r = 0; r < d_out; ++r)
+    for (size_t j = 0; j < n; ++j) wp[r * n + j] = w0[r * n + cache->perm[j]];
+  free(w0);
+
+  if (m) {
+    float* mp = (float*)xcalloc(n * n, sizeof(float));
+#pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < n; ++i) {
+      size_t pi = cache->perm[i];
+      for (size_t j = 0; j < n; ++j) mp[i * n + j] = m[pi * n + cache->perm[j]];
+      mp[i * n + i] += (float)cache->damp_val;
+    }
+    float* t1 = (float*)xcalloc(d_out * n, sizeof(float));
+    float* t2 = (float*)xcalloc(d_out * n, sizeof(float));
+    pgemm_f32(d_out, n, n, 1.0f, wp, (ptrdiff_t)n, 1, mp, (ptrdiff_t)n, 1, 0.0f, t1, (ptrdiff_t)n, 1);
+    pgemm_f32(d_out, n, n, 1.0f, t1, (ptrdiff_t)n, 1, U, 1, (ptrdiff_t)n, 0.0f, t2, (ptrdiff_t)n, 1);
+    pgemm_f32(d_out, n, n, 1.0f, t2, (ptrdiff_t)n, 1, U, (ptrdiff_t)n, 1, 0.0f, wp, (ptrdiff_t)n, 1);
+    free(mp);
+    free(t1);
+    free(t2);
+  }
+  double secs_prepare = now_secs() - t0;
+
+  uint8_t* gbits = (uint8_t*)xcalloc(ng, 1);
+  for (size_t gi = 0; gi < ng; ++gi) gbits[gi] = (uint8_t)(gi < nskel ? cfg->skeleton_bits : cfg->bits);
+  size_t nt = nthreads ? nthreads : 1;
+  size_t rc_rows;
+  if (cfg->row_chunk > 0) {
+    rc_rows = cfg->row_chunk;
+  } else {
+    rc_rows = (d_out + nt - 1) / nt;
+    if (rc_rows < 32) rc_rows = 32;
+    if (rc_rows > 256) rc_rows = 256;
+  }
+  if (rc_rows > d_out) rc_rows = d_out;
+  if (rc_rows < 1) rc_rows = 1;
+  size_t nchunks = (d_out + rc_rows - 1) / rc_rows;
+  chunk_stats* cs = (chunk_stats*)xcalloc(nchunks, sizeof(chunk_stats));
+
+  double t1 = now_secs();
+#pragma omp parallel for schedule(dynamic, 1)
+  for (size_t c = 0; c < nchunks; ++c) {
+    size_t r0 = c * rc_rows;
+    size_t rows = (d_out - r0 < rc_rows) ? d_out - r0 : rc_rows;
+    process_chunk(wp + r0 * n, rows, n, ng, g, U, H32, gbits, cfg, codes + r0 * n, scales + r0 * ng, zeros + r0 * ng,
+                  &cs[c]);
+  }
+  double secs_quant = now_secs() - t1;
+
+  memcpy(perm_out, cache->perm, n * sizeof(uint32_t));
+  memcpy(gbits_out, gbits, ng);
+  memset(st, 0, sizeof(*st));
+  for (size_t c = 0; c < nchunks; ++c) {
+    st->loss_gptq += cs[c].loss_gptq;
+    st->loss_final += cs[c].loss_final;
+    st->subblocks_total += cs[c].sb_total;
+    st->subblocks_refined += cs[c].sb_refined;
+    st->code_updates += cs[c].updates;
+  }
+  st->skeleton_groups = nskel;
+  size_t row_bits = 0;
+  for (size_t j = 0; j < n; ++j) row_bits += gbits[j / g];
+  st->bits_codes = (double)row_bits / (double)n;
+  st->bits_total = st->bits_codes + 24.0 / (double)g;
+  st->secs_prepare = secs_prepare;
+  st->secs_quant = secs_quant;
+  free(cs);
+  free(gbits);
+  free(wp);
+  free(perm);
+  return ORC_OK;
+}
+
+double orc_proxy_loss(const float* w_t, const float* w_hat, size_t rows, size_t n, const float* h) {
+  float* e = (float*)xcalloc(rows * n, sizeof(float));
+  float* eh = (float*)xcalloc(rows * n, sizeof(float));
+  for (size_t i = 0; i < rows * n; ++i) e[i] = w_t[i] - w_hat[i];
+  pgemm_f32(rows, n, n, 1.0f, e, (ptrdiff_t)n, 1, h, (ptrdiff_t)n, 1, 0.0f, eh, (ptrdiff_t)n, 1);
+  double s = 0.0;
+  for (size_t i = 0; i < rows * n; ++i) s += (double)e[i] * (double)eh[i];
+  free(e);
+  free(eh);
+  return s;
+}
+
+void orc_rtn_layer(const float* w, size_t d_out, size_t n, const orc_config* cfg, float* out) {
+  size_t g = effective_group(cfg, n);
+  float maxq = (float)((1u << cfg->bits) - 1u);
+#pragma omp parallel for schedule(static)
+  for (size_t r = 0; r < d_out; ++r) {
+    const float* src = w + r * n;
+    float* dst = out + r * n;
+    size_t j = 0;
+    while (j < n) {
+      size_t e = (j + g < n) ? j + g : n;
+      float s, z;
+      orc_find_params(src + j, e - j, cfg->bits, cfg->mse_grid, &s, &z);
+      for (size_t k = j; k < e; ++k) dst[k] = orc_quant_code(src[k], s, z, maxq, NULL);
+      j = e;
+    }
+  }
+}
+
+void orc_dequantize(size_t d_out, size_t n, size_t g, const uint32_t* perm, size_t ng, const uint8_t* codes,
+                    const float* scales, const float* zeros, float* out) {
+  for (size_t r = 0; r < d_out; ++r)
+    for (size_t j = 0; j < n; ++j) {
+      size_t gi = j / g;
+      out[r * n + perm[j]] = scales[r * ng + gi] * ((float)codes[r * n + j] - zeros[r * ng + gi]);
+    }
+}
+
+/* ------------------------------------------------------------------ rng.rs (src/rng.rs:22-57) */
+#define GAMMA 0x9E3779B97F4A7C15ULL
+static inline uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+  return z ^ (z >> 31);
+}
+void orc_rng_new(orc_rng* r, uint64_t seed) {
+  r->s = seed + GAMMA;
+  r->has_spare = 0;
+  r->spare = 0.0f;
+}
+uint64_t orc_rng_next_u64(orc_rng* r) {
+  r->s += GAMMA;
+  return mix64(r->s);
+}
+float orc_rng_uniform(orc_rng* r) { return ((float)(orc_rng_next_u64(r) >> 40) + 0.5f) / (float)(1ULL << 24); }
+float orc_rng_normal(orc_rng* r) {
+  if (r->has_spare) {
+    r->has_spare = 0;
+    return r->spare;
+  }
+  float u1 = orc_rng_uniform(r);
+  float u2 = orc_rng_uniform(r);
+  float rr = sqrtf(-2.0f * logf(u1));
+  float th = (2.0f * 3.14159265358979323846f) * u2;
+  r->spare = rr * sinf(th);
+  r->has_spare = 1;
+  return rr * cosf(th);
+}
+
+/* ------------------------------------------------------------------ synthetic generator */
+/* Counter-based: draw k of stream `seed` is mix64(seed + (k+1)*GAMMA). log and cos(2*pi*u) are
+ * written with +,-,*,/ only, so host and device (both compiled with -ffp-contract=off) produce
+ * the same bits. */
+static inline double u01_at(uint64_t seed, uint64_t k) {
+  uint64_t z = mix64(seed + (k + 1) * GAMMA);
+  return ((double)(z >> 12) + 0.5) * (1.0 / 4503599627370496.0);
+}
+
+double orc_synth_log(double x) {
+  uint64_t b;
+  memcpy(&b, &x, 8);
+  int e = (int)((b >> 52) & 0x7ff) - 1023;
+  uint64_t mb = (b & 0xfffffffffffffULL) | (1023ULL << 52);
+  double mm;
+  memcpy(&mm, &mb, 8);
+  if (mm > 1.4142135623730951) {
+    mm = mm * 0.5;
+    e += 1;
+  }
+  double s = (mm - 1.0) / (mm + 1.0);
+  double s2 = s * s;
+  double p = 0.043478260869565216; /* 1/23 */
+  p = p * s2 + 0.047619047619047616; /* 1/21 */
+  p = p * s2 + 0.05263157894736842;  /* 1/19 */
+  p = p * s2 + 0.058823529411764705; /* 1/17 */
+  p = p * s2 + 0.06666666666666667;  /* 1/15 */
+  p = p * s2 + 0.07692307692307693;  /* 1/13 */
+  p = p * s2 + 0.09090909090909091;  /* 1/11 */
+  p = p * s2 + 0.1111111111111111;   /* 1/9 */
+  p = p * s2 + 0.14285714285714285;  /* 1/7 */
+  p = p * s2 + 0.2;                  /* 1/5 */
+  p = p * s2 + 0.3333333333333333;   /* 1/3 */
+  p = p * s2 + 1.0;
+  return (double)e * 0.6931471805599453 + 2.0 * s * p;
+}
+
+double orc_synth_cos2pi(double u) {
+  double w = u - floor(u + 0.5);
+  if (w < 0.0) w = -w;
+  double sign = 1.0;
+  if (w > 0.25) {
+    w = 0.5 - w;
+    sign = -1.0;
+  }
+  double x = w * 6.283185307179586;
+  double x2 = x * x;
+  double p = 8.896791392450574e-22;   /* 1/22! */
+  p = p * x2 - 4.110317623312165e-19;  /* 1/20! */
+  p = p * x2 + 1.5619206968586225e-16; /* 1/18! */
+  p = p * x2 - 4.779477332387385e-14;  /* 1/16! */
+  p = p * x2 + 1.1470745597729725e-11; /* 1/14! */
+  p = p * x2 - 2.08767569878681e-09;   /* 1/12! */
+  p = p * x2 + 2.755731922398589e-07;  /* 1/10! */
+  p = p * x2 - 2.48015873015873e-05;   /* 1/8! */
+  p = p * x2 + 0.001388888888888889;   /* 1/6! */
+  p = p * x2 - 0.041666666666666664;   /* 1/4! */
+  p = p * x2 + 0.5;                    /* 1/2! */
+  p = 1.0 - p * x2;
+  return sign * p;
+}
+
+float orc_synth_normal_at(uint64_t seed, uint64_t i) {
+  double u1 = u01_at(seed, 2 * i);
+  double u2 = u01_at(seed, 2 * i + 1);
+  double r = sqrt(-2.0 * orc_synth_log(u1));
+  return (float)(r * orc_synth_cos2pi(u2));
+}
+
+void orc_synth_normal(uint64_t seed, uint64_t offset, size_t n, float sigma, float* out) {
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i) out[i] = orc_synth_normal_at(seed, offset + i) * sigma;
+}
+
+void orc_synth_outlier_scales(uint64_t seed, size_t n, double frac, float factor, float* scales) {
+  size_t k = (size_t)round(frac * (double)n);
+  if (k > n) k = n;
+  size_t* idx = (size_t*)xcalloc(n, sizeof(size_t));
+  for (size_t j = 0; j < n; ++j) {
+    idx[j] = j;
+    scales[j] = 1.0f;
+  }
+  for (size_t i = 0; i < k; ++i) {
+    size_t j = i + (size_t)(mix64(seed + (i + 1) * GAMMA) % (uint64_t)(n - i));
+    size_t t = idx[i];
+    idx[i] = idx[j];
+    idx[j] = t;
+  }
+  for (size_t i = 0; i < k; ++i) scales[idx[i]] = factor;
+  free(idx);
+}
+
+void orc_synth_tokens(uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale, float* x) {
+#pragma omp parallel for schedule(static)
+  for (size_t r = 0; r < t; ++r)
+    for (size_t j = 0; j < n; ++j)
+      x[r * n + j] = orc_synth_normal_at(seed, (row0 + r) * (uint64_t)n + j) * (ch_scale ? ch_scale[j] : 1.0f);
+}

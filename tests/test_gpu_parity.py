@@ -1,0 +1,273 @@
+"""GPU parity: the HIP library (through the C ABI) against the CPU oracle on identical inputs.
+
+Bar (from the task's north star): codes, zero points, permutation and group widths bit-exact;
+f16 scales bit-exact; loss_gptq / loss_final and U within 1e-6 relative (they come out
+bit-identical; the tolerance is only the stated bar). Gram accumulation is integer-free f32/f64
+arithmetic in the reference's exact order, so H is compared bit for bit as well.
+"""
+import numpy as np
+import pytest
+
+import cdclq
+import oracle as O
+from problems import damped, fixture_hessians, rand_spd, ref_problem, synth_layer
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-6  # loss / U tolerance from the north star
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = cdclq.Context(0)
+    yield c
+    c.close()
+
+
+def cfgs(**kw):
+    """The same configuration for both sides."""
+    g = cdclq.Config(**{k: (cdclq.Method.Gptq if v == "gptq" else cdclq.Method.Cdcl) if k == "method" else v
+                        for k, v in kw.items()})
+    o = O.config(**kw)
+    return g, o
+
+
+def run_both(ctx, w, h, m=None, nthreads=8, hkey="layer", **kw):
+    gcfg, ocfg = cfgs(**kw)
+    d_out, n = w.shape
+    print(f"[parity] d_out={d_out} n={n} m={'yes' if m is not None else 'no'} cfg={kw}", flush=True)
+    qg, sg = cdclq.quantize_layer(w, d_out, n, h, m, hkey, gcfg, cdclq.PrepCache(ctx=ctx), nthreads=nthreads)
+    ctx.clear_cache()
+    qo = O.quantize_layer(w, h, ocfg, m=m, hkey=hkey, nthreads=nthreads)
+    return qg, sg, qo
+
+
+def assert_same(qg, sg, qo, label=""):
+    so = qo.stats
+    assert np.array_equal(qg.perm, qo.perm), f"{label}: perm differs"
+    assert np.array_equal(qg.gbits, qo.gbits), f"{label}: gbits differ"
+    bad = np.argwhere(qg.codes != qo.codes)
+    if bad.size:
+        r, c = bad[0]
+        raise AssertionError(f"{label}: {len(bad)} code mismatches; first at row {r} col {c}: "
+                             f"gpu {qg.codes[r, c]} oracle {qo.codes[r, c]}; rows affected "
+                             f"{len(np.unique(bad[:, 0]))}")
+    sbad = np.argwhere(qg.scales.view(np.uint32) != qo.scales.view(np.uint32))
+    assert sbad.size == 0, f"{label}: {len(sbad)} scale mismatches, first {sbad[0]}"
+    assert np.array_equal(qg.zeros, qo.zeros), f"{label}: zero points differ"
+    for f in ("loss_gptq", "loss_final"):
+        a, b = getattr(sg, f), so[f]
+        assert abs(a - b) <= REL * max(abs(b), 1e-300), f"{label}: {f} gpu {a!r} oracle {b!r}"
+    for f in ("subblocks_total", "subblocks_refined", "code_updates", "skeleton_groups"):
+        assert getattr(sg, f) == so[f], f"{label}: {f} gpu {getattr(sg, f)} oracle {so[f]}"
+    assert sg.bits_codes == so["bits_codes"] and sg.bits_total == so["bits_total"]
+
+
+# ---------------------------------------------------------------- generator
+def test_synth_generator_matches_host(ctx):
+    n = 1 << 20
+    d = cdclq.DeviceArray(ctx, n, np.float32)
+    ctx.check(cdclq.lib().cdclq_synth_normal_device(ctx.ptr, 12345, 777, n, 0.5, d.ptr))
+    assert np.array_equal(d.download().view(np.uint32), O.synth_normal(12345, n, 0.5, offset=777).view(np.uint32))
+    t, nn = 300, 257
+    cs = O.synth_outlier_scales(5, nn, 0.01, 20.0)
+    x = cdclq.DeviceArray(ctx, (t, nn), np.float32)
+    ctx.check(cdclq.lib().cdclq_synth_tokens_device(ctx.ptr, 99, 11, t, nn, cs.ctypes.data, x.ptr))
+    assert np.array_equal(x.download().view(np.uint32), O.synth_tokens(99, t, nn, cs, row0=11).view(np.uint32))
+
+
+# ---------------------------------------------------------------- H accumulation
+@pytest.mark.parametrize("t,n", [(1, 8), (2047, 64), (2048, 100), (2049, 130), (4100, 96), (5000, 200)])
+@pytest.mark.parametrize("sym", [True, False])
+def test_gram_bitexact(ctx, t, n, sym):
+    rng = np.random.default_rng(t * 31 + n)
+    x = (rng.standard_normal((t, n)) * rng.uniform(0.1, 10, n)).astype(np.float32)
+    y = x if sym else (x + 0.05 * rng.standard_normal((t, n))).astype(np.float32)
+    h0 = rng.standard_normal((n, n))  # accumulate onto a non-symmetric start
+    hg = h0.copy()
+    cdclq.gram_accumulate(x, y, t, n, hg, ctx)
+    ho = O.gram_accumulate(x, None if sym else y, h0.copy())
+    assert np.array_equal(hg.view(np.uint64), ho.view(np.uint64))
+    if sym:
+        d = hg - h0
+        assert np.array_equal(d, d.T)
+
+
+# ---------------------------------------------------------------- U
+@pytest.mark.parametrize("n", [1, 5, 96, 150, 200, 400])
+def test_upper_chol_bitexact(ctx, n):
+    h = rand_spd(n, n + 2)
+    ug = cdclq.upper_chol_of_inverse(h, n, ctx)
+    uo = O.upper_chol_of_inverse(h)
+    assert np.array_equal(np.tril(ug, -1), np.zeros_like(ug))
+    assert np.all(np.diag(ug) > 0)
+    rel = np.abs(ug.astype(np.float64) - uo) / np.maximum(np.abs(uo), 1e-30)
+    assert rel.max() <= REL
+    assert np.array_equal(ug.view(np.uint32), uo.view(np.uint32)), f"{(ug != uo).sum()} U entries differ"
+
+
+def test_upper_chol_fixtures_bitexact(ctx):
+    for name, h in fixture_hessians().items():
+        n = h.shape[0]
+        hd = h.astype(np.float64)
+        hd[np.arange(n), np.arange(n)] += 0.01 * np.mean(np.diag(hd))
+        ug = cdclq.upper_chol_of_inverse(hd, n, ctx)
+        uo = O.upper_chol_of_inverse(hd)
+        assert np.array_equal(ug.view(np.uint32), uo.view(np.uint32)), name
+
+
+def test_not_pd_error_matches_reference_text(ctx):
+    n = 40
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((n, 10))
+    h = a @ a.T  # rank 10 < n, no damping -> non-positive pivot
+    with pytest.raises(cdclq.CdclqError) as eg:
+        cdclq.upper_chol_of_inverse(h, n, ctx)
+    with pytest.raises(O.OracleError) as eo:
+        O.upper_chol_of_inverse(h)
+    assert eg.value.code == cdclq.NOT_PD
+    assert str(eg.value) == str(eo.value)
+    assert "matrix is not positive definite (pivot" in str(eg.value)
+
+
+# ---------------------------------------------------------------- quantize_layer
+def small(**kw):
+    base = dict(bits=3, group=32, block=64, sub_block=16, act_order=False, row_chunk=8)
+    base.update(kw)
+    return base
+
+
+def test_engine_reference_problems(ctx):
+    """The configurations of the reference's own engine tests (src/engine.rs:883-988)."""
+    w, h = ref_problem(24, 96, 400, 11)
+    assert_same(*run_both(ctx, w, h, **small(method="gptq")), label="decomposition")
+    w, h = ref_problem(24, 96, 400, 12)
+    for frac in (0.25, 1.0):
+        assert_same(*run_both(ctx, w, h, **small(method="cdcl", refine_frac=frac, passes=2)), label=f"frac{frac}")
+    w, h = ref_problem(16, 128, 300, 13)
+    assert_same(*run_both(ctx, w, h, **small(act_order=True, skeleton_pct=25.0)), label="skeleton")
+    w, h = ref_problem(16, 64, 300, 14)
+    assert_same(*run_both(ctx, w, h, m=h, **small(method="gptq")), label="asym M=H")
+
+
+@pytest.mark.parametrize("bits,group,block,act,mse", [
+    (4, 128, 128, False, False), (3, 128, 128, True, False), (2, 64, 128, True, True), (8, 32, 64, True, False),
+    (4, 256, 128, False, False), (3, 0, 128, True, False), (4, 16, 128, True, True),
+])
+def test_quantize_variants(ctx, bits, group, block, act, mse):
+    w, x, h, _ = synth_layer(7 + bits, 80, 300, 1200)  # n = 300: ragged last groups
+    assert_same(*run_both(ctx, w, h, bits=bits, group=group, block=block, act_order=act, mse_grid=mse, row_chunk=32,
+                          passes=3), label=f"b{bits} g{group} B{block}")
+
+
+def test_quantize_repair_knobs(ctx):
+    w, x, h, _ = synth_layer(21, 70, 192, 900)
+    for kw in (dict(refine_frac=0.5, cd_sweeps=2), dict(refine_frac=0.0), dict(refit_scales=False, passes=4),
+               dict(passes=0), dict(tol=0.0, passes=5), dict(sub_block=48, passes=2), dict(row_chunk=0)):
+        assert_same(*run_both(ctx, w, h, bits=3, group=64, block=128, row_chunk=kw.pop("row_chunk", 16), **kw),
+                    label=str(kw))
+
+
+def test_quantize_skeleton_and_dead_columns(ctx):
+    w, x, h, _ = synth_layer(33, 64, 256, 800)
+    h = h.copy()
+    for j in (3, 100, 201):  # dead input channels: zero row and column
+        h[j, :] = 0
+        h[:, j] = 0
+    assert_same(*run_both(ctx, w, h, bits=2, group=32, block=64, act_order=True, skeleton_pct=10.0, mse_grid=True,
+                          row_chunk=16), label="skeleton+dead")
+
+
+def test_quantize_fixture_hessians(ctx):
+    for i, (name, h) in enumerate(fixture_hessians().items()):
+        n = h.shape[0]
+        w = O.synth_normal(100 + i, 48 * n, 0.02).reshape(48, n)
+        g = 16 if n % 16 == 0 else 0
+        assert_same(*run_both(ctx, w, h, bits=4, group=g, block=16 if g else 128, act_order=True, row_chunk=16,
+                              passes=3), label=name)
+
+
+def test_quantize_asymmetric_target(ctx):
+    w, x, h, _ = synth_layer(44, 96, 160, 700)
+    xt = (x + O.synth_normal(45, x.size, 0.05).reshape(x.shape)).astype(np.float32)
+    ht = O.gram_accumulate(xt).astype(np.float32)
+    m = O.gram_accumulate(x, xt).astype(np.float32)
+    assert_same(*run_both(ctx, w, ht, m=m, bits=3, group=32, block=32, act_order=True, row_chunk=32, passes=3),
+                label="asym")
+
+
+def test_quantize_config1_full(ctx):
+    """2048x2048, 4096 tokens, INT4 g128 B128, natural order, passes 4, tol 1e-6,
+    with H accumulated on the GPU from the same X (bit-exact) and row_chunk fixed at 64."""
+    n, d_out, t = 2048, 2048, 4096
+    cs = O.synth_outlier_scales(1, n, 0.01, 20.0)
+    x = O.synth_tokens(2, t, n, cs)
+    w = O.synth_normal(3, d_out * n, 0.02).reshape(d_out, n)
+    h64 = np.zeros((n, n))
+    cdclq.gram_accumulate(x, x, t, n, h64, ctx)
+    ho = O.gram_accumulate(x)
+    assert np.array_equal(h64.view(np.uint64), ho.view(np.uint64))
+    h = h64.astype(np.float32)
+    assert_same(*run_both(ctx, w, h, bits=4, group=128, block=128, damp=0.01, act_order=False, passes=4, tol=1e-6,
+                          row_chunk=64), label="config1")
+
+
+def test_prepcache_reuse(ctx):
+    """q/k/v-style reuse: same hkey and act-order perm -> one factorisation (src/engine.rs:718)."""
+    w1, x, h, _ = synth_layer(55, 64, 128, 600)
+    w2 = O.synth_normal(56, 32 * 128, 0.02).reshape(32, 128)
+    gcfg, ocfg = cfgs(bits=4, group=32, block=64, act_order=True, row_chunk=16, passes=2)
+    cache = cdclq.PrepCache(ctx=ctx)
+    ctx.clear_cache()
+    ctx.set_timing(True)
+    ctx.reset_timing()
+    q1, s1 = cdclq.quantize_layer(w1, 64, 128, h, None, "attn", gcfg, cache)
+    q2, s2 = cdclq.quantize_layer(w2, 32, 128, h, None, "attn", gcfg, cache)
+    t = ctx.timing()
+    ctx.set_timing(False)
+    assert t["factor"]["launches"] == 1
+    oc = O.Cache()
+    assert_same(q1, s1, O.quantize_layer(w1, h, ocfg, hkey="attn", cache=oc), "first")
+    assert_same(q2, s2, O.quantize_layer(w2, h, ocfg, hkey="attn", cache=oc), "reused")
+
+
+def test_validation_errors_match_reference(ctx):
+    w, x, h, _ = synth_layer(60, 8, 64, 200)
+    for kw in (dict(bits=9), dict(bits=1), dict(block=0), dict(group=48, block=64), dict(refine_frac=1.5),
+               dict(group=0, skeleton_pct=5.0)):
+        gcfg, ocfg = cfgs(**kw)
+        with pytest.raises(cdclq.CdclqError) as eg:
+            cdclq.quantize_layer(w, 8, 64, h, None, "v", gcfg, cdclq.PrepCache(ctx=ctx))
+        with pytest.raises(O.OracleError) as eo:
+            O.quantize_layer(w, h, ocfg)
+        assert eg.value.code == cdclq.INVALID_ARG
+        assert str(eg.value) == str(eo.value), kw
+
+
+def test_device_entry_point_matches_host(ctx):
+    w, x, h, _ = synth_layer(70, 48, 128, 500)
+    gcfg, _ = cfgs(bits=3, group=32, block=64, act_order=True, row_chunk=16, passes=2)
+    ctx.clear_cache()
+    qh, sh = cdclq.quantize_layer(w, 48, 128, h, None, "k", gcfg, cdclq.PrepCache(ctx=ctx))
+    ctx.clear_cache()
+    dw, dh = cdclq.DeviceArray.from_host(ctx, w), cdclq.DeviceArray.from_host(ctx, h)
+    ng = 4
+    dc = cdclq.DeviceArray(ctx, (48, 128), np.uint8)
+    ds = cdclq.DeviceArray(ctx, (48, ng), np.float32)
+    dz = cdclq.DeviceArray(ctx, (48, ng), np.float32)
+    perm, gbits, sd = cdclq.quantize_layer_device(ctx, dw, 48, 128, dh, None, "k", gcfg, dc, ds, dz)
+    assert np.array_equal(perm, qh.perm) and np.array_equal(gbits, qh.gbits)
+    assert np.array_equal(dc.download(), qh.codes)
+    assert np.array_equal(ds.download(), qh.scales) and np.array_equal(dz.download(), qh.zeros)
+    assert sd.loss_final == sh.loss_final
+
+
+def test_proxy_loss(ctx):
+    w, x, h, _ = synth_layer(80, 40, 96, 400)
+    gcfg, ocfg = cfgs(bits=3, group=32, block=32, act_order=False, row_chunk=8)
+    q, s = cdclq.quantize_layer(w, 40, 96, h, None, "p", gcfg, cdclq.PrepCache(ctx=ctx))
+    hd = damped(h, 0.01)
+    lg = cdclq.proxy_loss(w, q.dequantize(), 40, 96, hd, ctx)
+    lo = O.proxy_loss(w, q.dequantize(), hd)
+    assert abs(lg - lo) <= 1e-9 * abs(lo)
+    assert abs(lg - s.loss_final) / lg < 5e-3  # src/engine.rs:929 bookkeeping bar

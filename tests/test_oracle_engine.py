@@ -1,0 +1,259 @@
+"""Pins for the oracle's engine (src/engine.rs): the reference's own engine tests, an independent
+f64 per-column GPTQ (the algorithm of scripts/ref_gptq_check.py:25-64), the permutation rule as
+re-derived by tests/toy_models.rs:698-741, bits accounting, and planted mistakes that these
+checks must catch."""
+import numpy as np
+import pytest
+
+import oracle as O
+from problems import damped, ref_problem, synth_layer
+
+
+def cfg_small(**kw):
+    """src/engine.rs:883-885"""
+    base = dict(bits=3, group=32, block=64, sub_block=16, act_order=False, row_chunk=8)
+    base.update(kw)
+    return O.config(**base)
+
+
+@pytest.fixture(scope="module")
+def p11():
+    return ref_problem(24, 96, 400, 11)
+
+
+@pytest.fixture(scope="module")
+def p12():
+    return ref_problem(24, 96, 400, 12)
+
+
+def check_decomposition(w, h):
+    """src/engine.rs:890-902: sum eps_j^2 == tr(E H_d E^T), rel < 2e-3."""
+    cfg = cfg_small(method="gptq")
+    q = O.quantize_layer(w, h, cfg)
+    direct = O.proxy_loss(w, q.dequantize(), damped(h, cfg.damp))
+    return abs(direct - q.stats["loss_gptq"]) / direct
+
+
+def test_gptq_loss_decomposition_is_exact(p11):
+    assert check_decomposition(*p11) < 2e-3
+
+
+def check_repair(w, h):
+    """src/engine.rs:907-932. Returns a list of failed conditions."""
+    fails = []
+    cfg = cfg_small(method="gptq")
+    q0 = O.quantize_layer(w, h, cfg)
+    l0 = O.proxy_loss(w, q0.dequantize(), damped(h, cfg.damp))
+    for frac in (0.25, 1.0):
+        c2 = cfg_small(method="cdcl", refine_frac=frac, passes=2)
+        q1 = O.quantize_layer(w, h, c2)
+        s1 = q1.stats
+        l1 = O.proxy_loss(w, q1.dequantize(), damped(h, c2.damp))
+        if not abs(s1["loss_gptq"] - q0.stats["loss_gptq"]) / q0.stats["loss_gptq"] < 1e-6:
+            fails.append("phase1 differs")
+        if not l1 <= l0 * (1 + 1e-6):
+            fails.append("repair increased loss")
+        if not s1["loss_final"] <= s1["loss_gptq"]:
+            fails.append("final > gptq")
+        if not abs(l1 - s1["loss_final"]) / l1 < 5e-3:
+            fails.append("tracked vs direct")
+        if not l1 < l0:
+            fails.append("no improvement")
+    return fails
+
+
+def test_repair_is_monotone_and_bookkeeping_exact(p12):
+    assert check_repair(*p12) == []
+
+
+def test_skeleton_and_act_order_permutation():
+    """src/engine.rs:937-970."""
+    w, h = ref_problem(16, 128, 300, 13)
+    cfg = cfg_small(act_order=True, skeleton_pct=25.0)
+    q = O.quantize_layer(w, h, cfg)
+    assert sorted(q.perm.tolist()) == list(range(128))
+    assert q.stats["skeleton_groups"] == 1
+    assert q.gbits[0] == 8 and np.all(q.gbits[1:] == 3)
+    wd = q.dequantize()
+    first = set(q.perm[:32].tolist())
+    e = (w - wd).astype(np.float64) ** 2
+    mask = np.array([j in first for j in range(128)])
+    assert e[:, mask].sum() / 32 < e[:, ~mask].sum() / (128 - 32) * 0.2
+
+
+def test_asymmetric_target_reduces_to_symmetric_when_m_equals_h():
+    """src/engine.rs:975-988."""
+    w, h = ref_problem(16, 64, 300, 14)
+    cfg = cfg_small(method="gptq")
+    a = O.quantize_layer(w, h, cfg)
+    b = O.quantize_layer(w, h, cfg, m=h)
+    assert (a.codes == b.codes).mean() > 0.97
+    assert abs(a.stats["loss_gptq"] - b.stats["loss_gptq"]) / a.stats["loss_gptq"] < 0.05
+
+
+def textbook_gptq(W0, H0, bits, group, damp):
+    """Independent f64 per-column GPTQ, no lazy batching (scripts/ref_gptq_check.py:25-64)."""
+    rows, n = W0.shape
+    maxq = 2 ** bits - 1
+    H = H0.astype(np.float64).copy()
+    dead = np.diag(H) == 0
+    H[dead, dead] = 1.0
+    W = W0.astype(np.float64).copy()
+    W[:, dead] = 0.0
+    H += damp * np.mean(np.diag(H)) * np.eye(n)
+    U = np.linalg.cholesky(np.linalg.inv(H)).T
+    ng = (n + group - 1) // group
+    codes = np.zeros((rows, n), np.uint8)
+    Wq = np.zeros_like(W)
+    for j in range(n):
+        if j % group == 0:
+            v = W[:, j:j + group]
+            lo = np.minimum(v.min(axis=1), 0.0)
+            hi = np.maximum(v.max(axis=1), 0.0)
+            flat = (lo == 0) & (hi == 0)
+            lo = np.where(flat, -1.0, lo)
+            hi = np.where(flat, 1.0, hi)
+            s = np.maximum(((hi - lo) / maxq).astype(np.float16).astype(np.float64), 6.103515625e-5)
+            z = np.clip(np.round(-lo / s), 0, maxq)
+        q = np.clip(np.round(W[:, j] / s) + z, 0, maxq)
+        dq = s * (q - z)
+        err = (W[:, j] - dq) / U[j, j]
+        codes[:, j] = q.astype(np.uint8)
+        Wq[:, j] = dq
+        W[:, j:] -= np.outer(err, U[j, j:])
+    E = W0.astype(np.float64) * (~dead) - Wq
+    return codes, float(np.sum((E @ H) * E)), H
+
+
+def check_textbook(w, h, bits=3, group=64):
+    """Pass criteria of scripts/ref_gptq_check.py:82: codes >= 99.5% equal, loss rel < 5e-3."""
+    cfg = O.config(bits=bits, group=group, block=128, act_order=False, method="gptq", row_chunk=32)
+    q = O.quantize_layer(w, h, cfg)
+    codes, loss_ref, Hd = textbook_gptq(w, h, bits, group, cfg.damp)
+    wq = q.dequantize().astype(np.float64)
+    dead = np.diag(h) == 0
+    E = w.astype(np.float64) * (~dead) - wq
+    loss = float(np.sum((E @ Hd) * E))
+    return (codes == q.codes).mean(), abs(loss - loss_ref) / loss_ref
+
+
+@pytest.mark.parametrize("bits,group", [(3, 64), (4, 128), (2, 32)])
+def test_against_f64_textbook_gptq(bits, group):
+    w, x, h, _ = synth_layer(90 + bits, 64, 256, 2000)
+    same, rel = check_textbook(w, h, bits, group)
+    assert same > 0.995 and rel < 5e-3, (same, rel)
+
+
+def test_permutation_rule_rederived():
+    """tests/toy_models.rs:698-741: skeleton groups by H_jj * ||W_:j||^2 descending (index
+    tie-break), then the rest by H_jj descending; dead columns are zeroed before the ranking."""
+    w, x, h, _ = synth_layer(5, 40, 256, 600)
+    h = h.copy()
+    h[7, :] = 0
+    h[:, 7] = 0
+    for pct, act in ((0.0, True), (12.5, True), (12.5, False), (0.0, False)):
+        cfg = O.config(bits=3, group=32, block=64, act_order=act, skeleton_pct=pct, row_chunk=40, method="gptq")
+        q = O.quantize_layer(w, h, cfg)
+        hd = np.diag(h).astype(np.float64)
+        w0 = w.astype(np.float64).copy()
+        w0[:, hd == 0] = 0
+        n, g = 256, 32
+        nskel = min(int(np.floor(pct / 100 * n / g + 0.5)), n // g - 1)
+        skel = []
+        if nskel > 0:
+            sal = hd * (w0 ** 2).sum(axis=0)
+            skel = sorted(range(n), key=lambda j: (-sal[j], j))[:nskel * g]
+        rest = [j for j in range(n) if j not in set(skel)]
+        if act:
+            rest = sorted(rest, key=lambda j: (-hd[j], j))
+        assert q.perm.tolist() == skel + rest
+        assert q.stats["skeleton_groups"] == nskel
+
+
+def test_bits_accounting_and_grid_membership():
+    """src/quant.rs:239-250 and tests/toy_models.rs:179-192 (every code lies on its own grid)."""
+    w, x, h, _ = synth_layer(6, 48, 256, 600)
+    cfg = O.config(bits=2, group=32, block=64, act_order=True, skeleton_pct=12.5, skeleton_bits=8, row_chunk=16,
+                   passes=3)
+    q = O.quantize_layer(w, h, cfg)
+    nskel = q.stats["skeleton_groups"]
+    assert q.stats["bits_codes"] == (nskel * 32 * 8 + (256 - nskel * 32) * 2) / 256
+    assert q.stats["bits_total"] == q.stats["bits_codes"] + 24 / 32
+    gi = np.arange(256) // 32
+    maxq = (1 << q.gbits[gi].astype(np.int64)) - 1
+    assert np.all(q.codes <= maxq[None, :])
+    s, z = q.scales[:, gi], q.zeros[:, gi]
+    assert np.all(O.round_f16(q.scales) == q.scales) and np.all(q.scales >= 2.0 ** -14)
+    assert np.all(z == np.round(z)) and np.all((z >= 0) & (z <= maxq[None, :]))
+    dq = s * (q.codes.astype(np.float32) - z)
+    for r in range(0, 48, 7):
+        for j in range(0, 256, 5):
+            c, _ = O.quant_code(float(dq[r, j]), float(s[r, j]), float(z[r, j]), float(maxq[j]))
+            assert c == q.codes[r, j]
+
+
+def test_prepcache_reuse_gives_identical_results():
+    w, x, h, _ = synth_layer(8, 32, 128, 500)
+    cfg = O.config(bits=3, group=32, block=64, act_order=True, row_chunk=16, passes=2)
+    cache = O.Cache()
+    a = O.quantize_layer(w, h, cfg, hkey="qkv", cache=cache)
+    b = O.quantize_layer(w, h, cfg, hkey="qkv", cache=cache)
+    assert np.array_equal(a.codes, b.codes) and a.stats["loss_final"] == b.stats["loss_final"]
+
+
+def test_validation_messages():
+    """src/engine.rs:240-258 (exact text)."""
+    w, x, h, _ = synth_layer(9, 4, 64, 100)
+    cases = {
+        "bits and skeleton_bits must be in 2..=8": dict(bits=9),
+        "block and sub_block must be > 0": dict(sub_block=0),
+        "group size 48 must divide the block size 64 (or be a multiple of it)": dict(group=48, block=64),
+        "the skeleton needs a finite group size": dict(group=0, skeleton_pct=1.0),
+        "refine_frac must be in [0, 1]": dict(refine_frac=-0.1),
+    }
+    for msg, kw in cases.items():
+        with pytest.raises(O.OracleError) as e:
+            O.quantize_layer(w, h, O.config(**kw))
+        assert str(e.value) == msg
+
+
+# ---------------------------------------------------------------- planted mistakes
+def _caught(mid):
+    """Run the pinning checks with mutation `mid` planted in the oracle; True if any check fails."""
+    w11, h11 = ref_problem(24, 96, 400, 11)
+    w12, h12 = ref_problem(24, 96, 400, 12)
+    wt, _, ht, _ = synth_layer(93, 64, 256, 2000)
+    with O.mutation(mid):
+        if check_decomposition(w11, h11) >= 2e-3:
+            return True
+        if check_repair(w12, h12):
+            return True
+        same, rel = check_textbook(wt, ht)
+        if not (same > 0.995 and rel < 5e-3):
+            return True
+        hh = ht.astype(np.float64) + np.eye(256)
+        u = O.upper_chol_of_inverse(hh).astype(np.float64)
+        if np.abs(u.T @ u @ hh - np.eye(256)).max() >= 5e-4:
+            return True
+        x = np.ones((2049, 1), np.float32)
+        x[0, 0] = 4096.0
+        if O.gram_accumulate(x)[0, 0] != float(np.float32(2.0 ** 24 + 7 * 256)) + 1:
+            return True
+        v = ((np.arange(64, dtype=np.float32) - 20) * np.float32(0.013)).astype(np.float32)
+        s, _ = O.find_params(v, 3, False)
+        if np.float32(s) != np.float32(np.float16(s)):
+            return True
+    return False
+
+
+@pytest.mark.parametrize("mid,what", [
+    (1, "sign of the in-block compensation"), (2, "U transposed in the lazy GEMM"), (3, "scale not f16-rounded"),
+    (4, "sign of the CD loss delta"), (5, "one term dropped from the Cholesky update"),
+    (6, "undamped phase-2 metric"), (7, "ragged last token chunk dropped"), (8, "off-by-one in the inverse"),
+])
+def test_planted_mistakes_are_caught(mid, what):
+    assert _caught(mid), what
+
+
+def test_no_mutation_passes_all_checks():
+    assert not _caught(0)
