@@ -87,6 +87,8 @@ def lib() -> C.CDLL:
         "cdclq_quantize_layer_device": ([vp, vp, sz, sz, vp, vp, C.c_char_p, cfgp, sz, vp, vp, vp, vp, vp, stp], i32),
         "cdclq_gram_accumulate": ([vp, vp, vp, sz, sz, vp], i32),
         "cdclq_gram_accumulate_device": ([vp, vp, vp, sz, sz, vp], i32),
+        "cdclq_gram_accumulate_batch_device": ([vp, i32, C.POINTER(vp), C.POINTER(vp), C.POINTER(sz), C.POINTER(sz),
+                                                C.POINTER(vp)], i32),
         "cdclq_upper_chol_of_inverse": ([vp, vp, sz, vp], i32),
         "cdclq_upper_chol_of_inverse_device": ([vp, vp, sz, vp], i32),
         "cdclq_proxy_loss": ([vp, vp, vp, sz, sz, vp, C.POINTER(C.c_double)], i32),
@@ -120,7 +122,7 @@ def exported_symbols() -> list[str]:
         "cdclq_abi_version", "cdclq_sizeof_config", "cdclq_sizeof_stats", "cdclq_default_config",
         "cdclq_num_groups", "cdclq_ctx_create", "cdclq_ctx_destroy", "cdclq_last_error", "cdclq_ctx_clear_cache",
         "cdclq_quantize_layer", "cdclq_quantize_layer_device", "cdclq_gram_accumulate",
-        "cdclq_gram_accumulate_device", "cdclq_upper_chol_of_inverse", "cdclq_upper_chol_of_inverse_device",
+        "cdclq_gram_accumulate_device", "cdclq_gram_accumulate_batch_device", "cdclq_upper_chol_of_inverse", "cdclq_upper_chol_of_inverse_device",
         "cdclq_proxy_loss", "cdclq_device_alloc", "cdclq_device_free", "cdclq_memcpy_h2d", "cdclq_memcpy_d2h",
         "cdclq_memset_device", "cdclq_synth_normal_device", "cdclq_synth_outlier_scales", "cdclq_synth_tokens_device", "cdclq_f64_to_f32_device",
         "cdclq_ctx_set_timing", "cdclq_ctx_reset_timing", "cdclq_ctx_get_timing",
@@ -380,6 +382,14 @@ def gram_accumulate(x, y, t: int, n: int, h: np.ndarray, ctx: Context) -> np.nda
     assert h.dtype == np.float64 and h.shape == (n, n) and h.flags.c_contiguous
     ctx.check(lib().cdclq_gram_accumulate(ctx.ptr, x.ctypes.data, y.ctypes.data, t, n, h.ctypes.data))
     return h
+
+
+def gram_accumulate_batch_device(ctx: Context, xs, ys, ts, ns, hs):
+    """Several device-resident accumulations hs[i] += xs[i]^T ys[i] in one launch."""
+    k = len(xs)
+    arr = lambda v: (C.c_void_p * k)(*[a.ptr.value for a in v])
+    ctx.check(lib().cdclq_gram_accumulate_batch_device(ctx.ptr, k, arr(xs), arr(ys), (C.c_size_t * k)(*ts),
+                                                        (C.c_size_t * k)(*ns), arr(hs)))
 
 
 def upper_chol_of_inverse(h64, n: int, ctx: Context) -> np.ndarray:

@@ -62,9 +62,8 @@ struct cdclq_ctx {
   // workspace (grow-only)
   DevBuf w_in, h_in, m_in, x_in, y_in, h64_in, u_out, codes_o, scales_o, zeros_o;
   DevBuf wp, wwork, wq, ebuf, gbits_d, perm_d, deadp_d, dead_d, diag_d, colsq_d, invd, colloss_d;
-  DevBuf G, part, dlog, dcnt, active_d, sel_d, ld_d, upd_d, mp, t1, t2, a64, y64, tbuf, tpart, status_d, tiles_d,
-      proxy_p, cs_d;
-  int tiles_n = -1, tiles_sym = -1, tiles_count = 0;
+  DevBuf G, part, rlog, rcnt, clog, ccnt, active_d, sel_d, ld_d, upd_d, mp, t1, t2, a64, y64, tbuf, tpart, status_d,
+      tiles_d, proxy_p, cs_d;
   // one-entry PrepCache (src/engine.rs:207-223): key, perm, damping and the device factors
   bool cache_valid = false;
   std::string cache_key;
@@ -464,9 +463,18 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
     const int wdmax = std::max(do_cd ? sbw : 1, do_refit ? g : 1);
     CK(ensure(ctx, ctx->G, (size_t)d_out * wdmax * 4));
     CK(ensure(ctx, ctx->part, gemm_partials_elems(d_out, wdmax, n) * 4));
+    // Per-pass logs of accepted deltas (folded into the chunk losses in the reference's order).
     const int cap = std::max(1, do_cd ? sbw * (int)cfg->cd_sweeps : 1);
-    CK(ensure(ctx, ctx->dlog, (size_t)d_out * cap * 8));
-    CK(ensure(ctx, ctx->dcnt, (size_t)d_out * 4));
+    CK(ensure(ctx, ctx->rlog, (size_t)ng * d_out * 8));
+    CK(ensure(ctx, ctx->rcnt, (size_t)ng * d_out * 4));
+    if (do_cd) {
+      CK(ensure(ctx, ctx->clog, (size_t)n_sb * d_out * cap * 8));
+      CK(ensure(ctx, ctx->ccnt, (size_t)n_sb * d_out * 4));
+    }
+    double* rlog = P<double>(ctx->rlog);
+    uint32_t* rcnt = P<uint32_t>(ctx->rcnt);
+    double* clog = do_cd ? P<double>(ctx->clog) : nullptr;
+    uint32_t* ccnt = do_cd ? P<uint32_t>(ctx->ccnt) : nullptr;
     CK(ensure(ctx, ctx->active_d, (size_t)nchunks));
     CK(ensure(ctx, ctx->ld_d, (size_t)nchunks * 8));
     CK(ensure(ctx, ctx->upd_d, (size_t)nchunks * 8));
@@ -476,13 +484,12 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
     std::vector<double> prev(nchunks, 0.0);
     std::vector<uint64_t> upd(nchunks);
     auto refit_all = [&]() -> int {
+      HIPCK(hipMemsetAsync(rcnt, 0, (size_t)ng * d_out * 4, st));
       for (int gi = 0; gi < ng; ++gi) {
         const int c0 = gi * g, wd = std::min(c0 + g, n) - c0;
         CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32));
         HIPCK(refit_group(st, d_out, n, ng, g, gi, rc, P<float>(ctx->G), H32, codes, scales, zeros, wq, eb,
-                          P<uint8_t>(ctx->active_d), P<double>(ctx->dlog), P<uint32_t>(ctx->dcnt), cap));
-        HIPCK(chunk_accum(st, d_out, rc, nchunks, cap, P<double>(ctx->dlog), P<uint32_t>(ctx->dcnt),
-                          P<uint8_t>(ctx->active_d), P<double>(ctx->ld_d), P<uint64_t>(ctx->upd_d)));
+                          P<uint8_t>(ctx->active_d), rlog + (size_t)gi * d_out, rcnt + (size_t)gi * d_out));
       }
       return CDCLQ_OK;
     };
@@ -491,6 +498,7 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
       HIPCK(hipMemsetAsync(ctx->upd_d.p, 0, (size_t)nchunks * 8, st));
       if (do_refit) CK(refit_all());
       if (do_cd) {
+        HIPCK(hipMemsetAsync(ccnt, 0, (size_t)n_sb * d_out * 4, st));
         for (int s = 0; s < n_sb; ++s) {
           bool any = false;
           for (int c = 0; c < nchunks && !any; ++c) any = act[c] && sel[(size_t)c * n_sb + s];
@@ -499,11 +507,11 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
           CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32));
           HIPCK(cd_subblock(st, d_out, n, ng, g, c0, wd, s, n_sb, rc, (int)cfg->cd_sweeps, P<float>(ctx->G), H32,
                             P<uint8_t>(ctx->gbits_d), scales, zeros, codes, wq, eb, P<uint8_t>(ctx->active_d),
-                            P<uint8_t>(ctx->sel_d), P<double>(ctx->dlog), P<uint32_t>(ctx->dcnt), cap));
-          HIPCK(chunk_accum(st, d_out, rc, nchunks, cap, P<double>(ctx->dlog), P<uint32_t>(ctx->dcnt),
-                            P<uint8_t>(ctx->active_d), P<double>(ctx->ld_d), P<uint64_t>(ctx->upd_d)));
+                            P<uint8_t>(ctx->sel_d), clog + (size_t)s * d_out * cap, ccnt + (size_t)s * d_out, cap));
         }
       }
+      HIPCK(pass_accum(st, d_out, rc, nchunks, do_refit ? ng : 0, rlog, rcnt, do_cd ? n_sb : 0, cap, clog, ccnt,
+                       P<uint8_t>(ctx->active_d), P<double>(ctx->ld_d), P<uint64_t>(ctx->upd_d)));
       HIPCK(hipMemcpyAsync(ld.data(), ctx->ld_d.p, (size_t)nchunks * 8, hipMemcpyDeviceToHost, st));
       HIPCK(hipMemcpyAsync(upd.data(), ctx->upd_d.p, (size_t)nchunks * 8, hipMemcpyDeviceToHost, st));
       HIPCK(hipStreamSynchronize(st));
@@ -526,6 +534,8 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
       HIPCK(hipMemcpyAsync(ctx->active_d.p, act.data(), nchunks, hipMemcpyHostToDevice, st));
       HIPCK(hipMemsetAsync(ctx->upd_d.p, 0, (size_t)nchunks * 8, st));
       CK(refit_all());
+      HIPCK(pass_accum(st, d_out, rc, nchunks, ng, rlog, rcnt, 0, cap, clog, ccnt, P<uint8_t>(ctx->active_d),
+                       P<double>(ctx->ld_d), P<uint64_t>(ctx->upd_d)));
       HIPCK(hipMemcpyAsync(ld.data(), ctx->ld_d.p, (size_t)nchunks * 8, hipMemcpyDeviceToHost, st));
       HIPCK(hipMemcpyAsync(upd.data(), ctx->upd_d.p, (size_t)nchunks * 8, hipMemcpyDeviceToHost, st));
       HIPCK(hipStreamSynchronize(st));
@@ -558,27 +568,67 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
   return CDCLQ_OK;
 }
 
-int gram_device(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h) {
-  if (!x || !y || !h) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
-  if (n == 0 || t == 0) return CDCLQ_OK;
-  if (n > 65536 || t > ((size_t)1 << 31) - 4096)
-    return fail(ctx, CDCLQ_INVALID_ARG, "gram_accumulate: n <= 65536 and t < 2^31 in this build");
+// One launch of the matrix-core Gram kernel over several (X, Y, H) jobs (src/linalg.rs:388-418).
+int gram_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const float* const* ys, const size_t* ts,
+                      const size_t* ns, double* const* hs) {
+  if (count <= 0) return CDCLQ_OK;
+  if (!xs || !ys || !ts || !ns || !hs) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
   HIPCK(hipSetDevice(ctx->device));
-  const bool sym = (x == y);
-  if (ctx->tiles_n != (int)n || ctx->tiles_sym != (int)sym) {
-    std::vector<int2> v = gram_tiles((int)n, sym);
-    CK(ensure(ctx, ctx->tiles_d, v.size() * sizeof(int2)));
-    HIPCK(hipMemcpy(ctx->tiles_d.p, v.data(), v.size() * sizeof(int2), hipMemcpyHostToDevice));
-    ctx->tiles_n = (int)n;
-    ctx->tiles_sym = (int)sym;
-    ctx->tiles_count = (int)v.size();
+  hipStream_t st = ctx->st;
+  std::vector<GramJob> jobs;
+  std::vector<int> syms;
+  bool vec4 = true;
+  for (int i = 0; i < count; ++i) {
+    if (!xs[i] || !ys[i] || !hs[i]) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+    if (ns[i] == 0 || ts[i] == 0) continue;
+    if (ns[i] > 65536 || ts[i] > ((size_t)1 << 31) - 4096)
+      return fail(ctx, CDCLQ_INVALID_ARG, "gram_accumulate: n <= 65536 and t < 2^31 in this build");
+    jobs.push_back(GramJob{xs[i], ys[i], hs[i], (int)ns[i], (int)ts[i]});
+    vec4 = vec4 && (ns[i] % 4 == 0) && ((uintptr_t)xs[i] % 16 == 0) && ((uintptr_t)ys[i] % 16 == 0);
   }
+  if (jobs.empty()) return CDCLQ_OK;
+  // Mirrored (upper-triangle-only) tiles need Y == X and a bitwise-symmetric incoming H.
+  CK(ensure(ctx, ctx->status_d, 16 * (jobs.size() + 1)));
+  HIPCK(hipMemsetAsync(ctx->status_d.p, 0, 16 * (jobs.size() + 1), st));
+  for (size_t i = 0; i < jobs.size(); ++i)
+    if (jobs[i].x == jobs[i].y) HIPCK(sym_check(st, jobs[i].n, jobs[i].h, P<int>(ctx->status_d) + 4 * i));
+  std::vector<int> flags(4 * jobs.size());
+  HIPCK(hipMemcpyAsync(flags.data(), ctx->status_d.p, flags.size() * 4, hipMemcpyDeviceToHost, st));
+  HIPCK(hipStreamSynchronize(st));
+  std::vector<int4> tiles;
+  for (size_t i = 0; i < jobs.size(); ++i)
+    gram_mfma_tiles((int)i, jobs[i].n, jobs[i].x == jobs[i].y && flags[4 * i] == 0, tiles);
+  // XCD-aware order: workgroup w runs on XCD w % 8, so give each XCD a contiguous run of tiles
+  // (neighbouring tiles share X stripes in that XCD's L2).
+  {
+    const size_t nx = 8, m = tiles.size();
+    std::vector<int4> ord(m);
+    const size_t per = (m + nx - 1) / nx;
+    size_t w = 0;
+    for (size_t k = 0; k < per; ++k)
+      for (size_t x = 0; x < nx; ++x) {
+        const size_t src = x * per + k;
+        if (src < m) ord[w++] = tiles[src];
+      }
+    tiles.swap(ord);
+  }
+  CK(ensure(ctx, ctx->tiles_d, tiles.size() * sizeof(int4) + jobs.size() * sizeof(GramJob) + 64));
+  char* base = P<char>(ctx->tiles_d);
+  GramJob* djobs = reinterpret_cast<GramJob*>(base);
+  int4* dtiles = reinterpret_cast<int4*>(base + ((jobs.size() * sizeof(GramJob) + 63) / 64) * 64);
+  HIPCK(hipMemcpyAsync(djobs, jobs.data(), jobs.size() * sizeof(GramJob), hipMemcpyHostToDevice, st));
+  HIPCK(hipMemcpyAsync(dtiles, tiles.data(), tiles.size() * sizeof(int4), hipMemcpyHostToDevice, st));
   {
     PhaseScope ps(ctx, CDCLQ_PHASE_GRAM);
-    HIPCK(gram_accumulate(ctx->st, (int)t, (int)n, x, y, h, sym, P<int2>(ctx->tiles_d), ctx->tiles_count));
+    HIPCK(gram_mfma(st, djobs, dtiles, (int)tiles.size(), vec4));
   }
-  HIPCK(hipStreamSynchronize(ctx->st));
+  HIPCK(hipStreamSynchronize(st));
   return CDCLQ_OK;
+}
+
+int gram_device(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h) {
+  if (!x || !y || !h) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+  return gram_batch_device(ctx, 1, &x, &y, &t, &n, &h);
 }
 
 int uchol_device(cdclq_ctx* ctx, const double* h, size_t n_, float* u) {
@@ -659,7 +709,7 @@ void cdclq_ctx_destroy(cdclq_ctx* ctx) {
   DevBuf* bufs[] = {&ctx->w_in, &ctx->h_in, &ctx->m_in, &ctx->x_in, &ctx->y_in, &ctx->h64_in, &ctx->u_out,
                     &ctx->codes_o, &ctx->scales_o, &ctx->zeros_o, &ctx->wp, &ctx->wwork, &ctx->wq, &ctx->ebuf,
                     &ctx->gbits_d, &ctx->perm_d, &ctx->deadp_d, &ctx->dead_d, &ctx->diag_d, &ctx->colsq_d,
-                    &ctx->invd, &ctx->colloss_d, &ctx->G, &ctx->part, &ctx->dlog, &ctx->dcnt, &ctx->active_d,
+                    &ctx->invd, &ctx->colloss_d, &ctx->G, &ctx->part, &ctx->rlog, &ctx->rcnt, &ctx->clog, &ctx->ccnt, &ctx->active_d,
                     &ctx->sel_d, &ctx->ld_d, &ctx->upd_d, &ctx->mp, &ctx->t1, &ctx->t2, &ctx->a64, &ctx->y64,
                     &ctx->tbuf, &ctx->tpart, &ctx->status_d, &ctx->tiles_d, &ctx->proxy_p, &ctx->cs_d,
                     &ctx->cache_u, &ctx->cache_h32};
@@ -725,6 +775,13 @@ int cdclq_gram_accumulate_device(cdclq_ctx* ctx, const float* x, const float* y,
   if (!ctx) return CDCLQ_INVALID_ARG;
   ctx->err.clear();
   return gram_device(ctx, x, y, t, n, h);
+}
+
+int cdclq_gram_accumulate_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const float* const* ys,
+                                       const size_t* ts, const size_t* ns, double* const* hs) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  return gram_batch_device(ctx, count, xs, ys, ts, ns, hs);
 }
 
 int cdclq_gram_accumulate(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h) {

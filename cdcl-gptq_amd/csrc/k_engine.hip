@@ -235,7 +235,8 @@ __global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, i
                                                const uint8_t* __restrict__ codes, float* __restrict__ scales,
                                                const float* __restrict__ zeros, float* __restrict__ wq,
                                                float* __restrict__ e, const uint8_t* __restrict__ active,
-                                               double* __restrict__ dlog, uint32_t* __restrict__ dcnt, int cap) {
+                                               double* __restrict__ dlog, uint32_t* __restrict__ dcnt) {
+  // this step's log: one slot per row (dlog/dcnt point at the slot of group gi)
   const int lane = threadIdx.x & 63;
   const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
   if (r >= rows) return;
@@ -296,7 +297,7 @@ __global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, i
     if ((double)dl32 < 0.0) {
       if (lane == 0) {
         scales[(long)r * ng + gi] = s_new;
-        dlog[(long)r * cap] = (double)dl32;
+        dlog[r] = (double)dl32;
       }
 #pragma unroll
       for (int s = 0; s < NPL; ++s) {
@@ -399,26 +400,60 @@ __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int 
   if (lane == 0) dcnt[r] = moves;
 }
 
-// Per-chunk loss bookkeeping in the reference's order: rows ascending, each row's accepted
-// deltas in the order they were made (src/engine.rs:583, :640).
-__global__ __launch_bounds__(64) void k_chunk_accum(int rows, int rc, int nchunks, int cap,
-                                                    const double* __restrict__ dlog,
-                                                    const uint32_t* __restrict__ dcnt,
-                                                    const uint8_t* __restrict__ active, double* __restrict__ ld,
-                                                    uint64_t* __restrict__ upd) {
-  const int c = blockIdx.x * 64 + threadIdx.x;
-  if (c >= nchunks || !active[c]) return;
+// Per-chunk loss bookkeeping of one pass, in the reference's order (src/engine.rs:583, :640):
+// steps in execution order (refit groups, then CD sub-blocks), within a step rows ascending,
+// within a row its accepted deltas in the order they were made. One wave per chunk: the wave
+// gathers 64 rows' logged deltas into LDS in that order, then folds them sequentially in f64.
+constexpr int ACC_LDS = 4096;
+__global__ __launch_bounds__(64) void k_pass_accum(int rows, int rc, int nref, const double* __restrict__ rlog,
+                                                   const uint32_t* __restrict__ rcnt, int ncd, int cap,
+                                                   const double* __restrict__ clog,
+                                                   const uint32_t* __restrict__ ccnt,
+                                                   const uint8_t* __restrict__ active, double* __restrict__ ld,
+                                                   uint64_t* __restrict__ upd) {
+  __shared__ double vals[ACC_LDS];
+  const int c = blockIdx.x;
+  if (!active[c]) return;
+  const int lane = threadIdx.x;
+  const int r0 = c * rc, r1 = min(rows, r0 + rc);
   double acc = ld[c];
   uint64_t u = upd[c];
-  const int r1 = min(rows, (c + 1) * rc);
-  for (int r = c * rc; r < r1; ++r) {
-    const uint32_t k = dcnt[r];
-    const double* p = dlog + (long)r * cap;
-    for (uint32_t q = 0; q < k; ++q) acc = acc + p[q];
-    u += k;
+  for (int step = 0; step < nref + ncd; ++step) {
+    const bool refit = step < nref;
+    const long sbase = refit ? (long)step * rows : (long)(step - nref) * rows;
+    const uint32_t* cnt = refit ? rcnt : ccnt;
+    for (int base = r0; base < r1; base += 64) {
+      const int r = base + lane;
+      const uint32_t k = (r < r1) ? cnt[sbase + r] : 0u;
+      // exclusive prefix sum of k over the lanes
+      uint32_t incl = k;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += v;
+      }
+      const uint32_t total = __shfl(incl, 63, 64);
+      if (total == 0) continue;
+      const uint32_t off = incl - k;
+      u += total;
+      for (uint32_t done = 0; done < total; done += ACC_LDS) {
+        // rows whose deltas fall in [done, done + ACC_LDS) copy them in order
+        for (uint32_t q = 0; q < k; ++q) {
+          const uint32_t pos = off + q;
+          if (pos >= done && pos < done + ACC_LDS)
+            vals[pos - done] = refit ? rlog[sbase + r] : clog[(sbase + r) * cap + q];
+        }
+        __syncthreads();
+        const uint32_t m = min((uint32_t)ACC_LDS, total - done);
+        for (uint32_t i = 0; i < m; ++i) acc = acc + vals[i];
+        __syncthreads();
+      }
+    }
   }
-  ld[c] = acc;
-  upd[c] = u;
+  if (lane == 0) {
+    ld[c] = acc;
+    upd[c] = u;
+  }
 }
 
 // ---------------------------------------------------------------- synthetic inputs
@@ -526,13 +561,13 @@ hipError_t sub_f32(hipStream_t st, size_t count, const float* a, const float* b,
 
 hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, int rc, const float* G, const float* h32,
                        const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
-                       const uint8_t* active, double* dlog, uint32_t* dcnt, int cap) {
+                       const uint8_t* active, double* dlog, uint32_t* dcnt) {
   const int wd = std::min(gi * g + g, n) - gi * g;
   const dim3 grid((rows + 3) / 4), blk(256);
 #define REFIT_CASE(N)                                                                                                  \
   case N:                                                                                                              \
     hipLaunchKernelGGL(k_refit<N>, grid, blk, 0, st, rows, n, ng, g, gi, rc, G, h32, codes, scales, zeros, wq, e,      \
-                       active, dlog, dcnt, cap);                                                                       \
+                       active, dlog, dcnt);                                                                            \
     break;
   switch (npl_for(wd)) {
     REFIT_CASE(1)
@@ -570,9 +605,10 @@ hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, i
   return hipGetLastError();
 }
 
-hipError_t chunk_accum(hipStream_t st, int rows, int rc, int nchunks, int cap, const double* dlog, const uint32_t* dcnt,
-                       const uint8_t* active, double* ld, uint64_t* upd) {
-  hipLaunchKernelGGL(k_chunk_accum, dim3((nchunks + 63) / 64), dim3(64), 0, st, rows, rc, nchunks, cap, dlog, dcnt,
+hipError_t pass_accum(hipStream_t st, int rows, int rc, int nchunks, int nref, const double* rlog,
+                      const uint32_t* rcnt, int ncd, int cap, const double* clog, const uint32_t* ccnt,
+                      const uint8_t* active, double* ld, uint64_t* upd) {
+  hipLaunchKernelGGL(k_pass_accum, dim3(nchunks), dim3(64), 0, st, rows, rc, nref, rlog, rcnt, ncd, cap, clog, ccnt,
                      active, ld, upd);
   return hipGetLastError();
 }

@@ -134,94 +134,6 @@ __global__ __launch_bounds__(256) void k_combine(int m, int n, int np, T alpha, 
   *c = cv;
 }
 
-// ---- Gram accumulation (src/linalg.rs:388-418): per 2048-token chunk, tmp = X^T Y with the
-// panel-chained order above (alpha 1, beta 0), then H += (f64)tmp in chunk order. With Y == X the
-// chain of element (j, i) is the chain of (i, j) with the factors of every fma swapped, i.e. the
-// same bits, so only tiles with ti <= tj are computed and mirrored; each side keeps its own f64
-// accumulator because the incoming H need not be symmetric.
-template <bool SYM>
-__global__ __launch_bounds__(256) void k_gram(int t, int n, const float* __restrict__ X, const float* __restrict__ Y,
-                                              double* __restrict__ H, const int2* __restrict__ tiles) {
-  __shared__ float Xs[KT][BM + 4];
-  __shared__ float Ys[KT][BN + 4];
-  const int2 tl = tiles[blockIdx.x];
-  const int i0 = tl.x * BM, j0 = tl.y * BN;
-  const bool mirror = SYM && (tl.x != tl.y);
-  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-  double hA[4][4], hB[4][4];
-#pragma unroll
-  for (int a = 0; a < 4; ++a)
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int gi = i0 + ty * 4 + a, gj = j0 + tx * 4 + b;
-      const bool ok = gi < n && gj < n;
-      hA[a][b] = ok ? H[(long)gi * n + gj] : 0.0;
-      hB[a][b] = (ok && mirror) ? H[(long)gj * n + gi] : 0.0;
-    }
-  for (int c0 = 0; c0 < t; c0 += 2048) {
-    const int cend = min(t, c0 + 2048);
-    float acc[4][4], tmp[4][4];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        acc[a][b] = 0.0f;
-        tmp[a][b] = 0.0f;
-      }
-    for (int k0 = c0; k0 < cend; k0 += KT) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int e = tid + 256 * q;
-        const int kk = e >> 6, jj = e & 63;
-        const int tk = k0 + kk;
-        Xs[kk][jj] = (tk < cend && i0 + jj < n) ? X[(long)tk * n + i0 + jj] : 0.0f;
-        Ys[kk][jj] = (tk < cend && j0 + jj < n) ? Y[(long)tk * n + j0 + jj] : 0.0f;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int kk = 0; kk < KT; ++kk) {
-        float av[4], bv[4];
-#pragma unroll
-        for (int a = 0; a < 4; ++a) av[a] = Xs[kk][ty * 4 + a];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) bv[b] = Ys[kk][tx * 4 + b];
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-          for (int b = 0; b < 4; ++b) acc[a][b] = __builtin_fmaf(av[a], bv[b], acc[a][b]);
-      }
-      __syncthreads();
-      const int kn = k0 + KT;
-      if ((kn % CDCLQ_KC) == 0 || kn >= cend) {
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            tmp[a][b] = __builtin_fmaf(1.0f, acc[a][b], tmp[a][b]);
-            acc[a][b] = 0.0f;
-          }
-      }
-    }
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        hA[a][b] += (double)tmp[a][b];
-        if (mirror) hB[a][b] += (double)tmp[a][b];
-      }
-  }
-#pragma unroll
-  for (int a = 0; a < 4; ++a)
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int gi = i0 + ty * 4 + a, gj = j0 + tx * 4 + b;
-      if (gi < n && gj < n) {
-        H[(long)gi * n + gj] = hA[a][b];
-        if (mirror) H[(long)gj * n + gi] = hB[a][b];
-      }
-    }
-}
-
 }  // namespace
 
 size_t gemm_partials_elems(int m, int n, int k) {
@@ -267,23 +179,5 @@ template hipError_t gemm_chain<float>(hipStream_t, int, int, int, float, int, co
                                       long, long, float*, long, long, bool, float*);
 template hipError_t gemm_chain<double>(hipStream_t, int, int, int, double, int, const double*, long, long,
                                        const double*, long, long, double*, long, long, bool, double*);
-
-std::vector<int2> gram_tiles(int n, bool sym) {
-  const int nt = (n + BM - 1) / BM;
-  std::vector<int2> v;
-  for (int i = 0; i < nt; ++i)
-    for (int j = sym ? i : 0; j < nt; ++j) v.push_back(make_int2(i, j));
-  return v;
-}
-
-hipError_t gram_accumulate(hipStream_t st, int t, int n, const float* X, const float* Y, double* H, bool sym,
-                           const int2* tiles, int ntiles) {
-  if (n <= 0 || t <= 0 || ntiles <= 0) return hipSuccess;
-  if (sym)
-    hipLaunchKernelGGL((k_gram<true>), dim3(ntiles), dim3(256), 0, st, t, n, X, Y, H, tiles);
-  else
-    hipLaunchKernelGGL((k_gram<false>), dim3(ntiles), dim3(256), 0, st, t, n, X, Y, H, tiles);
-  return hipGetLastError();
-}
 
 }  // namespace cdclq

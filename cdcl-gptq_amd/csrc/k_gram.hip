@@ -1,0 +1,208 @@
+// H += X^T Y on the matrix cores (src/linalg.rs:388-418), bit-exact.
+//
+// The reference's order per element: for each 2048-token chunk, tmp = fold over KC = 256-token
+// panels of a fused-multiply-add chain in token order (first panel: tmp = chain; later panels:
+// tmp = tmp + chain), then h += (f64)tmp. v_mfma_f32_32x32x1_2b_f32 has K = 1: every instruction
+// adds exactly one product to each accumulator element with a single rounding, which the
+// day-0 probe showed to be bit-identical to fmaf (including denormals). A chain of these
+// instructions over the tokens of a panel is therefore the reference's chain.
+//
+// Work split: a 256-thread workgroup owns a 128 (rows) x 64 (cols) tile of one H; wave w owns
+// rows [64*(w>>1), +64) x cols [32*(w&1), +32) as one 2-block accumulator (block b = rows
+// 32b..32b+31). Tokens are staged 32 at a time through double-buffered LDS (row-major, so each
+// lane reads its row/col of the current token with a conflict-free ds_read_b32). The chunk sum
+// (f32) and the running H value (f64) stay in VGPRs for the whole token range, so H is read and
+// written once.
+//
+// A launch walks a list of tiles that may belong to several Hessians (GramJob), so the four
+// inputs of a decoder layer fill the GPU together. For symmetric jobs only tiles of the upper
+// 128x128 super-tile triangle are listed and off-diagonal results are also written transposed
+// (exact: fma(a, b, c) == fma(b, a, c)); this requires the incoming H to be symmetric, which the
+// host checks.
+#include "cdclq_dev.h"
+#include "kernels.h"
+
+namespace cdclq {
+namespace {
+
+typedef float v32f __attribute__((ext_vector_type(32)));
+
+constexpr int TI = 128, TJ = 64, KT = 32;
+
+__device__ __forceinline__ v32f mfma32(float a, float b, v32f c) {
+  return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, 0);
+}
+
+template <bool VEC4>
+__global__ __launch_bounds__(256, 2) void k_gram_mfma(const GramJob* __restrict__ jobs,
+                                                      const int4* __restrict__ tiles) {
+  __shared__ float Xs[2][KT][TI];
+  __shared__ float Ys[2][KT][TJ];
+  const int4 tl = tiles[blockIdx.x];
+  const GramJob jb = jobs[tl.x];
+  const int n = jb.n, T = jb.t;
+  const float* __restrict__ X = jb.x;
+  const float* __restrict__ Y = jb.y;
+  double* __restrict__ H = jb.h;
+  const int i0 = tl.y * TI, j0 = tl.z * TJ;
+  const bool mirror = tl.w != 0;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wi = wv >> 1, wj = wv & 1;
+
+  // Per-lane output coordinates of accumulator register r (probe-verified layout):
+  // block b = r >> 4, i = 8*((r&15)>>2) + 4*(lane>>5) + (r&3), j = lane & 31.
+  const int rbase = i0 + 64 * wi + 4 * (lane >> 5);
+  const int col = j0 + 32 * wj + (lane & 31);
+  double h[32];
+#pragma unroll
+  for (int r = 0; r < 32; ++r) {
+    const int row = rbase + 32 * (r >> 4) + 8 * ((r & 15) >> 2) + (r & 3);
+    h[r] = (row < n && col < n) ? H[(long)row * n + col] : 0.0;
+  }
+
+  // stage loader: Xs = X[t0:t0+KT, i0:i0+TI], Ys = X[t0:t0+KT, j0:j0+TJ] (zero outside)
+  float4 px[4], py[2];
+  auto gload = [&](int t0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = tid + 256 * q;  // 0..1023 float4 slots of the 32 x 128 tile
+      const int kk = e >> 5, c4 = (e & 31) * 4;
+      const int t = t0 + kk, c = i0 + c4;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (t < T) {
+        const float* p = X + (long)t * n + c;
+        if (VEC4 && c + 3 < n) {
+          v = *reinterpret_cast<const float4*>(p);
+        } else {
+          if (c < n) v.x = p[0];
+          if (c + 1 < n) v.y = p[1];
+          if (c + 2 < n) v.z = p[2];
+          if (c + 3 < n) v.w = p[3];
+        }
+      }
+      px[q] = v;
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int e = tid + 256 * q;  // 0..511 float4 slots of the 32 x 64 tile
+      const int kk = e >> 4, c4 = (e & 15) * 4;
+      const int t = t0 + kk, c = j0 + c4;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (t < T) {
+        const float* p = Y + (long)t * n + c;
+        if (VEC4 && c + 3 < n) {
+          v = *reinterpret_cast<const float4*>(p);
+        } else {
+          if (c < n) v.x = p[0];
+          if (c + 1 < n) v.y = p[1];
+          if (c + 2 < n) v.z = p[2];
+          if (c + 3 < n) v.w = p[3];
+        }
+      }
+      py[q] = v;
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = tid + 256 * q;
+      *reinterpret_cast<float4*>(&Xs[buf][e >> 5][(e & 31) * 4]) = px[q];
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int e = tid + 256 * q;
+      *reinterpret_cast<float4*>(&Ys[buf][e >> 4][(e & 15) * 4]) = py[q];
+    }
+  };
+
+  const int nstage = (T + KT - 1) / KT;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  v32f acc = {};
+  float tmp[32];
+#pragma unroll
+  for (int r = 0; r < 32; ++r) tmp[r] = 0.0f;
+  const float* xa = &Xs[0][0][64 * wi + lane];
+  const float* yb = &Ys[0][0][32 * wj + (lane & 31)];
+  for (int s = 0; s < nstage; ++s) {
+    const int buf = s & 1;
+    const int t0 = s * KT;
+    if (s + 1 < nstage) gload(t0 + KT);
+    const float* xs = xa + buf * (KT * TI);
+    const float* ys = yb + buf * (KT * TJ);
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) acc = mfma32(xs[kk * TI], ys[kk * TJ], acc);
+    const int tn = t0 + KT;
+    if ((tn % CDCLQ_KC) == 0 || tn >= T) {  // panel end: tmp = fma(1, chain, tmp)
+#pragma unroll
+      for (int r = 0; r < 32; ++r) tmp[r] = __builtin_fmaf(1.0f, acc[r], tmp[r]);
+      acc = v32f{};
+      if ((tn % 2048) == 0 || tn >= T) {  // chunk end: h += (f64) tmp
+#pragma unroll
+        for (int r = 0; r < 32; ++r) {
+          h[r] += (double)tmp[r];
+          tmp[r] = 0.0f;
+        }
+      }
+    }
+    if (s + 1 < nstage) lstore(buf ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int r = 0; r < 32; ++r) {
+    const int row = rbase + 32 * (r >> 4) + 8 * ((r & 15) >> 2) + (r & 3);
+    if (row < n && col < n) {
+      H[(long)row * n + col] = h[r];
+      if (mirror) H[(long)col * n + row] = h[r];
+    }
+  }
+}
+
+// flag |= (h not bitwise symmetric)
+__global__ __launch_bounds__(256) void k_sym_check(int n, const double* __restrict__ h, int* flag) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)n * n) return;
+  const int i = (int)(idx / n), j = (int)(idx % n);
+  if (j <= i) return;
+  const unsigned long long a = __double_as_longlong(h[idx]);
+  const unsigned long long b = __double_as_longlong(h[(long)j * n + i]);
+  if (a != b) atomicOr(flag, 1);
+}
+
+}  // namespace
+
+void gram_mfma_tiles(int job, int n, bool sym, std::vector<int4>& out) {
+  const int ni = (n + TI - 1) / TI;
+  const int nj = (n + TJ - 1) / TJ;
+  if (!sym) {
+    for (int I = 0; I < ni; ++I)
+      for (int J = 0; J < nj; ++J) out.push_back(make_int4(job, I, J, 0));
+    return;
+  }
+  // upper triangle of 128x128 super-tiles; each super-tile = two 128x64 workgroup tiles
+  for (int I = 0; I < ni; ++I)
+    for (int S = I; S < ni; ++S)
+      for (int h = 0; h < 2; ++h) {
+        const int J = 2 * S + h;
+        if (J >= nj) continue;
+        out.push_back(make_int4(job, I, J, S != I ? 1 : 0));
+      }
+}
+
+hipError_t gram_mfma(hipStream_t st, const GramJob* jobs, const int4* tiles, int ntiles, bool vec4) {
+  if (ntiles <= 0) return hipSuccess;
+  if (vec4)
+    hipLaunchKernelGGL(k_gram_mfma<true>, dim3(ntiles), dim3(256), 0, st, jobs, tiles);
+  else
+    hipLaunchKernelGGL(k_gram_mfma<false>, dim3(ntiles), dim3(256), 0, st, jobs, tiles);
+  return hipGetLastError();
+}
+
+hipError_t sym_check(hipStream_t st, int n, const double* h, int* flag) {
+  const long nn = (long)n * n;
+  hipLaunchKernelGGL(k_sym_check, dim3((unsigned)((nn + 255) / 256)), dim3(256), 0, st, n, h, flag);
+  return hipGetLastError();
+}
+
+}  // namespace cdclq

@@ -19,11 +19,19 @@ hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, int beta_one
                       const T* B, long rsb, long csb, T* C, long rsc, long csc, bool lower, T* partials);
 size_t gemm_partials_elems(int m, int n, int k);
 
-// H (n x n, f64) += X^T Y over 2048-token chunks; X, Y token-major (t x n). sym: Y == X.
-// `tiles` lists the 64x64 output tiles (gram_tiles), uploaded by the caller.
-std::vector<int2> gram_tiles(int n, bool sym);
-hipError_t gram_accumulate(hipStream_t st, int t, int n, const float* X, const float* Y, double* H, bool sym,
-                           const int2* tiles, int ntiles);
+// ---- k_gram.hip: H (n x n, f64) += X^T Y over 2048-token chunks on the matrix cores.
+struct GramJob {
+  const float* x;  // t x n, token-major
+  const float* y;  // t x n (== x for a Hessian)
+  double* h;       // n x n accumulator
+  int n;
+  int t;
+};
+// Appends the workgroup tiles of job `job` (int4: job, row block of 128, col block of 64,
+// mirror flag). `sym`: Y == X and the incoming H is symmetric.
+void gram_mfma_tiles(int job, int n, bool sym, std::vector<int4>& out);
+hipError_t gram_mfma(hipStream_t st, const GramJob* jobs, const int4* tiles, int ntiles, bool vec4);
+hipError_t sym_check(hipStream_t st, int n, const double* h, int* flag);
 
 // ---- k_factor.hip: damping, Cholesky, triangular inverse, U
 hipError_t build_flipped(hipStream_t st, int n, const float* h, const uint32_t* perm, double damp_val, double* a,
@@ -49,13 +57,16 @@ hipError_t colloss(hipStream_t st, int rows, int n, int rc, const float* err, do
 hipError_t sub_f32(hipStream_t st, size_t count, const float* a, const float* b, float* out);
 hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, int rc, const float* G, const float* h32,
                        const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
-                       const uint8_t* active, double* dlog, uint32_t* dcnt, int cap);
+                       const uint8_t* active, double* dlog, uint32_t* dcnt);
 hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
                        int sweeps, const float* G, const float* h32, const uint8_t* gbits, const float* scales,
                        const float* zeros, uint8_t* codes, float* wq, float* e, const uint8_t* active,
                        const uint8_t* sel, double* dlog, uint32_t* dcnt, int cap);
-hipError_t chunk_accum(hipStream_t st, int rows, int rc, int nchunks, int cap, const double* dlog, const uint32_t* dcnt,
-                       const uint8_t* active, double* ld, uint64_t* upd);
+// Folds one pass's logged deltas into the per-chunk loss (exact reference order); nref refit
+// steps (rlog/rcnt: [nref][rows]) then ncd CD steps (clog: [ncd][rows][cap], ccnt: [ncd][rows]).
+hipError_t pass_accum(hipStream_t st, int rows, int rc, int nchunks, int nref, const double* rlog,
+                      const uint32_t* rcnt, int ncd, int cap, const double* clog, const uint32_t* ccnt,
+                      const uint8_t* active, double* ld, uint64_t* upd);
 hipError_t synth_normal(hipStream_t st, uint64_t seed, uint64_t offset, size_t count, float sigma, float* out);
 hipError_t synth_tokens(hipStream_t st, uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale,
                         float* x);

@@ -120,6 +120,13 @@ int cdclq_quantize_layer_device(cdclq_ctx* ctx, const float* w, size_t d_out, si
  * t x n f32. y == x selects the symmetric Hessian path. */
 int cdclq_gram_accumulate(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h);
 int cdclq_gram_accumulate_device(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h);
+/* `count` independent accumulations in one launch (device pointers): hs[i] += xs[i]^T ys[i] with
+ * ts[i] tokens of width ns[i]. Each result equals a separate gram_accumulate call; batching only
+ * lets the inputs of one decoder layer (q/k/v, o, gate/up, down) share the GPU. The reference's
+ * capture script accumulates all of a layer's Hessians in the same forward pass
+ * (scripts/capture_hessians.py:233-245). */
+int cdclq_gram_accumulate_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const float* const* ys,
+                                       const size_t* ts, const size_t* ns, double* const* hs);
 
 /* linalg::upper_chol_of_inverse (src/linalg.rs:362-375): u (n x n f32, upper) with
  * h^-1 = u^T u. h is not modified. */

@@ -94,6 +94,26 @@ def test_gram_bitexact(ctx, t, n, sym):
         assert np.array_equal(hz, hz.T)
 
 
+def test_gram_batch_matches_single_calls(ctx):
+    """Several accumulations in one launch: symmetric from zero, cross-covariance, symmetric
+    start that is not bitwise symmetric (must take the unmirrored path), odd widths."""
+    rng = np.random.default_rng(5)
+    cases = []
+    for (t, n, kind) in ((3000, 300, "sym0"), (2100, 130, "asym"), (2500, 97, "symstart"), (4096, 256, "sym0")):
+        x = (rng.standard_normal((t, n)) * rng.uniform(0.1, 5, n)).astype(np.float32)
+        y = x if kind != "asym" else (x + 0.1 * rng.standard_normal((t, n))).astype(np.float32)
+        h0 = np.zeros((n, n)) if kind == "sym0" else rng.standard_normal((n, n))
+        cases.append((t, n, x, y, h0))
+    dx = [cdclq.DeviceArray.from_host(ctx, c[2]) for c in cases]
+    dy = [d if c[3] is c[2] else cdclq.DeviceArray.from_host(ctx, c[3]) for d, c in zip(dx, cases)]
+    dh = [cdclq.DeviceArray.from_host(ctx, c[4]) for c in cases]
+    print("[parity] gram batch of", [(c[0], c[1]) for c in cases], flush=True)
+    cdclq.gram_accumulate_batch_device(ctx, dx, dy, [c[0] for c in cases], [c[1] for c in cases], dh)
+    for (t, n, x, y, h0), d in zip(cases, dh):
+        ho = O.gram_accumulate(x, None if y is x else y, h0.copy())
+        assert np.array_equal(d.download().view(np.uint64), ho.view(np.uint64)), (t, n)
+
+
 # ---------------------------------------------------------------- U
 @pytest.mark.parametrize("n", [1, 5, 96, 150, 200, 400])
 def test_upper_chol_bitexact(ctx, n):
