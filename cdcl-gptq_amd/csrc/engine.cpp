@@ -240,12 +240,12 @@ int factor(cdclq_ctx* ctx, int n, double* a, double* y, float* u) {
   return CDCLQ_OK;
 }
 
-// The G = E H[:, c0:c0+wd] GEMM of phase 2 (src/engine.rs:548, :608).
+// The G = E H[:, c0:c0+wd] GEMM of phase 2 (src/engine.rs:548, :608): per-panel chains into
+// ctx->part, then folded in panel order into ctx->G.
 int grad_gemm(cdclq_ctx* ctx, int rows, int n, int c0, int wd, const float* e, const float* h32) {
-  return gemm_chain<float>(ctx->st, rows, wd, n, 1.0f, 0, e, n, 1, h32 + c0, n, 1, P<float>(ctx->G), wd, 1, false,
-                           P<float>(ctx->part)) == hipSuccess
-             ? CDCLQ_OK
-             : fail(ctx, CDCLQ_DEVICE, "gradient GEMM launch failed");
+  hipError_t err = panel_gemm(ctx->st, rows, wd, n, e, n, h32 + c0, n, P<float>(ctx->part));
+  if (err == hipSuccess) err = fold_panels(ctx->st, rows, wd, (n + 255) / 256, P<float>(ctx->part), P<float>(ctx->G));
+  return err == hipSuccess ? CDCLQ_OK : fail(ctx, CDCLQ_DEVICE, std::string("gradient GEMM: ") + hipGetErrorString(err));
 }
 
 int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, const float* h, const float* m,
@@ -461,8 +461,8 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
     HIPCK(hipMemcpyAsync(ctx->sel_d.p, sel.data(), sel.size(), hipMemcpyHostToDevice, st));
     HIPCK(sub_f32(st, wn, wp, wq, eb));  // e = W - W_hat (src/engine.rs:516-519)
     const int wdmax = std::max(do_cd ? sbw : 1, do_refit ? g : 1);
+    CK(ensure(ctx, ctx->part, panel_partials_elems(d_out, wdmax, n) * 4));
     CK(ensure(ctx, ctx->G, (size_t)d_out * wdmax * 4));
-    CK(ensure(ctx, ctx->part, gemm_partials_elems(d_out, wdmax, n) * 4));
     // Per-pass logs of accepted deltas (folded into the chunk losses in the reference's order).
     const int cap = std::max(1, do_cd ? sbw * (int)cfg->cd_sweeps : 1);
     CK(ensure(ctx, ctx->rlog, (size_t)ng * d_out * 8));

@@ -226,180 +226,6 @@ __global__ __launch_bounds__(256) void k_sub(long count, const float* __restrict
   if (idx < count) o[idx] = a[idx] - b[idx];
 }
 
-// ---------------------------------------------------------------- phase 2 (src/engine.rs:534-670)
-// Closed-form f16 scale refit of group gi for every row of an active chunk (src/engine.rs:543-587).
-// G = E H[:, group] (rows x wd) comes from the chain GEMM. hu = uu H_CC is chained here per lane.
-template <int NPL>
-__global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, int gi, int rc,
-                                               const float* __restrict__ G, const float* __restrict__ h32,
-                                               const uint8_t* __restrict__ codes, float* __restrict__ scales,
-                                               const float* __restrict__ zeros, float* __restrict__ wq,
-                                               float* __restrict__ e, const uint8_t* __restrict__ active,
-                                               double* __restrict__ dlog, uint32_t* __restrict__ dcnt) {
-  // this step's log: one slot per row (dlog/dcnt point at the slot of group gi)
-  const int lane = threadIdx.x & 63;
-  const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
-  if (r >= rows) return;
-  if (!active[r / rc]) {
-    if (lane == 0) dcnt[r] = 0;
-    return;
-  }
-  const int c0 = gi * g, wd = min(c0 + g, n) - c0;
-  const float z = zeros[(long)r * ng + gi];
-  const float s_old = scales[(long)r * ng + gi];
-  float uu[NPL], gg[NPL], cvh[NPL], acc[NPL];
-#pragma unroll
-  for (int s = 0; s < NPL; ++s) {
-    const int k = s * 64 + lane;
-    uu[s] = (k < wd) ? (float)codes[(long)r * n + c0 + k] - z : 0.0f;
-    gg[s] = (k < wd) ? G[(long)r * wd + k] : 0.0f;
-    cvh[s] = 0.0f;
-    acc[s] = 0.0f;
-  }
-  // hu[k2] = sum_k uu[k] * H[c0+k][c0+k2] (sgemm at src/engine.rs:560, KC-panelled)
-#pragma unroll
-  for (int s1 = 0; s1 < NPL; ++s1) {
-    for (int kk = 0; kk < 64; ++kk) {
-      const int k = s1 * 64 + kk;
-      if (k >= wd) break;
-      const float uk = readlane(uu[s1], kk);
-      const float* hrow = h32 + (long)(c0 + k) * n + c0;
-#pragma unroll
-      for (int s2 = 0; s2 < NPL; ++s2) {
-        const int k2 = s2 * 64 + lane;
-        if (k2 < wd) acc[s2] = __builtin_fmaf(uk, hrow[k2], acc[s2]);
-      }
-      if (((k + 1) % CDCLQ_KC) == 0 || k + 1 == wd) {
-#pragma unroll
-        for (int s2 = 0; s2 < NPL; ++s2) {
-          cvh[s2] = __builtin_fmaf(1.0f, acc[s2], cvh[s2]);
-          acc[s2] = 0.0f;
-        }
-      }
-    }
-  }
-  float num = 0.0f, den = 0.0f;
-#pragma unroll
-  for (int s1 = 0; s1 < NPL; ++s1) {
-    for (int kk = 0; kk < 64; ++kk) {
-      const int k = s1 * 64 + kk;
-      if (k >= wd) break;
-      const float uk = readlane(uu[s1], kk);
-      num = num + uk * readlane(gg[s1], kk);
-      den = den + uk * readlane(cvh[s1], kk);
-    }
-  }
-  uint32_t moved = 0;
-  if (den > 1e-30f) {
-    const float s_new = rs_maxf(round_f16(s_old + num / den), CDCLQ_F16_MIN_NORMAL);
-    const float d = s_new - s_old;
-    const float dl32 = (-2.0f * d) * num + (d * d) * den;
-    if ((double)dl32 < 0.0) {
-      if (lane == 0) {
-        scales[(long)r * ng + gi] = s_new;
-        dlog[r] = (double)dl32;
-      }
-#pragma unroll
-      for (int s = 0; s < NPL; ++s) {
-        const int k = s * 64 + lane;
-        if (k < wd) {
-          const long o = (long)r * n + c0 + k;
-          const float ndq = s_new * uu[s];
-          e[o] = e[o] + (wq[o] - ndq);
-          wq[o] = ndq;
-        }
-      }
-      moved = 1;
-    }
-  }
-  if (lane == 0) dcnt[r] = moved;
-}
-
-// Coordinate-descent sweeps over sub-block [c0, c0+wd) (src/engine.rs:600-658).
-template <int NPL>
-__global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
-                                            int sweeps, const float* __restrict__ G, const float* __restrict__ h32,
-                                            const uint8_t* __restrict__ gbits, const float* __restrict__ scales,
-                                            const float* __restrict__ zeros, uint8_t* __restrict__ codes,
-                                            float* __restrict__ wq, float* __restrict__ e,
-                                            const uint8_t* __restrict__ active, const uint8_t* __restrict__ sel,
-                                            double* __restrict__ dlog, uint32_t* __restrict__ dcnt, int cap) {
-  const int lane = threadIdx.x & 63;
-  const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
-  if (r >= rows) return;
-  const int chunk = r / rc;
-  if (!active[chunk] || !sel[(long)chunk * nsb + sb]) {
-    if (lane == 0) dcnt[r] = 0;
-    return;
-  }
-  float gg[NPL], mwq[NPL], me[NPL];
-  int mc[NPL];
-#pragma unroll
-  for (int s = 0; s < NPL; ++s) {
-    const int k = s * 64 + lane;
-    const long o = (long)r * n + c0 + k;
-    gg[s] = (k < wd) ? G[(long)r * wd + k] : 0.0f;
-    mwq[s] = (k < wd) ? wq[o] : 0.0f;
-    me[s] = (k < wd) ? e[o] : 0.0f;
-    mc[s] = (k < wd) ? (int)codes[o] : 0;
-  }
-  uint32_t moves = 0;
-  double* dl = dlog + (long)r * cap;
-  for (int sw = 0; sw < sweeps; ++sw) {
-    int changed = 0;
-#pragma unroll
-    for (int s = 0; s < NPL; ++s) {
-      for (int ii = 0; ii < 64; ++ii) {
-        const int jj = s * 64 + ii;
-        if (jj >= wd) break;
-        const int j = c0 + jj;
-        const int gi = j / g;
-        const float maxq = (float)((1u << gbits[gi]) - 1u);
-        const float sc = scales[(long)r * ng + gi];
-        const float z = zeros[(long)r * ng + gi];
-        const float hjj = h32[(long)j * n + j];
-        const float cur = readlane(mwq[s], ii);
-        const float gj = readlane(gg[s], ii);
-        const int code = readlane_i(mc[s], ii);
-        const float target = cur + gj / hjj;
-        float q;
-        const float newdq = quant_dq(target, sc, z, maxq, &q);
-        const int qc = (int)code_of(q);
-        if (qc != code) {
-          const float de = cur - newdq;
-          const float d32 = (2.0f * de) * gj + (de * de) * hjj;
-          if (lane == 0) dl[moves] = (double)d32;
-          ++moves;
-          const float* hrow = h32 + (long)j * n + c0;
-#pragma unroll
-          for (int s2 = 0; s2 < NPL; ++s2) {
-            const int k = s2 * 64 + lane;
-            if (k < wd) gg[s2] = gg[s2] + de * hrow[k];
-          }
-          if (lane == ii) {
-            mwq[s] = newdq;
-            mc[s] = qc;
-            me[s] = me[s] + de;
-          }
-          changed = 1;
-        }
-      }
-    }
-    if (!changed) break;
-  }
-#pragma unroll
-  for (int s = 0; s < NPL; ++s) {
-    const int k = s * 64 + lane;
-    if (k < wd) {
-      const long o = (long)r * n + c0 + k;
-      wq[o] = mwq[s];
-      e[o] = me[s];
-      codes[o] = (uint8_t)mc[s];
-    }
-  }
-  if (lane == 0) dcnt[r] = moves;
-}
-
 // Per-chunk loss bookkeeping of one pass, in the reference's order (src/engine.rs:583, :640):
 // steps in execution order (refit groups, then CD sub-blocks), within a step rows ascending,
 // within a row its accepted deltas in the order they were made. One wave per chunk: the wave
@@ -556,52 +382,6 @@ hipError_t colloss(hipStream_t st, int rows, int n, int rc, const float* err, do
 
 hipError_t sub_f32(hipStream_t st, size_t count, const float* a, const float* b, float* out) {
   hipLaunchKernelGGL(k_sub, dim3(nblk((long)count)), dim3(256), 0, st, (long)count, a, b, out);
-  return hipGetLastError();
-}
-
-hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, int rc, const float* G, const float* h32,
-                       const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
-                       const uint8_t* active, double* dlog, uint32_t* dcnt) {
-  const int wd = std::min(gi * g + g, n) - gi * g;
-  const dim3 grid((rows + 3) / 4), blk(256);
-#define REFIT_CASE(N)                                                                                                  \
-  case N:                                                                                                              \
-    hipLaunchKernelGGL(k_refit<N>, grid, blk, 0, st, rows, n, ng, g, gi, rc, G, h32, codes, scales, zeros, wq, e,      \
-                       active, dlog, dcnt);                                                                            \
-    break;
-  switch (npl_for(wd)) {
-    REFIT_CASE(1)
-    REFIT_CASE(2)
-    REFIT_CASE(4)
-    REFIT_CASE(8)
-    REFIT_CASE(16)
-    default:
-      return hipErrorInvalidValue;
-  }
-#undef REFIT_CASE
-  return hipGetLastError();
-}
-
-hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
-                       int sweeps, const float* G, const float* h32, const uint8_t* gbits, const float* scales,
-                       const float* zeros, uint8_t* codes, float* wq, float* e, const uint8_t* active,
-                       const uint8_t* sel, double* dlog, uint32_t* dcnt, int cap) {
-  const dim3 grid((rows + 3) / 4), blk(256);
-#define CD_CASE(N)                                                                                                     \
-  case N:                                                                                                              \
-    hipLaunchKernelGGL(k_cd<N>, grid, blk, 0, st, rows, n, ng, g, c0, wd, sb, nsb, rc, sweeps, G, h32, gbits, scales,  \
-                       zeros, codes, wq, e, active, sel, dlog, dcnt, cap);                                             \
-    break;
-  switch (npl_for(wd)) {
-    CD_CASE(1)
-    CD_CASE(2)
-    CD_CASE(4)
-    CD_CASE(8)
-    CD_CASE(16)
-    default:
-      return hipErrorInvalidValue;
-  }
-#undef CD_CASE
   return hipGetLastError();
 }
 

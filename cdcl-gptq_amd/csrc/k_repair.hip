@@ -1,0 +1,421 @@
+// Phase-2 kernels (src/engine.rs:534-670): the repair gradient G = E H[:, c0:c0+wd] on the matrix
+// cores, and the refit / coordinate-descent sweeps that consume it.
+//
+// Gradient. The reference computes G with matrixmultiply (k = n): per element a fused chain over
+// each KC = 256 panel of k, panels folded in order. k_panel_gemm computes every panel's chain in
+// parallel with v_mfma_f32_16x16x1_4b_f32 (K = 1, single rounding per product, bit-identical to
+// fmaf) and stores the per-panel values; k_fold then folds them in panel order, one thread per
+// element. Workgroup: 256 rows x 64 cols x one panel; wave w owns 64 rows as four 16-row groups,
+// each one 4-block accumulator (block b = cols 16b..16b+15); E and the panel of H are staged in
+// double-buffered LDS, 16 k at a time.
+//
+// Sweeps. One wavefront per row (columns spread over lanes, wave-uniform column loop). The refit
+// needs all of H_CC for every row, so a workgroup of 16 rows stages it in LDS when it fits; the
+// descent touches a row of H_sb only when a code moves and reads it from L2.
+#include <algorithm>
+
+#include "cdclq_dev.h"
+#include "kernels.h"
+
+namespace cdclq {
+namespace {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int PR = 256;  // rows per panel-GEMM workgroup
+constexpr int PC = 64;   // cols per panel-GEMM workgroup
+
+__device__ __forceinline__ v16f mfma16(float a, float b, v16f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0);
+}
+
+constexpr int SK = 16;        // k per LDS stage
+constexpr int ES = SK + 4;     // padded row stride of the E stage (16-byte aligned, conflict-free b128 reads)
+
+template <bool VEC4>
+__global__ __launch_bounds__(256, 2) void k_panel_gemm(int m, int wd, int k, const float* __restrict__ A, long lda,
+                                                       const float* __restrict__ B, long ldb, float* __restrict__ P) {
+  __shared__ float Es[2][PR * ES];  // E[r0:r0+256, k-slice], row-major, padded
+  __shared__ float Hs[2][SK * PC];  // B[k-slice, cb:cb+64]
+  const int p = blockIdx.y;
+  const int k0 = p * CDCLQ_KC;
+  const int kc = min(CDCLQ_KC, k - k0);
+  const int r0 = blockIdx.x * PR;
+  const int cb = blockIdx.z * PC;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // global -> register prefetch of one stage: 8 float4 of E (256 rows x 32 k), 2 float4 of B (32 x 64)
+  constexpr int EQ = PR * SK / 4 / 256;  // float4 of E per thread per stage
+  constexpr int HQ = SK * PC / 4 / 256;  // float4 of B per thread per stage
+  constexpr int K4 = SK / 4;             // float4 per E row per stage
+  float4 pe[EQ], ph[HQ];
+  auto gload = [&](int ks) {
+#pragma unroll
+    for (int q = 0; q < EQ; ++q) {
+      const int e = tid + 256 * q;  // row = e / K4, k4 = (e % K4) * 4
+      const int r = r0 + e / K4, kk = ks + (e % K4) * 4;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (r < m) {
+        const float* src = A + (long)r * lda + k0 + kk;
+        if (VEC4 && kk + 3 < kc) {
+          v = *reinterpret_cast<const float4*>(src);
+        } else {
+          if (kk < kc) v.x = src[0];
+          if (kk + 1 < kc) v.y = src[1];
+          if (kk + 2 < kc) v.z = src[2];
+          if (kk + 3 < kc) v.w = src[3];
+        }
+      }
+      pe[q] = v;
+    }
+#pragma unroll
+    for (int q = 0; q < HQ; ++q) {
+      const int e = tid + 256 * q;  // kk = e >> 4, c4 = (e & 15) * 4
+      const int kk = ks + (e >> 4), c = cb + (e & 15) * 4;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (kk < kc) {
+        const float* src = B + (long)(k0 + kk) * ldb + c;
+        if (c < wd) v.x = src[0];
+        if (c + 1 < wd) v.y = src[1];
+        if (c + 2 < wd) v.z = src[2];
+        if (c + 3 < wd) v.w = src[3];
+      }
+      ph[q] = v;
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < EQ; ++q) {
+      const int e = tid + 256 * q;
+      *reinterpret_cast<float4*>(&Es[buf][(e / K4) * ES + (e % K4) * 4]) = pe[q];
+    }
+#pragma unroll
+    for (int q = 0; q < HQ; ++q) {
+      const int e = tid + 256 * q;
+      *reinterpret_cast<float4*>(&Hs[buf][(e >> 4) * PC + (e & 15) * 4]) = ph[q];
+    }
+  };
+  v16f acc[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) acc[q] = v16f{};
+  const int nst = (kc + SK - 1) / SK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int s = 0; s < nst; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < nst) gload((s + 1) * SK);
+    const float* es = &Es[buf][(64 * wv + (lane & 15)) * ES];
+    const float* hs = &Hs[buf][lane];
+#pragma unroll
+    for (int k4 = 0; k4 < SK; k4 += 4) {
+      float4 a[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a[q] = *reinterpret_cast<const float4*>(es + 16 * q * ES + k4);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float b = hs[(k4 + u) * PC];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float av = u == 0 ? a[q].x : u == 1 ? a[q].y : u == 2 ? a[q].z : a[q].w;
+          acc[q] = mfma16(av, b, acc[q]);
+        }
+      }
+    }
+    if (s + 1 < nst) lstore(buf ^ 1);
+    __syncthreads();
+  }
+  // D_b[i][j] at reg 4b + (i&3), lane j + 16*(i>>2): row 16q + i, col 16b + j
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int row = r0 + 64 * wv + 16 * q + 4 * (lane >> 4) + (j & 3);
+      const int col = cb + 16 * (j >> 2) + (lane & 15);
+      if (row < m && col < wd) P[((long)p * m + row) * wd + col] = acc[q][j];
+    }
+}
+
+// G[r][c] = ordered fold of the panel chains (alpha 1, beta 0): C = fma(1, P_p, C) for p = 0, 1, ...
+// One thread per entry, panel loads unrolled so many are in flight.
+__global__ __launch_bounds__(256) void k_fold(long count, int np, const float* __restrict__ P, float* __restrict__ G) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= count) return;
+  const float* src = P + idx;
+  float g = 0.0f;
+  int p = 0;
+  for (; p + 8 <= np; p += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[(long)(p + u) * count];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) g = __builtin_fmaf(1.0f, v[u], g);
+  }
+  for (; p < np; ++p) g = __builtin_fmaf(1.0f, src[(long)p * count], g);
+  G[idx] = g;
+}
+
+constexpr int RPW = 4;  // rows per wave in the refit kernel (16 rows per workgroup share H_CC in LDS)
+
+// Closed-form f16 scale refit of group gi (src/engine.rs:543-587).
+template <int NPL, bool LDSH>
+__global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, int gi, int rc, const float* __restrict__ G,
+                                               const float* __restrict__ h32,
+                                               const uint8_t* __restrict__ codes, float* __restrict__ scales,
+                                               const float* __restrict__ zeros, float* __restrict__ wq,
+                                               float* __restrict__ e, const uint8_t* __restrict__ active,
+                                               double* __restrict__ dlog, uint32_t* __restrict__ dcnt) {
+  extern __shared__ float hcc[];  // H_CC (wd x wd) when LDSH
+  const int c0 = gi * g, wd = min(c0 + g, n) - c0;
+  const int lane = threadIdx.x & 63;
+  const int rbase = blockIdx.x * 4 * RPW;
+  if (LDSH) {
+    for (int x = threadIdx.x; x < wd * wd; x += 256) hcc[x] = h32[(long)(c0 + x / wd) * n + c0 + x % wd];
+    __syncthreads();
+  }
+  for (int q = 0; q < RPW; ++q) {
+    const int r = __builtin_amdgcn_readfirstlane(rbase + q * 4 + (threadIdx.x >> 6));
+    if (r >= rows) break;
+    if (!active[r / rc]) {
+      if (lane == 0) dcnt[r] = 0;
+      continue;
+    }
+    const float z = zeros[(long)r * ng + gi];
+    const float s_old = scales[(long)r * ng + gi];
+    float uu[NPL], gg[NPL], cvh[NPL], acc[NPL];
+#pragma unroll
+    for (int s = 0; s < NPL; ++s) {
+      const int k = s * 64 + lane;
+      uu[s] = (k < wd) ? (float)codes[(long)r * n + c0 + k] - z : 0.0f;
+      gg[s] = (k < wd) ? G[(long)r * wd + k] : 0.0f;
+      cvh[s] = 0.0f;
+      acc[s] = 0.0f;
+    }
+    // hu[k2] = sum_k uu[k] * H[c0+k][c0+k2] (sgemm at src/engine.rs:560, KC-panelled)
+#pragma unroll
+    for (int s1 = 0; s1 < NPL; ++s1) {
+      for (int kk = 0; kk < 64; ++kk) {
+        const int k = s1 * 64 + kk;
+        if (k >= wd) break;
+        const float uk = readlane(uu[s1], kk);
+#pragma unroll
+        for (int s2 = 0; s2 < NPL; ++s2) {
+          const int k2 = s2 * 64 + lane;
+          if (k2 < wd) {
+            const float hv = LDSH ? hcc[k * wd + k2] : h32[(long)(c0 + k) * n + c0 + k2];
+            acc[s2] = __builtin_fmaf(uk, hv, acc[s2]);
+          }
+        }
+        if (((k + 1) % CDCLQ_KC) == 0 || k + 1 == wd) {
+#pragma unroll
+          for (int s2 = 0; s2 < NPL; ++s2) {
+            cvh[s2] = __builtin_fmaf(1.0f, acc[s2], cvh[s2]);
+            acc[s2] = 0.0f;
+          }
+        }
+      }
+    }
+    float num = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int s1 = 0; s1 < NPL; ++s1) {
+      for (int kk = 0; kk < 64; ++kk) {
+        const int k = s1 * 64 + kk;
+        if (k >= wd) break;
+        const float uk = readlane(uu[s1], kk);
+        num = num + uk * readlane(gg[s1], kk);
+        den = den + uk * readlane(cvh[s1], kk);
+      }
+    }
+    uint32_t moved = 0;
+    if (den > 1e-30f) {
+      const float s_new = rs_maxf(round_f16(s_old + num / den), CDCLQ_F16_MIN_NORMAL);
+      const float d = s_new - s_old;
+      const float dl32 = (-2.0f * d) * num + (d * d) * den;
+      if ((double)dl32 < 0.0) {
+        if (lane == 0) {
+          scales[(long)r * ng + gi] = s_new;
+          dlog[r] = (double)dl32;
+        }
+#pragma unroll
+        for (int s = 0; s < NPL; ++s) {
+          const int k = s * 64 + lane;
+          if (k < wd) {
+            const long o = (long)r * n + c0 + k;
+            const float ndq = s_new * uu[s];
+            e[o] = e[o] + (wq[o] - ndq);
+            wq[o] = ndq;
+          }
+        }
+        moved = 1;
+      }
+    }
+    if (lane == 0) dcnt[r] = moved;
+  }
+}
+
+// Coordinate-descent sweeps over sub-block [c0, c0+wd) (src/engine.rs:600-658); one wave per row.
+template <int NPL>
+__global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
+                                            int sweeps, const float* __restrict__ G, const float* __restrict__ h32,
+                                            const uint8_t* __restrict__ gbits, const float* __restrict__ scales,
+                                            const float* __restrict__ zeros, uint8_t* __restrict__ codes,
+                                            float* __restrict__ wq, float* __restrict__ e,
+                                            const uint8_t* __restrict__ active, const uint8_t* __restrict__ sel,
+                                            double* __restrict__ dlog, uint32_t* __restrict__ dcnt, int cap) {
+  const int lane = threadIdx.x & 63;
+  const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (r >= rows) return;
+  const int chunk = r / rc;
+  if (!active[chunk] || !sel[(long)chunk * nsb + sb]) {
+    if (lane == 0) dcnt[r] = 0;
+    return;
+  }
+  float gg[NPL], mwq[NPL], me[NPL];
+  int mc[NPL];
+#pragma unroll
+  for (int s = 0; s < NPL; ++s) {
+    const int k = s * 64 + lane;
+    const long o = (long)r * n + c0 + k;
+    gg[s] = (k < wd) ? G[(long)r * wd + k] : 0.0f;
+    mwq[s] = (k < wd) ? wq[o] : 0.0f;
+    me[s] = (k < wd) ? e[o] : 0.0f;
+    mc[s] = (k < wd) ? (int)codes[o] : 0;
+  }
+  uint32_t moves = 0;
+  double* dl = dlog + (long)r * cap;
+  for (int sw = 0; sw < sweeps; ++sw) {
+    int changed = 0;
+#pragma unroll
+    for (int s = 0; s < NPL; ++s) {
+      for (int ii = 0; ii < 64; ++ii) {
+        const int jj = s * 64 + ii;
+        if (jj >= wd) break;
+        const int j = c0 + jj;
+        const int gi = j / g;
+        const float maxq = (float)((1u << gbits[gi]) - 1u);
+        const float sc = scales[(long)r * ng + gi];
+        const float z = zeros[(long)r * ng + gi];
+        const float hjj = h32[(long)j * n + j];
+        const float cur = readlane(mwq[s], ii);
+        const float gj = readlane(gg[s], ii);
+        const int code = __builtin_amdgcn_readlane(mc[s], ii);
+        const float target = cur + gj / hjj;
+        float qv;
+        const float newdq = quant_dq(target, sc, z, maxq, &qv);
+        const int qc = (int)code_of(qv);
+        if (qc != code) {
+          const float de = cur - newdq;
+          const float d32 = (2.0f * de) * gj + (de * de) * hjj;
+          if (lane == 0) dl[moves] = (double)d32;
+          ++moves;
+          const float* hrow = h32 + (long)j * n + c0;
+#pragma unroll
+          for (int s2 = 0; s2 < NPL; ++s2) {
+            const int k = s2 * 64 + lane;
+            if (k < wd) gg[s2] = gg[s2] + de * hrow[k];
+          }
+          if (lane == ii) {
+            mwq[s] = newdq;
+            mc[s] = qc;
+            me[s] = me[s] + de;
+          }
+          changed = 1;
+        }
+      }
+    }
+    if (!changed) break;
+  }
+#pragma unroll
+  for (int s = 0; s < NPL; ++s) {
+    const int k = s * 64 + lane;
+    if (k < wd) {
+      const long o = (long)r * n + c0 + k;
+      wq[o] = mwq[s];
+      e[o] = me[s];
+      codes[o] = (uint8_t)mc[s];
+    }
+  }
+  if (lane == 0) dcnt[r] = moves;
+}
+
+int npl_for(int cnt) {
+  if (cnt <= 64) return 1;
+  if (cnt <= 128) return 2;
+  if (cnt <= 256) return 4;
+  if (cnt <= 512) return 8;
+  if (cnt <= 1024) return 16;
+  return 0;
+}
+
+}  // namespace
+
+size_t panel_partials_elems(int m, int wd, int k) {
+  return (size_t)((k + CDCLQ_KC - 1) / CDCLQ_KC) * (size_t)m * (size_t)wd;
+}
+
+hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long lda, const float* B, long ldb,
+                      float* P) {
+  if (m <= 0 || wd <= 0 || k <= 0) return hipSuccess;
+  const dim3 grid((m + PR - 1) / PR, (k + CDCLQ_KC - 1) / CDCLQ_KC, (wd + PC - 1) / PC);
+  const bool vec4 = (lda % 4 == 0) && ((uintptr_t)A % 16 == 0);
+  if (vec4)
+    hipLaunchKernelGGL(k_panel_gemm<true>, grid, dim3(256), 0, st, m, wd, k, A, lda, B, ldb, P);
+  else
+    hipLaunchKernelGGL(k_panel_gemm<false>, grid, dim3(256), 0, st, m, wd, k, A, lda, B, ldb, P);
+  return hipGetLastError();
+}
+
+hipError_t fold_panels(hipStream_t st, int m, int wd, int np, const float* P, float* G) {
+  const long count = (long)m * wd;
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fold, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st, count, np, P, G);
+  return hipGetLastError();
+}
+
+hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, int rc, const float* G,
+                       const float* h32, const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
+                       const uint8_t* active, double* dlog, uint32_t* dcnt) {
+  const int wd = std::min(gi * g + g, n) - gi * g;
+  const dim3 grid((rows + 4 * RPW - 1) / (4 * RPW)), blk(256);
+#define REFIT_CASE(N, L)                                                                                               \
+  hipLaunchKernelGGL((k_refit<N, L>), grid, blk, (L) ? (size_t)wd * wd * 4 : 0, st, rows, n, ng, g, gi, rc, G, h32,    \
+                     codes, scales, zeros, wq, e, active, dlog, dcnt)
+  static bool lds_raised = false;  // 64 KB of dynamic LDS for H_CC at wd = 128
+  if (!lds_raised) {
+    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_refit<2, true>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 65536);
+    if (err != hipSuccess) return err;
+    lds_raised = true;
+  }
+  switch (npl_for(wd)) {
+    case 1: REFIT_CASE(1, true); break;
+    case 2: REFIT_CASE(2, true); break;
+    case 4: REFIT_CASE(4, false); break;
+    case 8: REFIT_CASE(8, false); break;
+    case 16: REFIT_CASE(16, false); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef REFIT_CASE
+  return hipGetLastError();
+}
+
+hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
+                       int sweeps, const float* G, const float* h32, const uint8_t* gbits, const float* scales,
+                       const float* zeros, uint8_t* codes, float* wq, float* e, const uint8_t* active,
+                       const uint8_t* sel, double* dlog, uint32_t* dcnt, int cap) {
+  const dim3 grid((rows + 3) / 4), blk(256);
+#define CD_CASE(N)                                                                                                     \
+  hipLaunchKernelGGL((k_cd<N>), grid, blk, 0, st, rows, n, ng, g, c0, wd, sb, nsb, rc, sweeps, G, h32, gbits, scales,  \
+                     zeros, codes, wq, e, active, sel, dlog, dcnt, cap)
+  switch (npl_for(wd)) {
+    case 1: CD_CASE(1); break;
+    case 2: CD_CASE(2); break;
+    case 4: CD_CASE(4); break;
+    case 8: CD_CASE(8); break;
+    case 16: CD_CASE(16); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef CD_CASE
+  return hipGetLastError();
+}
+
+}  // namespace cdclq
