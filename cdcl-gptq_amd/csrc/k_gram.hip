@@ -26,6 +26,9 @@ namespace cdclq {
 namespace {
 
 typedef float v32f __attribute__((ext_vector_type(32)));
+typedef __attribute__((address_space(1))) const float gfloat;
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const f4v gf4v;
 
 constexpr int TI = 128, TJ = 64, KT = 32;
 
@@ -43,7 +46,7 @@ __global__ __launch_bounds__(256, 2) void k_gram_mfma(const GramJob* __restrict_
   const int n = jb.n, T = jb.t;
   const float* __restrict__ X = jb.x;
   const float* __restrict__ Y = jb.y;
-  double* __restrict__ H = jb.h;
+  __attribute__((address_space(1))) double* H = (__attribute__((address_space(1))) double*)jb.h;
   const int i0 = tl.y * TI, j0 = tl.z * TJ;
   const bool mirror = tl.w != 0;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -60,58 +63,58 @@ __global__ __launch_bounds__(256, 2) void k_gram_mfma(const GramJob* __restrict_
     h[r] = (row < n && col < n) ? H[(long)row * n + col] : 0.0;
   }
 
-  // stage loader: Xs = X[t0:t0+KT, i0:i0+TI], Ys = X[t0:t0+KT, j0:j0+TJ] (zero outside)
-  float4 px[4], py[2];
+  // Stage loader: Xs = X[t0:t0+KT, i0:i0+TI], Ys = Y[t0:t0+KT, j0:j0+TJ] (zero outside). The job's
+  // pointers come from memory, so they are cast to the global address space explicitly: generic
+  // (flat) loads would share the LDS wait counter and stall every LDS read behind them.
+  const gfloat* Xg = (const gfloat*)X;
+  const gfloat* Yg = (const gfloat*)Y;
+  f4v px[4], py[2];
+  unsigned okm = 0;  // bit q (X) / 4 + q (Y): the slot lies inside the matrix
+  // VEC4 (n % 4 == 0): every thread always issues its 16-byte loads, from an address clamped into
+  // the matrix, and slots outside are zeroed only when written to LDS; no branches or selects sit
+  // between the loads and the matrix-core loop, so the prefetch of the next stage stays in flight.
+  auto ld4 = [&](const gfloat* base, int t, int c, int bit) -> f4v {
+    if (VEC4) {
+      okm |= (t < T && c < n) ? (1u << bit) : 0u;
+      return *(const gf4v*)(base + (long)min(t, T - 1) * n + min(c, n - 4));
+    }
+    f4v v = {0.f, 0.f, 0.f, 0.f};
+    if (t < T) {
+      const gfloat* p = base + (long)t * n + c;
+      if (c < n) v.x = p[0];
+      if (c + 1 < n) v.y = p[1];
+      if (c + 2 < n) v.z = p[2];
+      if (c + 3 < n) v.w = p[3];
+    }
+    return v;
+  };
   auto gload = [&](int t0) {
+    okm = 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int e = tid + 256 * q;  // 0..1023 float4 slots of the 32 x 128 tile
-      const int kk = e >> 5, c4 = (e & 31) * 4;
-      const int t = t0 + kk, c = i0 + c4;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (t < T) {
-        const float* p = X + (long)t * n + c;
-        if (VEC4 && c + 3 < n) {
-          v = *reinterpret_cast<const float4*>(p);
-        } else {
-          if (c < n) v.x = p[0];
-          if (c + 1 < n) v.y = p[1];
-          if (c + 2 < n) v.z = p[2];
-          if (c + 3 < n) v.w = p[3];
-        }
-      }
-      px[q] = v;
+      px[q] = ld4(Xg, t0 + (e >> 5), i0 + (e & 31) * 4, q);
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int e = tid + 256 * q;  // 0..511 float4 slots of the 32 x 64 tile
-      const int kk = e >> 4, c4 = (e & 15) * 4;
-      const int t = t0 + kk, c = j0 + c4;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (t < T) {
-        const float* p = Y + (long)t * n + c;
-        if (VEC4 && c + 3 < n) {
-          v = *reinterpret_cast<const float4*>(p);
-        } else {
-          if (c < n) v.x = p[0];
-          if (c + 1 < n) v.y = p[1];
-          if (c + 2 < n) v.z = p[2];
-          if (c + 3 < n) v.w = p[3];
-        }
-      }
-      py[q] = v;
+      py[q] = ld4(Yg, t0 + (e >> 4), j0 + (e & 15) * 4, 4 + q);
     }
+  };
+  auto keep = [&](f4v v, int bit) -> f4v {
+    if (!VEC4 || ((okm >> bit) & 1u)) return v;
+    return f4v{0.f, 0.f, 0.f, 0.f};
   };
   auto lstore = [&](int buf) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int e = tid + 256 * q;
-      *reinterpret_cast<float4*>(&Xs[buf][e >> 5][(e & 31) * 4]) = px[q];
+      *reinterpret_cast<f4v*>(&Xs[buf][e >> 5][(e & 31) * 4]) = keep(px[q], q);
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int e = tid + 256 * q;
-      *reinterpret_cast<float4*>(&Ys[buf][e >> 4][(e & 15) * 4]) = py[q];
+      *reinterpret_cast<f4v*>(&Ys[buf][e >> 4][(e & 15) * 4]) = keep(py[q], 4 + q);
     }
   };
 
