@@ -154,9 +154,14 @@ __global__ __launch_bounds__(256) void k_fold(long count, int np, const float* _
   G[idx] = g;
 }
 
-constexpr int RPW = 4;  // rows per wave in the refit kernel (16 rows per workgroup share H_CC in LDS)
+// Closed-form f16 scale refit of group gi (src/engine.rs:543-587). One wavefront advances RW rows
+// together (columns over lanes), so every H_CC element read from LDS feeds RW independent chains;
+// H_CC is staged once per workgroup as a zero-padded WP x WP tile.
+template <int NPL>
+constexpr int refit_rows_per_wave() {
+  return NPL <= 2 ? 4 : 1;
+}
 
-// Closed-form f16 scale refit of group gi (src/engine.rs:543-587).
 template <int NPL, bool LDSH>
 __global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, int gi, int rc, const float* __restrict__ G,
                                                const float* __restrict__ h32,
@@ -164,72 +169,132 @@ __global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, i
                                                const float* __restrict__ zeros, float* __restrict__ wq,
                                                float* __restrict__ e, const uint8_t* __restrict__ active,
                                                double* __restrict__ dlog, uint32_t* __restrict__ dcnt) {
-  extern __shared__ float hcc[];  // H_CC (wd x wd) when LDSH
+  constexpr int RW = refit_rows_per_wave<NPL>();
+  constexpr int WP = 64 * NPL;
+  extern __shared__ float hcc[];  // H_CC, WP x WP (zero outside wd x wd) when LDSH
   const int c0 = gi * g, wd = min(c0 + g, n) - c0;
   const int lane = threadIdx.x & 63;
-  const int rbase = blockIdx.x * 4 * RPW;
   if (LDSH) {
-    for (int x = threadIdx.x; x < wd * wd; x += 256) hcc[x] = h32[(long)(c0 + x / wd) * n + c0 + x % wd];
+    constexpr int PER = WP * WP / 256;
+    constexpr int BATCH = PER < 16 ? PER : 16;
+#pragma unroll
+    for (int b = 0; b < PER; b += BATCH) {
+      float v[BATCH];
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) {  // clamped addresses: every load is unconditional
+        const int x = threadIdx.x + 256 * (b + u);
+        const int k = x / WP, k2 = x % WP;
+        v[u] = h32[(long)(c0 + min(k, wd - 1)) * n + c0 + min(k2, wd - 1)];
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep the whole batch of loads in flight before any use
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) {
+        const int x = threadIdx.x + 256 * (b + u);
+        hcc[x] = (x / WP < wd && x % WP < wd) ? v[u] : 0.0f;
+      }
+    }
     __syncthreads();
   }
-  for (int q = 0; q < RPW; ++q) {
-    const int r = __builtin_amdgcn_readfirstlane(rbase + q * 4 + (threadIdx.x >> 6));
-    if (r >= rows) break;
-    if (!active[r / rc]) {
-      if (lane == 0) dcnt[r] = 0;
-      continue;
-    }
-    const float z = zeros[(long)r * ng + gi];
-    const float s_old = scales[(long)r * ng + gi];
-    float uu[NPL], gg[NPL], cvh[NPL], acc[NPL];
+  const int rbase = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (threadIdx.x >> 6)) * RW);
+  bool live[RW];
+  bool any = false;
+#pragma unroll
+  for (int q = 0; q < RW; ++q) {
+    const int r = rbase + q;
+    live[q] = r < rows && active[r / rc];
+    any = any || live[q];
+    if (r < rows && !live[q] && lane == 0) dcnt[r] = 0;
+  }
+  if (!any) return;
+
+  float uu[RW][NPL], gg[RW][NPL], acc[RW][NPL], cvh[RW][NPL];
+#pragma unroll
+  for (int q = 0; q < RW; ++q) {
+    const int r = rbase + q;
+    const float z = live[q] ? zeros[(long)r * ng + gi] : 0.0f;
 #pragma unroll
     for (int s = 0; s < NPL; ++s) {
       const int k = s * 64 + lane;
-      uu[s] = (k < wd) ? (float)codes[(long)r * n + c0 + k] - z : 0.0f;
-      gg[s] = (k < wd) ? G[(long)r * wd + k] : 0.0f;
-      cvh[s] = 0.0f;
-      acc[s] = 0.0f;
+      const bool in = live[q] && k < wd;
+      uu[q][s] = in ? (float)codes[(long)r * n + c0 + k] - z : 0.0f;
+      gg[q][s] = in ? G[(long)r * wd + k] : 0.0f;
+      acc[q][s] = 0.0f;
+      cvh[q][s] = 0.0f;
     }
-    // hu[k2] = sum_k uu[k] * H[c0+k][c0+k2] (sgemm at src/engine.rs:560, KC-panelled)
+  }
+  // hu[k2] = sum_k uu[k] * H[c0+k][c0+k2] (sgemm at src/engine.rs:560: fma chain per KC panel)
+  auto hu_step = [&](int k, int s1, int kl) {
+    float h[NPL];
 #pragma unroll
-    for (int s1 = 0; s1 < NPL; ++s1) {
-      for (int kk = 0; kk < 64; ++kk) {
-        const int k = s1 * 64 + kk;
-        if (k >= wd) break;
-        const float uk = readlane(uu[s1], kk);
+    for (int s2 = 0; s2 < NPL; ++s2) {
+      const int k2 = s2 * 64 + lane;
+      if (LDSH)
+        h[s2] = hcc[k * WP + k2];
+      else
+        h[s2] = k2 < wd ? h32[(long)(c0 + k) * n + c0 + k2] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < RW; ++q) {
+      const float uk = readlane(uu[q][s1], kl);
+#pragma unroll
+      for (int s2 = 0; s2 < NPL; ++s2) acc[q][s2] = __builtin_fmaf(uk, h[s2], acc[q][s2]);
+    }
+  };
+#pragma unroll
+  for (int s1 = 0; s1 < NPL; ++s1) {
+    const int kb = s1 * 64;
+    if (kb >= wd) break;
+    const int cnt = min(64, wd - kb);
+    if (cnt == 64) {
+#pragma unroll 16
+      for (int kl = 0; kl < 64; ++kl) hu_step(kb + kl, s1, kl);
+    } else {
+      for (int kl = 0; kl < cnt; ++kl) hu_step(kb + kl, s1, kl);
+    }
+    if (((kb + 64) % CDCLQ_KC) == 0 || kb + cnt == wd) {  // panel end: C = fma(1, chain, C)
+#pragma unroll
+      for (int q = 0; q < RW; ++q)
 #pragma unroll
         for (int s2 = 0; s2 < NPL; ++s2) {
-          const int k2 = s2 * 64 + lane;
-          if (k2 < wd) {
-            const float hv = LDSH ? hcc[k * wd + k2] : h32[(long)(c0 + k) * n + c0 + k2];
-            acc[s2] = __builtin_fmaf(uk, hv, acc[s2]);
-          }
+          cvh[q][s2] = __builtin_fmaf(1.0f, acc[q][s2], cvh[q][s2]);
+          acc[q][s2] = 0.0f;
         }
-        if (((k + 1) % CDCLQ_KC) == 0 || k + 1 == wd) {
-#pragma unroll
-          for (int s2 = 0; s2 < NPL; ++s2) {
-            cvh[s2] = __builtin_fmaf(1.0f, acc[s2], cvh[s2]);
-            acc[s2] = 0.0f;
-          }
-        }
-      }
     }
-    float num = 0.0f, den = 0.0f;
+  }
+  // num = sum_k u_k g_k, den = sum_k u_k hu_k, sequential in k (src/engine.rs:562-566)
+  float num[RW], den[RW];
 #pragma unroll
-    for (int s1 = 0; s1 < NPL; ++s1) {
-      for (int kk = 0; kk < 64; ++kk) {
-        const int k = s1 * 64 + kk;
-        if (k >= wd) break;
-        const float uk = readlane(uu[s1], kk);
-        num = num + uk * readlane(gg[s1], kk);
-        den = den + uk * readlane(cvh[s1], kk);
-      }
+  for (int q = 0; q < RW; ++q) num[q] = den[q] = 0.0f;
+  auto nd_step = [&](int s1, int kl) {
+#pragma unroll
+    for (int q = 0; q < RW; ++q) {
+      const float uk = readlane(uu[q][s1], kl);
+      num[q] = num[q] + uk * readlane(gg[q][s1], kl);
+      den[q] = den[q] + uk * readlane(cvh[q][s1], kl);
     }
+  };
+#pragma unroll
+  for (int s1 = 0; s1 < NPL; ++s1) {
+    const int kb = s1 * 64;
+    if (kb >= wd) break;
+    const int cnt = min(64, wd - kb);
+    if (cnt == 64) {
+#pragma unroll 16
+      for (int kl = 0; kl < 64; ++kl) nd_step(s1, kl);
+    } else {
+      for (int kl = 0; kl < cnt; ++kl) nd_step(s1, kl);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < RW; ++q) {
+    if (!live[q]) continue;
+    const int r = rbase + q;
+    const float s_old = scales[(long)r * ng + gi];
     uint32_t moved = 0;
-    if (den > 1e-30f) {
-      const float s_new = rs_maxf(round_f16(s_old + num / den), CDCLQ_F16_MIN_NORMAL);
+    if (den[q] > 1e-30f) {
+      const float s_new = rs_maxf(round_f16(s_old + num[q] / den[q]), CDCLQ_F16_MIN_NORMAL);
       const float d = s_new - s_old;
-      const float dl32 = (-2.0f * d) * num + (d * d) * den;
+      const float dl32 = (-2.0f * d) * num[q] + (d * d) * den[q];
       if ((double)dl32 < 0.0) {
         if (lane == 0) {
           scales[(long)r * ng + gi] = s_new;
@@ -240,7 +305,7 @@ __global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, i
           const int k = s * 64 + lane;
           if (k < wd) {
             const long o = (long)r * n + c0 + k;
-            const float ndq = s_new * uu[s];
+            const float ndq = s_new * uu[q][s];
             e[o] = e[o] + (wq[o] - ndq);
             wq[o] = ndq;
           }
@@ -375,10 +440,6 @@ hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, i
                        const float* h32, const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
                        const uint8_t* active, double* dlog, uint32_t* dcnt) {
   const int wd = std::min(gi * g + g, n) - gi * g;
-  const dim3 grid((rows + 4 * RPW - 1) / (4 * RPW)), blk(256);
-#define REFIT_CASE(N, L)                                                                                               \
-  hipLaunchKernelGGL((k_refit<N, L>), grid, blk, (L) ? (size_t)wd * wd * 4 : 0, st, rows, n, ng, g, gi, rc, G, h32,    \
-                     codes, scales, zeros, wq, e, active, dlog, dcnt)
   static bool lds_raised = false;  // 64 KB of dynamic LDS for H_CC at wd = 128
   if (!lds_raised) {
     const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_refit<2, true>),
@@ -386,6 +447,13 @@ hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, i
     if (err != hipSuccess) return err;
     lds_raised = true;
   }
+#define REFIT_CASE(N, L)                                                                                               \
+  do {                                                                                                                 \
+    constexpr int rows_per_wg = 4 * refit_rows_per_wave<N>();                                                        \
+    const size_t lds = (L) ? (size_t)(64 * N) * (64 * N) * 4 : 0;                                                      \
+    hipLaunchKernelGGL((k_refit<N, L>), dim3((rows + rows_per_wg - 1) / rows_per_wg), dim3(256), lds, st, rows, n, ng, \
+                       g, gi, rc, G, h32, codes, scales, zeros, wq, e, active, dlog, dcnt);                            \
+  } while (0)
   switch (npl_for(wd)) {
     case 1: REFIT_CASE(1, true); break;
     case 2: REFIT_CASE(2, true); break;
