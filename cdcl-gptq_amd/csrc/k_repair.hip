@@ -9,9 +9,9 @@
 // each one 4-block accumulator (block b = cols 16b..16b+15); E and the panel of H are staged in
 // double-buffered LDS, 16 k at a time.
 //
-// Sweeps. One wavefront per row (columns spread over lanes, wave-uniform column loop). The refit
-// needs all of H_CC for every row, so a workgroup of 16 rows stages it in LDS when it fits; the
-// descent touches a row of H_sb only when a code moves and reads it from L2.
+// Sweeps. One wavefront per row, columns spread over lanes. The refit needs all of H_CC for every
+// row, so a workgroup of 16 rows stages it in LDS when it fits; the descent evaluates all columns of
+// a sub-block at once and touches a row of H_sb only when a code moves, reading it from L2.
 #include <algorithm>
 
 #include "cdclq_dev.h"
@@ -317,7 +317,14 @@ __global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, i
   }
 }
 
-// Coordinate-descent sweeps over sub-block [c0, c0+wd) (src/engine.rs:600-658); one wave per row.
+// Coordinate-descent sweeps over sub-block [c0, c0+wd) (src/engine.rs:600-658); one wave per row,
+// one column per lane. The reference visits the columns one after another and a column's decision
+// depends on the gradient left by the moves before it. Every lane evaluates its own column's
+// decision with the current gradient (the same IEEE operations the sequential visit would do);
+// the lowest column at or after the cursor whose code changes is the next move of the sequential
+// order, since the columns before it saw exactly this gradient and kept their codes. The move is
+// applied (gradient update over the whole sub-block, wave-parallel), the cursor jumps past it and
+// the columns after it are evaluated again. A sweep therefore costs one round per move plus one.
 template <int NPL>
 __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
                                             int sweeps, const float* __restrict__ G, const float* __restrict__ h32,
@@ -334,57 +341,63 @@ __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int 
     if (lane == 0) dcnt[r] = 0;
     return;
   }
-  float gg[NPL], mwq[NPL], me[NPL];
+  // per-column state and parameters, one column per lane and slice
+  float gg[NPL], mwq[NPL], me[NPL], hd[NPL], sc[NPL], zz[NPL], mq[NPL];
   int mc[NPL];
 #pragma unroll
   for (int s = 0; s < NPL; ++s) {
     const int k = s * 64 + lane;
-    const long o = (long)r * n + c0 + k;
-    gg[s] = (k < wd) ? G[(long)r * wd + k] : 0.0f;
-    mwq[s] = (k < wd) ? wq[o] : 0.0f;
-    me[s] = (k < wd) ? e[o] : 0.0f;
-    mc[s] = (k < wd) ? (int)codes[o] : 0;
+    const bool in = k < wd;
+    const int j = c0 + min(k, wd - 1);
+    const long o = (long)r * n + j;
+    const int gi = j / g;
+    gg[s] = in ? G[(long)r * wd + k] : 0.0f;
+    mwq[s] = in ? wq[o] : 0.0f;
+    me[s] = in ? e[o] : 0.0f;
+    mc[s] = in ? (int)codes[o] : 0;
+    hd[s] = h32[(long)j * n + j];
+    sc[s] = scales[(long)r * ng + gi];
+    zz[s] = zeros[(long)r * ng + gi];
+    mq[s] = (float)((1u << gbits[gi]) - 1u);
   }
   uint32_t moves = 0;
   double* dl = dlog + (long)r * cap;
   for (int sw = 0; sw < sweeps; ++sw) {
-    int changed = 0;
+    bool changed = false;
 #pragma unroll
     for (int s = 0; s < NPL; ++s) {
-      for (int ii = 0; ii < 64; ++ii) {
-        const int jj = s * 64 + ii;
-        if (jj >= wd) break;
-        const int j = c0 + jj;
-        const int gi = j / g;
-        const float maxq = (float)((1u << gbits[gi]) - 1u);
-        const float sc = scales[(long)r * ng + gi];
-        const float z = zeros[(long)r * ng + gi];
-        const float hjj = h32[(long)j * n + j];
-        const float cur = readlane(mwq[s], ii);
-        const float gj = readlane(gg[s], ii);
-        const int code = __builtin_amdgcn_readlane(mc[s], ii);
-        const float target = cur + gj / hjj;
+      const bool in = s * 64 + lane < wd;
+      int start = 0;
+      while (start < 64) {
+        // this lane's column, visited now: target = w_hat_j + g_j / H_jj (src/engine.rs:626-640)
+        const float target = mwq[s] + gg[s] / hd[s];
         float qv;
-        const float newdq = quant_dq(target, sc, z, maxq, &qv);
+        const float newdq = quant_dq(target, sc[s], zz[s], mq[s], &qv);
         const int qc = (int)code_of(qv);
-        if (qc != code) {
-          const float de = cur - newdq;
-          const float d32 = (2.0f * de) * gj + (de * de) * hjj;
-          if (lane == 0) dl[moves] = (double)d32;
-          ++moves;
-          const float* hrow = h32 + (long)j * n + c0;
+        const uint64_t mask = __ballot(in && lane >= start && qc != mc[s]);
+        if (mask == 0) break;
+        const int jl = __builtin_amdgcn_readfirstlane(__builtin_ctzll(mask));
+        const float cur = readlane(mwq[s], jl);
+        const float nd = readlane(newdq, jl);
+        const float gj = readlane(gg[s], jl);
+        const float hjj = readlane(hd[s], jl);
+        const float de = cur - nd;
+        const float d32 = (2.0f * de) * gj + (de * de) * hjj;
+        if (lane == 0) dl[moves] = (double)d32;
+        ++moves;
+        const float* hrow = h32 + (long)(c0 + s * 64 + jl) * n + c0;
 #pragma unroll
-          for (int s2 = 0; s2 < NPL; ++s2) {
-            const int k = s2 * 64 + lane;
-            if (k < wd) gg[s2] = gg[s2] + de * hrow[k];
-          }
-          if (lane == ii) {
-            mwq[s] = newdq;
-            mc[s] = qc;
-            me[s] = me[s] + de;
-          }
-          changed = 1;
+        for (int s2 = 0; s2 < NPL; ++s2) {
+          const int k = s2 * 64 + lane;
+          if (k < wd) gg[s2] = gg[s2] + de * hrow[k];
         }
+        if (lane == jl) {
+          mwq[s] = nd;
+          mc[s] = qc;
+          me[s] = me[s] + de;
+        }
+        changed = true;
+        start = jl + 1;
       }
     }
     if (!changed) break;
