@@ -64,7 +64,9 @@ __global__ __launch_bounds__(256) void k_gemm(int m, int n, int k, T alpha, int 
         kk = e >> 6;
       }
       const int gi = i0 + ii, gk = k0 + kk;
-      As[kk][ii] = (gi < m && gk < kend) ? A[(long)gi * rsa + (long)gk * csa] : T(0);
+      // past the end of k: A = -0, B = +0, so the padded step fma(-0, +0, c) = c + (-0) = c is exact
+      // for every c, -0 included (a chain can reach -0 through underflow)
+      As[kk][ii] = (gi < m && gk < kend) ? A[(long)gi * rsa + (long)gk * csa] : T(-0.0);
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {

@@ -73,12 +73,12 @@ __global__ __launch_bounds__(256, 2) void k_gram_mfma(const GramJob* __restrict_
   // VEC4 (n % 4 == 0): every thread always issues its 16-byte loads, from an address clamped into
   // the matrix, and slots outside are zeroed only when written to LDS; no branches or selects sit
   // between the loads and the matrix-core loop, so the prefetch of the next stage stays in flight.
-  auto ld4 = [&](const gfloat* base, int t, int c, int bit) -> f4v {
+  auto ld4 = [&](const gfloat* base, int t, int c, int bit, float pad) -> f4v {
     if (VEC4) {
       okm |= (t < T && c < n) ? (1u << bit) : 0u;
       return *(const gf4v*)(base + (long)min(t, T - 1) * n + min(c, n - 4));
     }
-    f4v v = {0.f, 0.f, 0.f, 0.f};
+    f4v v = {pad, pad, pad, pad};
     if (t < T) {
       const gfloat* p = base + (long)t * n + c;
       if (c < n) v.x = p[0];
@@ -93,28 +93,30 @@ __global__ __launch_bounds__(256, 2) void k_gram_mfma(const GramJob* __restrict_
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int e = tid + 256 * q;  // 0..1023 float4 slots of the 32 x 128 tile
-      px[q] = ld4(Xg, t0 + (e >> 5), i0 + (e & 31) * 4, q);
+      px[q] = ld4(Xg, t0 + (e >> 5), i0 + (e & 31) * 4, q, -0.0f);
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int e = tid + 256 * q;  // 0..511 float4 slots of the 32 x 64 tile
-      py[q] = ld4(Yg, t0 + (e >> 4), j0 + (e & 15) * 4, 4 + q);
+      py[q] = ld4(Yg, t0 + (e >> 4), j0 + (e & 15) * 4, 4 + q, 0.0f);
     }
   };
-  auto keep = [&](f4v v, int bit) -> f4v {
+  // Slots outside the matrix: X is -0 and Y is +0, so a padded token adds fma(-0, +0, c) = c + (-0),
+  // which leaves every chain value unchanged (a chain can reach -0 through underflow).
+  auto keep = [&](f4v v, int bit, float pad) -> f4v {
     if (!VEC4 || ((okm >> bit) & 1u)) return v;
-    return f4v{0.f, 0.f, 0.f, 0.f};
+    return f4v{pad, pad, pad, pad};
   };
   auto lstore = [&](int buf) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int e = tid + 256 * q;
-      *reinterpret_cast<f4v*>(&Xs[buf][e >> 5][(e & 31) * 4]) = keep(px[q], q);
+      *reinterpret_cast<f4v*>(&Xs[buf][e >> 5][(e & 31) * 4]) = keep(px[q], q, -0.0f);
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int e = tid + 256 * q;
-      *reinterpret_cast<f4v*>(&Ys[buf][e >> 4][(e & 15) * 4]) = keep(py[q], 4 + q);
+      *reinterpret_cast<f4v*>(&Ys[buf][e >> 4][(e & 15) * 4]) = keep(py[q], 4 + q, 0.0f);
     }
   };
 

@@ -3,16 +3,16 @@
 //
 // Gradient. The reference computes G with matrixmultiply (k = n): per element a fused chain over
 // each KC = 256 panel of k, panels folded in order. k_panel_gemm computes every panel's chain in
-// parallel with v_mfma_f32_16x16x1_4b_f32 (K = 1, single rounding per product, bit-identical to
+// parallel with v_mfma_f32_32x32x1_2b_f32 (K = 1, single rounding per product, bit-identical to
 // fmaf) and stores the per-panel values; k_fold then folds them in panel order, one thread per
-// element. Workgroup: 256 rows x 64 cols x one panel; wave w owns 64 rows as four 16-row groups,
-// each one 4-block accumulator (block b = cols 16b..16b+15); E and the panel of H are staged in
-// double-buffered LDS, 16 k at a time.
+// element. Workgroup: 128 rows x 64 cols x one panel, E and the panel of H staged in
+// double-buffered LDS.
 //
 // Sweeps. One wavefront per row, columns spread over lanes. The refit needs all of H_CC for every
 // row, so a workgroup of 16 rows stages it in LDS when it fits; the descent evaluates all columns of
 // a sub-block at once and touches a row of H_sb only when a code moves, reading it from L2.
 #include <algorithm>
+#include <cstdint>
 
 #include "cdclq_dev.h"
 #include "kernels.h"
@@ -22,58 +22,85 @@ namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int PR = 256;  // rows per panel-GEMM workgroup
+typedef float v32f __attribute__((ext_vector_type(32)));
+
+constexpr int PR = 128;  // rows per panel-GEMM workgroup (32 per wave)
 constexpr int PC = 64;   // cols per panel-GEMM workgroup
 
-__device__ __forceinline__ v16f mfma16(float a, float b, v16f c) {
-  return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0);
+__device__ __forceinline__ v32f mfma32(float a, float b, v32f c) {
+  return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, 0);
 }
 
-constexpr int SK = 16;        // k per LDS stage
-constexpr int ES = SK + 4;     // padded row stride of the E stage (16-byte aligned, conflict-free b128 reads)
-
-template <bool VEC4>
-__global__ __launch_bounds__(256, 2) void k_panel_gemm(int m, int wd, int k, const float* __restrict__ A, long lda,
-                                                       const float* __restrict__ B, long ldb, float* __restrict__ P) {
-  __shared__ float Es[2][PR * ES];  // E[r0:r0+256, k-slice], row-major, padded
-  __shared__ float Hs[2][SK * PC];  // B[k-slice, cb:cb+64]
-  const int p = blockIdx.y;
-  const int k0 = p * CDCLQ_KC;
-  const int kc = min(CDCLQ_KC, k - k0);
-  const int r0 = blockIdx.x * PR;
-  const int cb = blockIdx.z * PC;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  // global -> register prefetch of one stage: 8 float4 of E (256 rows x 32 k), 2 float4 of B (32 x 64)
+// Work unit: 128 rows x 64 cols x one KC panel. Wave w owns rows 32w..32w+31 as one
+// v_mfma_f32_32x32x1_2b accumulator whose two blocks are the column halves: lanes i and 32 + i
+// supply A row i, lane L supplies B column L. SK = k per LDS stage; the E stage is row-major with
+// a padded stride (16-byte aligned rows, conflict-free b128 reads), the B stage is k-major.
+//
+// The grid is sized to the resident workgroup slots and each workgroup walks a contiguous range
+// of units (panels fastest, so consecutive units continue along the same E rows). The stage
+// pipeline runs across unit boundaries: the first stage of the next unit is loaded while the last
+// stage of the current one is multiplied, and the accumulator is written out and cleared between
+// them, so no workgroup pays a cold start per panel.
+template <int SK, bool VEC4>
+__global__ __launch_bounds__(256) void k_panel_gemm(int m, int wd, int k, const float* __restrict__ A, long lda,
+                                                    const float* __restrict__ B, long ldb, float* __restrict__ P,
+                                                    int nunits) {
+  constexpr int ES = SK + 4;
   constexpr int EQ = PR * SK / 4 / 256;  // float4 of E per thread per stage
   constexpr int HQ = SK * PC / 4 / 256;  // float4 of B per thread per stage
   constexpr int K4 = SK / 4;             // float4 per E row per stage
+  static_assert(EQ >= 1 && HQ >= 1, "stage too small for the workgroup");
+  __shared__ float Es[2][PR * ES];
+  __shared__ float Hs[2][SK * PC];
+  const int np = (k + CDCLQ_KC - 1) / CDCLQ_KC;
+  const int nrt = (m + PR - 1) / PR;
+  const int u0 = (int)((long)blockIdx.x * nunits / gridDim.x);
+  const int u1 = (int)((long)(blockIdx.x + 1) * nunits / gridDim.x);
+  if (u0 >= u1) return;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  struct Unit {
+    int r0, cb, p, k0, kc, nst;
+  };
+  auto unit = [&](int u) {
+    Unit t;
+    const int ct = u / (nrt * np), rem = u % (nrt * np);
+    t.r0 = (rem / np) * PR;
+    t.p = rem % np;
+    t.cb = ct * PC;
+    t.k0 = t.p * CDCLQ_KC;
+    t.kc = min(CDCLQ_KC, k - t.k0);
+    t.nst = (t.kc + SK - 1) / SK;
+    return t;
+  };
   float4 pe[EQ], ph[HQ];
-  auto gload = [&](int ks) {
+  // VEC4: unconditional 16-byte loads from clamped addresses (rows >= m only feed outputs that are
+  // never stored; k slots past the panel are replaced below); otherwise guarded scalar loads.
+  auto gload = [&](const Unit& t, int ks) {
 #pragma unroll
     for (int q = 0; q < EQ; ++q) {
-      const int e = tid + 256 * q;  // row = e / K4, k4 = (e % K4) * 4
-      const int r = r0 + e / K4, kk = ks + (e % K4) * 4;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (r < m) {
-        const float* src = A + (long)r * lda + k0 + kk;
-        if (VEC4 && kk + 3 < kc) {
-          v = *reinterpret_cast<const float4*>(src);
-        } else {
-          if (kk < kc) v.x = src[0];
-          if (kk + 1 < kc) v.y = src[1];
-          if (kk + 2 < kc) v.z = src[2];
-          if (kk + 3 < kc) v.w = src[3];
+      const int e = tid + 256 * q;
+      const int r = t.r0 + e / K4, kk = ks + (e % K4) * 4;
+      if (VEC4) {
+        pe[q] = *reinterpret_cast<const float4*>(A + (long)min(r, m - 1) * lda + t.k0 + min(kk, t.kc - 4));
+      } else {
+        float4 v = make_float4(-0.f, -0.f, -0.f, -0.f);
+        if (r < m) {
+          const float* src = A + (long)r * lda + t.k0 + kk;
+          if (kk < t.kc) v.x = src[0];
+          if (kk + 1 < t.kc) v.y = src[1];
+          if (kk + 2 < t.kc) v.z = src[2];
+          if (kk + 3 < t.kc) v.w = src[3];
         }
+        pe[q] = v;
       }
-      pe[q] = v;
     }
 #pragma unroll
     for (int q = 0; q < HQ; ++q) {
       const int e = tid + 256 * q;  // kk = e >> 4, c4 = (e & 15) * 4
-      const int kk = ks + (e >> 4), c = cb + (e & 15) * 4;
+      const int kk = ks + (e >> 4), c = t.cb + (e & 15) * 4;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (kk < kc) {
-        const float* src = B + (long)(k0 + kk) * ldb + c;
+      if (kk < t.kc) {
+        const float* src = B + (long)(t.k0 + kk) * ldb + c;
         if (c < wd) v.x = src[0];
         if (c + 1 < wd) v.y = src[1];
         if (c + 2 < wd) v.z = src[2];
@@ -82,11 +109,16 @@ __global__ __launch_bounds__(256, 2) void k_panel_gemm(int m, int wd, int k, con
       ph[q] = v;
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf, const Unit& t, int ks) {
 #pragma unroll
     for (int q = 0; q < EQ; ++q) {
       const int e = tid + 256 * q;
-      *reinterpret_cast<float4*>(&Es[buf][(e / K4) * ES + (e % K4) * 4]) = pe[q];
+      float4 v = pe[q];
+      // k is a multiple of 4 under VEC4, so a slot is either wholly inside the panel or wholly past
+      // its end (then the clamped load read other data). Past the end, E is -0 and B is +0: the
+      // step fma(-0, +0, c) = c + (-0) = c leaves every chain value unchanged, -0 included.
+      if (VEC4 && ks + (e % K4) * 4 >= t.kc) v = make_float4(-0.f, -0.f, -0.f, -0.f);
+      *reinterpret_cast<float4*>(&Es[buf][(e / K4) * ES + (e % K4) * 4]) = v;
     }
 #pragma unroll
     for (int q = 0; q < HQ; ++q) {
@@ -94,45 +126,54 @@ __global__ __launch_bounds__(256, 2) void k_panel_gemm(int m, int wd, int k, con
       *reinterpret_cast<float4*>(&Hs[buf][(e >> 4) * PC + (e & 15) * 4]) = ph[q];
     }
   };
-  v16f acc[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) acc[q] = v16f{};
-  const int nst = (kc + SK - 1) / SK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int s = 0; s < nst; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < nst) gload((s + 1) * SK);
-    const float* es = &Es[buf][(64 * wv + (lane & 15)) * ES];
+  v32f acc = {};
+  auto compute = [&](int buf) {
+    const float* es = &Es[buf][(32 * wv + (lane & 31)) * ES];
     const float* hs = &Hs[buf][lane];
 #pragma unroll
     for (int k4 = 0; k4 < SK; k4 += 4) {
-      float4 a[4];
+      const float4 a = *reinterpret_cast<const float4*>(es + k4);
+      acc = mfma32(a.x, hs[(k4 + 0) * PC], acc);
+      acc = mfma32(a.y, hs[(k4 + 1) * PC], acc);
+      acc = mfma32(a.z, hs[(k4 + 2) * PC], acc);
+      acc = mfma32(a.w, hs[(k4 + 3) * PC], acc);
+    }
+  };
+  int u = u0, s = 0, buf = 0;
+  Unit cur = unit(u);
+  gload(cur, 0);
+  lstore(0, cur, 0);
+  __syncthreads();
+  while (true) {
+    // the stage after (u, s) in this workgroup's sequence
+    int un = u, sn = s + 1;
+    Unit nxt = cur;
+    if (sn >= cur.nst) {
+      un = u + 1;
+      sn = 0;
+      if (un < u1) nxt = unit(un);
+    }
+    const bool more = un < u1;
+    if (more) gload(nxt, sn * SK);
+    compute(buf);
+    if (sn == 0) {  // (u, s) was the unit's last stage: write its chains and start the next
+      // block b = r >> 4 (cols 32b..), row i = (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), col j = lane & 31
 #pragma unroll
-      for (int q = 0; q < 4; ++q) a[q] = *reinterpret_cast<const float4*>(es + 16 * q * ES + k4);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float b = hs[(k4 + u) * PC];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float av = u == 0 ? a[q].x : u == 1 ? a[q].y : u == 2 ? a[q].z : a[q].w;
-          acc[q] = mfma16(av, b, acc[q]);
-        }
+      for (int r = 0; r < 32; ++r) {
+        const int row = cur.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
+        const int col = cur.cb + 32 * (r >> 4) + (lane & 31);
+        if (row < m && col < wd) P[((long)cur.p * m + row) * wd + col] = acc[r];
       }
+      acc = v32f{};
     }
-    if (s + 1 < nst) lstore(buf ^ 1);
+    if (!more) break;
+    lstore(buf ^ 1, nxt, sn * SK);
     __syncthreads();
+    buf ^= 1;
+    u = un;
+    s = sn;
+    cur = nxt;
   }
-  // D_b[i][j] at reg 4b + (i&3), lane j + 16*(i>>2): row 16q + i, col 16b + j
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int row = r0 + 64 * wv + 16 * q + 4 * (lane >> 4) + (j & 3);
-      const int col = cb + 16 * (j >> 2) + (lane & 15);
-      if (row < m && col < wd) P[((long)p * m + row) * wd + col] = acc[q][j];
-    }
 }
 
 // G[r][c] = ordered fold of the panel chains (alpha 1, beta 0): C = fma(1, P_p, C) for p = 0, 1, ...
@@ -433,12 +474,30 @@ size_t panel_partials_elems(int m, int wd, int k) {
 hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long lda, const float* B, long ldb,
                       float* P) {
   if (m <= 0 || wd <= 0 || k <= 0) return hipSuccess;
-  const dim3 grid((m + PR - 1) / PR, (k + CDCLQ_KC - 1) / CDCLQ_KC, (wd + PC - 1) / PC);
-  const bool vec4 = (lda % 4 == 0) && ((uintptr_t)A % 16 == 0);
+  const bool vec4 = (lda % 4 == 0) && ((uintptr_t)A % 16 == 0) && k % 4 == 0;
+  constexpr int SK = 32;
+  const long nunits = (long)((m + PR - 1) / PR) * ((k + CDCLQ_KC - 1) / CDCLQ_KC) * ((wd + PC - 1) / PC);
+  if (nunits > INT32_MAX) return hipErrorInvalidValue;
+  // one workgroup per resident slot (occupancy is a property of the kernel, cached per process)
+  static int slots[2] = {0, 0};
+  int& sl = slots[vec4 ? 1 : 0];
+  if (sl == 0) {
+    int dev = 0, cus = 0, per = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err == hipSuccess)
+      err = vec4 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_panel_gemm<SK, true>, 256, 0)
+                 : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_panel_gemm<SK, false>, 256, 0);
+    if (err != hipSuccess) return err;
+    sl = std::max(1, cus * std::max(1, per));
+  }
+  const int grid = (int)std::min<long>(nunits, sl);
   if (vec4)
-    hipLaunchKernelGGL(k_panel_gemm<true>, grid, dim3(256), 0, st, m, wd, k, A, lda, B, ldb, P);
+    hipLaunchKernelGGL((k_panel_gemm<SK, true>), dim3(grid), dim3(256), 0, st, m, wd, k, A, lda, B, ldb, P,
+                       (int)nunits);
   else
-    hipLaunchKernelGGL(k_panel_gemm<false>, grid, dim3(256), 0, st, m, wd, k, A, lda, B, ldb, P);
+    hipLaunchKernelGGL((k_panel_gemm<SK, false>), dim3(grid), dim3(256), 0, st, m, wd, k, A, lda, B, ldb, P,
+                       (int)nunits);
   return hipGetLastError();
 }
 
