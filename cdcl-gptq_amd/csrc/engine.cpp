@@ -232,7 +232,7 @@ int factor(cdclq_ctx* ctx, int n, double* a, double* y, float* u) {
     double* t = P<double>(ctx->tbuf);
     // t = L[s:e, 0:s] Y[0:s, 0:s]; Y[s:e, 0:s] = -Y_ss t  (src/linalg.rs:307-343)
     HIPCK(gemm_chain<double>(st, w, s, s, 1.0, 0, a + (long)s * n, n, 1, y, n, 1, t, s, 1, false,
-                             s > 256 ? P<double>(ctx->tpart) : nullptr));
+                             s > 256 ? P<double>(ctx->tpart) : nullptr, /*b_lower_tri=*/true));
     HIPCK(gemm_chain<double>(st, w, s, w, -1.0, 0, y + (long)s * n + s, n, 1, t, s, 1, y + (long)s * n, n, 1, false,
                              (double*)nullptr));
   }

@@ -48,79 +48,146 @@ __global__ __launch_bounds__(256) void k_build_flipped_f64(int n, const double* 
   a[idx] = h[nn - 1 - idx];
 }
 
-// Unblocked factorisation of the diagonal block (src/linalg.rs:209-229).
+// Unblocked factorisation of the diagonal block (src/linalg.rs:209-229). The reference works by
+// columns (left-looking): d = a_jj - sum_{t<j} l_jt l_jt, l_jj = sqrt(d), then
+// l_ij = (a_ij - sum_{t<j} l_it l_jt) / l_jj, every term a separate multiply and subtract in t
+// order. Applying the subtraction of column t to the whole trailing triangle as soon as column t
+// is final (right-looking) performs exactly the same operations on every element in the same
+// order, with the trailing triangle updated in parallel.
+//
+// Element (i, j) lives in a register of thread (i % 16, j % 16) of a 16 x 16 thread grid for the
+// whole factorisation (2-D cyclic, so every step's trailing triangle is spread over all threads).
+// Per step t: the pivot and the divisions of column t run one per thread from the LDS copy of the
+// column (pre), then every thread applies column t to its elements (slot rows and columns that lie
+// wholly before t are skipped by the wave); the owners of column t + 1 copy it to LDS for the next
+// step.
+constexpr int DS = NBC / 16;  // row / column slots per thread
 __global__ __launch_bounds__(256) void k_chol_diag(int n, double* __restrict__ a, int k, int kb, int* status,
                                                    double* pivot) {
-  __shared__ double L[NBC][NBC + 1];
-  __shared__ int fail;
+  __shared__ double pre[NBC];  // column t with all earlier columns applied, before the division
+  __shared__ double col[NBC];  // column t of L
   if (*status) return;
-  const int tid = threadIdx.x;
-  for (int e = tid; e < kb * kb; e += 256) {
-    const int i = e / kb, j = e % kb;
-    L[i][j] = (j <= i) ? a[(long)(k + i) * n + k + j] : 0.0;
-  }
-  if (tid == 0) fail = 0;
+  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
+  const int wrow_max = 4 * ((tid >> 6) + 1) - 1;  // the wave's largest tr
+  double v[DS][DS];
+#pragma unroll
+  for (int r = 0; r < DS; ++r)
+#pragma unroll
+    for (int c = 0; c < DS; ++c) {
+      const int i = 16 * r + tr, j = 16 * c + tc;
+      v[r][c] = a[(long)(k + min(i, kb - 1)) * n + k + min(j, kb - 1)];
+    }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < DS; ++r)
+#pragma unroll
+    for (int c = 0; c < DS; ++c) {
+      const int i = 16 * r + tr, j = 16 * c + tc;
+      if (!(i < kb && j <= i)) v[r][c] = 0.0;
+      if (j == 0 && i < kb) pre[i] = v[r][c];
+    }
   __syncthreads();
-  for (int j = 0; j < kb; ++j) {
-    if (tid == 0) {
-      double d = L[j][j];
-      for (int t = 0; t < j; ++t) {
-        const double v = L[j][t];
-        d = d - v * v;
-      }
-      if (!(d > 0.0) || !isfinite(d)) {
-        fail = 1;
-        *status = k + j + 1;
+  for (int t = 0; t < kb; ++t) {
+    const double d = pre[t];  // every thread reads the same pivot: the branch below is uniform
+    if (!(d > 0.0) || !isfinite(d)) {
+      if (tid == 0) {
+        *status = k + t + 1;
         *pivot = d;
-      } else {
-        L[j][j] = sqrt(d);
+      }
+      return;
+    }
+    const double ltt = sqrt(d);
+    if (tid == t) col[t] = ltt;
+    if (tid > t && tid < kb) col[tid] = pre[tid] / ltt;
+    __syncthreads();
+    double ci[DS], cj[DS];
+#pragma unroll
+    for (int q = 0; q < DS; ++q) {
+      ci[q] = col[16 * q + tr];
+      cj[q] = col[16 * q + tc];
+    }
+#pragma unroll
+    for (int r = 0; r < DS; ++r) {
+      if (16 * r + wrow_max < t) continue;  // the wave's rows in this slot are all finished
+#pragma unroll
+      for (int c = 0; c < DS; ++c) {
+        if (16 * c + 15 < t) continue;  // all columns of this slot are finished
+        const int i = 16 * r + tr, j = 16 * c + tc;
+        if (i < kb && i >= t) {
+          if (j == t)
+            v[r][c] = ci[r];
+          else if (j > t && j <= i)
+            v[r][c] = v[r][c] - ci[r] * cj[c];
+          if (j == t + 1 && j <= i) pre[i] = v[r][c];
+        }
       }
     }
     __syncthreads();
-    if (fail) return;
-    const double dj = L[j][j];
-    for (int i = j + 1 + tid; i < kb; i += 256) {
-      double s = L[i][j];
-      for (int t = 0; t < j; ++t) s = s - L[i][t] * L[j][t];
-      L[i][j] = s / dj;
+  }
+#pragma unroll
+  for (int r = 0; r < DS; ++r)
+#pragma unroll
+    for (int c = 0; c < DS; ++c) {
+      const int i = 16 * r + tr, j = 16 * c + tc;
+      if (i < kb && j <= i) a[(long)(k + i) * n + k + j] = v[r][c];
     }
-    __syncthreads();
-  }
-  for (int e = tid; e < kb * kb; e += 256) {
-    const int i = e / kb, j = e % kb;
-    if (j <= i) a[(long)(k + i) * n + k + j] = L[i][j];
-  }
 }
 
-// Panel solve X L_kk^T = A_panel for all rows below the block (src/linalg.rs:233-241).
+// Panel solve X L_kk^T = A_panel for all rows below the block (src/linalg.rs:233-241). One wave
+// advances PANEL_RPW rows together (columns over lanes), so the LDS reads of L and the long
+// divisions of the rows overlap.
 constexpr int PANEL_RPW = 4;  // rows per wave
 __global__ __launch_bounds__(256) void k_chol_panel(int n, double* __restrict__ a, int k, int kb,
                                                     const int* status) {
   __shared__ double LT[NBC][NBC + 1];  // LT[t][j] = L[j][t]
   if (*status) return;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  for (int e = tid; e < kb * kb; e += 256) {
-    const int j = e / kb, t = e % kb;
-    LT[t][j] = (t <= j) ? a[(long)(k + j) * n + k + t] : 0.0;
+  {  // stage the block with all of a thread's loads in flight at once
+    constexpr int PER = NBC * NBC / 256;
+    double v[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = tid + 256 * q, j = e / NBC, t = e % NBC;
+      v[q] = a[(long)(k + min(j, kb - 1)) * n + k + min(t, kb - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = tid + 256 * q, j = e / NBC, t = e % NBC;
+      LT[t][j] = (t <= j && j < kb) ? v[q] : 0.0;
+    }
   }
   __syncthreads();
   const int kend = k + kb;
+  const int i0 = kend + (blockIdx.x * 4 + wv) * PANEL_RPW;
+  double s0[PANEL_RPW], s1[PANEL_RPW];
+#pragma unroll
   for (int q = 0; q < PANEL_RPW; ++q) {
-    const int i = kend + (blockIdx.x * PANEL_RPW + q) * 4 + wv;
+    const int i = min(i0 + q, n - 1);  // rows past the end are computed but never stored
+    const double* row = a + (long)i * n + k;
+    s0[q] = (lane < kb) ? row[lane] : 0.0;
+    s1[q] = (lane + 64 < kb) ? row[lane + 64] : 0.0;
+  }
+  for (int t = 0; t < kb; ++t) {
+    const double ltt = LT[t][t];
+    const double l0 = LT[t][lane], l1 = (lane + 64 < NBC) ? LT[t][lane + 64] : 0.0;
+#pragma unroll
+    for (int q = 0; q < PANEL_RPW; ++q) {
+      const double st = (t < 64) ? readlane_f64(s0[q], t) : readlane_f64(s1[q], t - 64);
+      const double xt = st / ltt;
+      if (lane == t) s0[q] = xt;
+      if (lane + 64 == t) s1[q] = xt;
+      if (lane > t && lane < kb) s0[q] = s0[q] - xt * l0;
+      if (lane + 64 > t && lane + 64 < kb) s1[q] = s1[q] - xt * l1;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < PANEL_RPW; ++q) {
+    const int i = i0 + q;
     if (i >= n) break;
     double* row = a + (long)i * n + k;
-    double s0 = (lane < kb) ? row[lane] : 0.0;
-    double s1 = (lane + 64 < kb) ? row[lane + 64] : 0.0;
-    for (int t = 0; t < kb; ++t) {
-      const double st = (t < 64) ? readlane_f64(s0, t) : readlane_f64(s1, t - 64);
-      const double xt = st / LT[t][t];
-      if (lane == t) s0 = xt;
-      if (lane + 64 == t) s1 = xt;
-      if (lane > t && lane < kb) s0 = s0 - xt * LT[t][lane];
-      if (lane + 64 > t && lane + 64 < kb) s1 = s1 - xt * LT[t][lane + 64];
-    }
-    if (lane < kb) row[lane] = s0;
-    if (lane + 64 < kb) row[lane + 64] = s1;
+    if (lane < kb) row[lane] = s0[q];
+    if (lane + 64 < kb) row[lane + 64] = s1[q];
   }
 }
 

@@ -20,10 +20,15 @@ __device__ __forceinline__ double fma_t(double a, double b, double c) { return _
 
 // 64x64 output tile per 256-thread workgroup, 4x4 per thread, k staged through LDS in steps of
 // KT (KT divides KC, so panel ends coincide with stage ends).
+//
+// b_tri: B is lower triangular (B[k][c] = +0 for k < c). Every product before the first nonzero
+// row of the tile's columns is fma(a, +0, +0) = +0 on a chain that is still +0, and a panel made
+// only of such products folds to +0, so the tile starts its k loop at its first column (rounded
+// down to a stage, which keeps the panel ends on stage ends) with identical results.
 template <typename T, bool SPLIT, bool LOWER>
 __global__ __launch_bounds__(256) void k_gemm(int m, int n, int k, T alpha, int beta_one, const T* __restrict__ A,
                                               long rsa, long csa, const T* __restrict__ B, long rsb, long csb,
-                                              T* __restrict__ C, long rsc, long csc, T* __restrict__ P) {
+                                              T* __restrict__ C, long rsc, long csc, T* __restrict__ P, int b_tri) {
   __shared__ T As[KT][BM + 4];
   __shared__ T Bs[KT][BN + 4];
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
@@ -34,6 +39,8 @@ __global__ __launch_bounds__(256) void k_gemm(int m, int n, int k, T alpha, int 
     kbeg = blockIdx.z * CDCLQ_KC;
     kend = min(k, kbeg + CDCLQ_KC);
   }
+  // the k loop starts at kfirst; the panel bookkeeping still counts from kbeg
+  const int kfirst = b_tri ? max(kbeg, (j0 / KT) * KT) : kbeg;
   T acc[4][4], cv[4][4];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
@@ -51,7 +58,7 @@ __global__ __launch_bounds__(256) void k_gemm(int m, int n, int k, T alpha, int 
         if (gi < m && gj < n) cv[a][b] = C[(long)gi * rsc + (long)gj * csc];
       }
   }
-  for (int k0 = kbeg; k0 < kend; k0 += KT) {
+  for (int k0 = kfirst; k0 < kend; k0 += KT) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int e = tid + 256 * q;
@@ -145,7 +152,10 @@ size_t gemm_partials_elems(int m, int n, int k) {
 
 template <typename T>
 hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, int beta_one, const T* A, long rsa, long csa,
-                      const T* B, long rsb, long csb, T* C, long rsc, long csc, bool lower, T* partials) {
+                      const T* B, long rsb, long csb, T* C, long rsc, long csc, bool lower, T* partials,
+                      bool b_lower_tri) {
+  // the zero-prefix skip relies on C starting at +0, i.e. beta == 0
+  const int bt = (b_lower_tri && !beta_one) ? 1 : 0;
   if (m <= 0 || n <= 0) return hipSuccess;
   if (k <= 0) {
     // k == 0: C = beta * C (src/linalg.rs:82-91); beta in {0, 1}
@@ -161,7 +171,7 @@ hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, int beta_one
     dim3 g3 = grid;
     g3.z = np;
     hipLaunchKernelGGL((k_gemm<T, true, false>), g3, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa, B, rsb,
-                       csb, C, rsc, csc, partials);
+                       csb, C, rsc, csc, partials, bt);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((k_combine<T>), dim3((unsigned)(((long)m * n + 255) / 256)), dim3(256), 0, st, m, n, np, alpha,
@@ -170,16 +180,16 @@ hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, int beta_one
   }
   if (lower)
     hipLaunchKernelGGL((k_gemm<T, false, true>), grid, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa, B,
-                       rsb, csb, C, rsc, csc, (T*)nullptr);
+                       rsb, csb, C, rsc, csc, (T*)nullptr, bt);
   else
     hipLaunchKernelGGL((k_gemm<T, false, false>), grid, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa, B,
-                       rsb, csb, C, rsc, csc, (T*)nullptr);
+                       rsb, csb, C, rsc, csc, (T*)nullptr, bt);
   return hipGetLastError();
 }
 
 template hipError_t gemm_chain<float>(hipStream_t, int, int, int, float, int, const float*, long, long, const float*,
-                                      long, long, float*, long, long, bool, float*);
+                                      long, long, float*, long, long, bool, float*, bool);
 template hipError_t gemm_chain<double>(hipStream_t, int, int, int, double, int, const double*, long, long,
-                                       const double*, long, long, double*, long, long, bool, double*);
+                                       const double*, long, long, double*, long, long, bool, double*, bool);
 
 }  // namespace cdclq

@@ -16,7 +16,8 @@ namespace cdclq {
 // non-null, panels run in parallel into partials[npanel][m][n] and are combined in panel order.
 template <typename T>
 hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, int beta_one, const T* A, long rsa, long csa,
-                      const T* B, long rsb, long csb, T* C, long rsc, long csc, bool lower, T* partials);
+                      const T* B, long rsb, long csb, T* C, long rsc, long csc, bool lower, T* partials,
+                      bool b_lower_tri = false);
 size_t gemm_partials_elems(int m, int n, int k);
 
 // ---- k_gram.hip: H (n x n, f64) += X^T Y over 2048-token chunks on the matrix cores.
