@@ -7,7 +7,7 @@ inputs of q/k/v, o, gate/up and down) and 7 quantize_layer calls (INT4, g128, B1
 damp 0.01, repair on with the reference defaults), with the factor cache shared by q/k/v and by
 gate/up as in the reference pipeline. Inputs (X, W) are generated in HBM before the timed region.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4|c1] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4|c1] [--no-cpu-baseline] [--profile-gram]
 
 Prints one JSON line (rank 0). The CPU baseline is the C restatement of the reference (oracle/)
 timed on a bounded sample of the same workload on this host and extrapolated (see `sample`).
@@ -103,6 +103,45 @@ def cpu_baseline(spec: dict, cores: int) -> dict:
             "phases_s": {"gram": round(gram_full, 2), "factor": round(fac_full, 2), "quant": round(quant_full, 2)}}
 
 
+def recorded_traffic(config: str):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated against a copy of known size); None if not recorded."""
+    path = os.path.join(ROOT, "profiles", f"gram_{config}_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def profile_gram(ctx, spec, xs, h64s):
+    """One calibration copy of known size, then one batched gram launch (for rocprofv3 --pmc)."""
+    import ctypes
+    import cdclq
+    nbytes = 1 << 30
+    src = cdclq.DeviceArray(ctx, (nbytes // 4,), np.float32)
+    dst = cdclq.DeviceArray(ctx, (nbytes // 4,), np.float32)
+    src.zero()
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    rc = hip.hipMemcpy(dst.ptr, src.ptr, nbytes, 3)  # hipMemcpyDeviceToDevice: one copy kernel
+    if rc != 0 or hip.hipDeviceSynchronize() != 0:
+        raise RuntimeError(f"calibration copy failed ({rc})")
+    keys = list(spec["inputs"])
+    for key in keys:
+        h64s[key].zero()
+    T = spec["tokens"]
+    cdclq.gram_accumulate_batch_device(ctx, [xs[k] for k in keys], [xs[k] for k in keys], [T] * len(keys),
+                                       [spec["inputs"][k] for k in keys], [h64s[k] for k in keys])
+    x_bytes = sum(T * n * 4 for n in spec["inputs"].values())
+    h_bytes = sum(n * n * 8 for n in spec["inputs"].values())
+    print(json.dumps({"profile": "gram", "workload": spec["workload"], "calibration_copy_bytes": nbytes,
+                      "algorithmic_read_bytes": x_bytes + h_bytes, "algorithmic_write_bytes": h_bytes}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -110,6 +149,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-gram", action="store_true",
+                    help="counter-collection run: one 1 GiB device-to-device copy (calibration of the HBM "
+                         "byte counters), then one launch of the dominant kernel on this config's inputs")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
@@ -130,6 +172,10 @@ def main():
         ctx.check(cdclq.lib().cdclq_synth_tokens_device(ctx.ptr, 2000 + 7 * i, 0, T, n, cs.ctypes.data, xs[key].ptr))
         h64s[key] = cdclq.DeviceArray(ctx, (n, n), np.float64)
         h32s[key] = cdclq.DeviceArray(ctx, (n, n), np.float32)
+    if args.profile_gram:
+        profile_gram(ctx, spec, xs, h64s)
+        ctx.close()
+        return
     ws, outs = {}, {}
     cfg = cdclq.Config(**spec["cfg"])
     for li, (name, d_out, key) in enumerate(spec["layers"]):
@@ -209,7 +255,8 @@ def main():
             "peak": FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": recorded_traffic(args.config),
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, profiles/gram_c4_traffic.md)",
             "launches": gram_launches,
         },
     }
