@@ -228,55 +228,80 @@ __global__ __launch_bounds__(256) void k_sub(long count, const float* __restrict
 
 // Per-chunk loss bookkeeping of one pass, in the reference's order (src/engine.rs:583, :640):
 // steps in execution order (refit groups, then CD sub-blocks), within a step rows ascending,
-// within a row its accepted deltas in the order they were made. One wave per chunk: the wave
-// gathers 64 rows' logged deltas into LDS in that order, then folds them sequentially in f64.
+// within a row its accepted deltas in the order they were made. One workgroup per chunk. For each
+// step and batch of up to 256 rows the workgroup scans the rows' delta counts, gathers the deltas
+// into LDS in fold order (every output position finds its row by binary search over the scanned
+// offsets, so all loads are independent), and wave 0 folds them sequentially in f64.
 constexpr int ACC_LDS = 4096;
-__global__ __launch_bounds__(64) void k_pass_accum(int rows, int rc, int nref, const double* __restrict__ rlog,
-                                                   const uint32_t* __restrict__ rcnt, int ncd, int cap,
-                                                   const double* __restrict__ clog,
-                                                   const uint32_t* __restrict__ ccnt,
-                                                   const uint8_t* __restrict__ active, double* __restrict__ ld,
-                                                   uint64_t* __restrict__ upd) {
+__global__ __launch_bounds__(256) void k_pass_accum(int rows, int rc, int nref, const double* __restrict__ rlog,
+                                                    const uint32_t* __restrict__ rcnt, int ncd, int cap,
+                                                    const double* __restrict__ clog,
+                                                    const uint32_t* __restrict__ ccnt,
+                                                    const uint8_t* __restrict__ active, double* __restrict__ ld,
+                                                    uint64_t* __restrict__ upd) {
   __shared__ double vals[ACC_LDS];
+  __shared__ uint32_t offs[257];  // exclusive offsets of the batch's rows; offs[nr] = total
+  __shared__ uint32_t wsum[4];
   const int c = blockIdx.x;
   if (!active[c]) return;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int r0 = c * rc, r1 = min(rows, r0 + rc);
-  double acc = ld[c];
+  double acc = ld[c];  // meaningful in wave 0
   uint64_t u = upd[c];
   for (int step = 0; step < nref + ncd; ++step) {
     const bool refit = step < nref;
     const long sbase = refit ? (long)step * rows : (long)(step - nref) * rows;
     const uint32_t* cnt = refit ? rcnt : ccnt;
-    for (int base = r0; base < r1; base += 64) {
-      const int r = base + lane;
-      const uint32_t k = (r < r1) ? cnt[sbase + r] : 0u;
-      // exclusive prefix sum of k over the lanes
+    for (int base = r0; base < r1; base += 256) {
+      const int nr = min(256, r1 - base);
+      const int r = base + tid;
+      const uint32_t k = (tid < nr) ? cnt[sbase + r] : 0u;
+      // workgroup exclusive scan of k
       uint32_t incl = k;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const uint32_t v = __shfl_up(incl, o, 64);
         if (lane >= o) incl += v;
       }
-      const uint32_t total = __shfl(incl, 63, 64);
-      if (total == 0) continue;
-      const uint32_t off = incl - k;
+      if (lane == 63) wsum[wv] = incl;
+      __syncthreads();
+      uint32_t before = 0;
+      for (int w = 0; w < wv; ++w) before += wsum[w];
+      const uint32_t total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+      offs[tid] = before + incl - k;
+      if (tid == 0) offs[nr] = total;  // nr <= 256; entries past nr are never searched
+      __syncthreads();
+      if (total == 0) continue;  // uniform
       u += total;
       for (uint32_t done = 0; done < total; done += ACC_LDS) {
-        // rows whose deltas fall in [done, done + ACC_LDS) copy them in order
-        for (uint32_t q = 0; q < k; ++q) {
-          const uint32_t pos = off + q;
-          if (pos >= done && pos < done + ACC_LDS)
-            vals[pos - done] = refit ? rlog[sbase + r] : clog[(sbase + r) * cap + q];
+        const uint32_t m = min((uint32_t)ACC_LDS, total - done);
+        for (uint32_t i = tid; i < m; i += 256) {
+          const uint32_t pos = done + i;
+          int lo = 0, hi = nr;  // largest j in [0, nr) with offs[j] <= pos
+          while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (offs[mid] <= pos) lo = mid; else hi = mid;
+          }
+          const long rr = sbase + base + lo;
+          vals[i] = refit ? rlog[rr] : clog[rr * cap + (pos - offs[lo])];
         }
         __syncthreads();
-        const uint32_t m = min((uint32_t)ACC_LDS, total - done);
-        for (uint32_t i = 0; i < m; ++i) acc = acc + vals[i];
+        if (wv == 0) {
+          uint32_t i = 0;
+          for (; i + 8 <= m; i += 8) {
+            double v[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) v[q] = vals[i + q];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) acc = acc + v[q];
+          }
+          for (; i < m; ++i) acc = acc + vals[i];
+        }
         __syncthreads();
       }
     }
   }
-  if (lane == 0) {
+  if (tid == 0) {
     ld[c] = acc;
     upd[c] = u;
   }
@@ -388,7 +413,7 @@ hipError_t sub_f32(hipStream_t st, size_t count, const float* a, const float* b,
 hipError_t pass_accum(hipStream_t st, int rows, int rc, int nchunks, int nref, const double* rlog,
                       const uint32_t* rcnt, int ncd, int cap, const double* clog, const uint32_t* ccnt,
                       const uint8_t* active, double* ld, uint64_t* upd) {
-  hipLaunchKernelGGL(k_pass_accum, dim3(nchunks), dim3(64), 0, st, rows, rc, nref, rlog, rcnt, ncd, cap, clog, ccnt,
+  hipLaunchKernelGGL(k_pass_accum, dim3(nchunks), dim3(256), 0, st, rows, rc, nref, rlog, rcnt, ncd, cap, clog, ccnt,
                      active, ld, upd);
   return hipGetLastError();
 }
