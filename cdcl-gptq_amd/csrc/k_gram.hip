@@ -88,7 +88,31 @@ __global__ __launch_bounds__(256, 2) void k_gram_mfma(const GramJob* __restrict_
     }
     return v;
   };
+  // Interior tiles with whole stages (all of config 4) take a lean path: a uniform stage base plus
+  // per-lane offsets fixed for the whole launch, so a stage's six loads cost no vector ALU work.
+  const bool interior = VEC4 && i0 + TI <= n && j0 + TJ <= n;
+  int offx[4], offy[2];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = tid + 256 * q;
+    offx[q] = (e >> 5) * n + i0 + (e & 31) * 4;
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int e = tid + 256 * q;
+    offy[q] = (e >> 4) * n + j0 + (e & 15) * 4;
+  }
   auto gload = [&](int t0) {
+    if (interior && t0 + KT <= T) {
+      okm = 0x3f;
+      const gfloat* xst = Xg + (long)t0 * n;
+      const gfloat* yst = Yg + (long)t0 * n;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) px[q] = *(const gf4v*)(xst + offx[q]);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) py[q] = *(const gf4v*)(yst + offy[q]);
+      return;
+    }
     okm = 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
