@@ -595,32 +595,39 @@ int gram_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const f
   std::vector<int> flags(4 * jobs.size());
   HIPCK(hipMemcpyAsync(flags.data(), ctx->status_d.p, flags.size() * 4, hipMemcpyDeviceToHost, st));
   HIPCK(hipStreamSynchronize(st));
-  std::vector<int4> tiles;
-  for (size_t i = 0; i < jobs.size(); ++i)
-    gram_mfma_tiles((int)i, jobs[i].n, jobs[i].x == jobs[i].y && flags[4 * i] == 0, tiles);
+  // Jobs whose tiles are all interior go to the direct-to-LDS kernel, the rest to k_gram_mfma.
+  std::vector<int4> tiles[2];
+  for (size_t i = 0; i < jobs.size(); ++i) {
+    const int kind = gram_dma_eligible(jobs[i].n, jobs[i].t, jobs[i].x, jobs[i].y) ? 1 : 0;
+    gram_mfma_tiles((int)i, jobs[i].n, jobs[i].x == jobs[i].y && flags[4 * i] == 0, tiles[kind]);
+  }
   // XCD-aware order: workgroup w runs on XCD w % 8, so give each XCD a contiguous run of tiles
   // (neighbouring tiles share X stripes in that XCD's L2).
-  {
-    const size_t nx = 8, m = tiles.size();
+  for (auto& tl : tiles) {
+    const size_t nx = 8, m = tl.size();
     std::vector<int4> ord(m);
     const size_t per = (m + nx - 1) / nx;
     size_t w = 0;
     for (size_t k = 0; k < per; ++k)
       for (size_t x = 0; x < nx; ++x) {
         const size_t src = x * per + k;
-        if (src < m) ord[w++] = tiles[src];
+        if (src < m) ord[w++] = tl[src];
       }
-    tiles.swap(ord);
+    tl.swap(ord);
   }
-  CK(ensure(ctx, ctx->tiles_d, tiles.size() * sizeof(int4) + jobs.size() * sizeof(GramJob) + 64));
+  const size_t ntile = tiles[0].size() + tiles[1].size();
+  CK(ensure(ctx, ctx->tiles_d, ntile * sizeof(int4) + jobs.size() * sizeof(GramJob) + 64));
   char* base = P<char>(ctx->tiles_d);
   GramJob* djobs = reinterpret_cast<GramJob*>(base);
   int4* dtiles = reinterpret_cast<int4*>(base + ((jobs.size() * sizeof(GramJob) + 63) / 64) * 64);
   HIPCK(hipMemcpyAsync(djobs, jobs.data(), jobs.size() * sizeof(GramJob), hipMemcpyHostToDevice, st));
-  HIPCK(hipMemcpyAsync(dtiles, tiles.data(), tiles.size() * sizeof(int4), hipMemcpyHostToDevice, st));
+  HIPCK(hipMemcpyAsync(dtiles, tiles[0].data(), tiles[0].size() * sizeof(int4), hipMemcpyHostToDevice, st));
+  HIPCK(hipMemcpyAsync(dtiles + tiles[0].size(), tiles[1].data(), tiles[1].size() * sizeof(int4),
+                       hipMemcpyHostToDevice, st));
   {
     PhaseScope ps(ctx, CDCLQ_PHASE_GRAM);
-    HIPCK(gram_mfma(st, djobs, dtiles, (int)tiles.size(), vec4));
+    HIPCK(gram_mfma(st, djobs, dtiles, (int)tiles[0].size(), vec4));
+    HIPCK(gram_dma(st, djobs, dtiles + tiles[0].size(), (int)tiles[1].size()));
   }
   HIPCK(hipStreamSynchronize(st));
   return CDCLQ_OK;

@@ -188,6 +188,109 @@ __global__ __launch_bounds__(256, 2) void k_gram_mfma(const GramJob* __restrict_
   }
 }
 
+// Direct-to-LDS variant for jobs whose tiles are all interior and whose token count is a multiple
+// of KT (n % 128 == 0, T % 32 == 0, 16-byte aligned rows; every config-4 input). The workgroup's
+// stages are filled with global_load_lds_dwordx4 (lane L's 16 bytes land at the instruction's LDS
+// base + 16 L), so no registers hold prefetched data and no LDS stores are issued; a ring of DNB
+// stages keeps two stages in flight behind the one being multiplied, with one barrier per stage.
+// Arithmetic, per-element operation order, panel and chunk folds are those of k_gram_mfma.
+constexpr int DNB = 3;                   // stages in the ring
+constexpr int DSTAGE = KT * (TI + TJ);   // floats per stage: X [32][128], Y [32][64]
+constexpr int DPW = DSTAGE / 256 / 4;    // 1 KB load instructions per wave and stage (6)
+
+__device__ __forceinline__ void dma16(const float* g, float* lds) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                   (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) with expcnt / lgkmcnt unconstrained (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+__global__ __launch_bounds__(256, 2) void k_gram_dma(const GramJob* __restrict__ jobs,
+                                                     const int4* __restrict__ tiles) {
+  __shared__ float R[DNB][DSTAGE];
+  const int4 tl = tiles[blockIdx.x];
+  const GramJob jb = jobs[tl.x];
+  const int n = jb.n, T = jb.t;
+  __attribute__((address_space(1))) double* H = (__attribute__((address_space(1))) double*)jb.h;
+  const int i0 = tl.y * TI, j0 = tl.z * TJ;
+  const bool mirror = tl.w != 0;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wi = wv >> 1, wj = wv & 1;
+  const int rbase = i0 + 64 * wi + 4 * (lane >> 5);
+  const int col = j0 + 32 * wj + (lane & 31);
+  double h[32];
+#pragma unroll
+  for (int r = 0; r < 32; ++r) h[r] = H[(long)(rbase + 32 * (r >> 4) + 8 * ((r & 15) >> 2) + (r & 3)) * n + col];
+  // Stage layout: X [32 tokens][128 cols] (instructions 0..15, two tokens each: lane -> token
+  // lane >> 5, columns 4 (lane & 31)), then Y [32][64] (instructions 16..23, four tokens each:
+  // lane -> token lane >> 4, columns 4 (lane & 15)). Wave w issues instructions w, w + 4, ...
+  const float* src[DPW];
+  int dst[DPW];
+#pragma unroll
+  for (int q = 0; q < DPW; ++q) {
+    const int ins = wv + 4 * q;
+    if (ins < 16) {
+      src[q] = jb.x + (long)(2 * ins + (lane >> 5)) * n + i0 + 4 * (lane & 31);
+      dst[q] = 256 * ins;
+    } else {
+      src[q] = jb.y + (long)(4 * (ins - 16) + (lane >> 4)) * n + j0 + 4 * (lane & 15);
+      dst[q] = 256 * ins;
+    }
+  }
+  const int nstage = T / KT;
+  auto issue = [&](int s) {
+    float* buf = &R[s % DNB][0];
+    const long t0n = (long)s * KT * n;
+#pragma unroll
+    for (int q = 0; q < DPW; ++q) dma16(src[q] + t0n, buf + dst[q]);
+  };
+  issue(0);
+  if (nstage > 1) issue(1);
+  v32f acc = {};
+  float tmp[32];
+#pragma unroll
+  for (int r = 0; r < 32; ++r) tmp[r] = 0.0f;
+  for (int s = 0; s < nstage; ++s) {
+    // this wave's part of stage s has landed once at most stage s + 1's loads are outstanding;
+    // the barrier then publishes every wave's part and retires all reads of stage s - 1
+    if (s + 1 < nstage)
+      wait_vmcnt<DPW>();
+    else
+      wait_vmcnt<0>();
+    // a bare barrier: a fenced one would also wait for the next stage's loads still in flight
+    __builtin_amdgcn_s_barrier();
+    if (s + 2 < nstage) issue(s + 2);  // into the buffer of stage s - 1
+    const float* xs = &R[s % DNB][64 * wi + lane];
+    const float* ys = &R[s % DNB][KT * TI + 32 * wj + (lane & 31)];
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) acc = mfma32(xs[kk * TI], ys[kk * TJ], acc);
+    const int tn = (s + 1) * KT;
+    if ((tn % CDCLQ_KC) == 0 || tn >= T) {  // panel end: tmp = fma(1, chain, tmp)
+#pragma unroll
+      for (int r = 0; r < 32; ++r) tmp[r] = __builtin_fmaf(1.0f, acc[r], tmp[r]);
+      acc = v32f{};
+      if ((tn % 2048) == 0 || tn >= T) {  // chunk end: h += (f64) tmp
+#pragma unroll
+        for (int r = 0; r < 32; ++r) {
+          h[r] += (double)tmp[r];
+          tmp[r] = 0.0f;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 32; ++r) {
+    const int row = rbase + 32 * (r >> 4) + 8 * ((r & 15) >> 2) + (r & 3);
+    H[(long)row * n + col] = h[r];
+    if (mirror) H[(long)col * n + row] = h[r];
+  }
+}
+
 // flag |= (h not bitwise symmetric)
 __global__ __launch_bounds__(256) void k_sym_check(int n, const double* __restrict__ h, int* flag) {
   const long idx = (long)blockIdx.x * 256 + threadIdx.x;
@@ -226,6 +329,16 @@ hipError_t gram_mfma(hipStream_t st, const GramJob* jobs, const int4* tiles, int
   else
     hipLaunchKernelGGL(k_gram_mfma<false>, dim3(ntiles), dim3(256), 0, st, jobs, tiles);
   return hipGetLastError();
+}
+
+hipError_t gram_dma(hipStream_t st, const GramJob* jobs, const int4* tiles, int ntiles) {
+  if (ntiles <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_gram_dma, dim3(ntiles), dim3(256), 0, st, jobs, tiles);
+  return hipGetLastError();
+}
+
+bool gram_dma_eligible(int n, int t, const void* x, const void* y) {
+  return n % 128 == 0 && t % KT == 0 && t > 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0;
 }
 
 hipError_t sym_check(hipStream_t st, int n, const double* h, int* flag) {

@@ -77,7 +77,8 @@ def test_synth_generator_matches_host(ctx):
 
 
 # ---------------------------------------------------------------- H accumulation
-@pytest.mark.parametrize("t,n", [(1, 8), (2047, 64), (2048, 100), (2049, 130), (4100, 96), (5000, 200)])
+@pytest.mark.parametrize("t,n", [(1, 8), (2047, 64), (2048, 100), (2049, 130), (4100, 96), (5000, 200),
+                                 (32, 128), (4128, 128), (2080, 384)])
 @pytest.mark.parametrize("sym", [True, False])
 def test_gram_bitexact(ctx, t, n, sym):
     rng = np.random.default_rng(t * 31 + n)
