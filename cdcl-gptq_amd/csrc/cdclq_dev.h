@@ -134,4 +134,30 @@ __device__ __host__ __forceinline__ float synth_normal_at(uint64_t seed, uint64_
   return (float)(r * synth_cos2pi(u2));
 }
 
+// ---- direct-to-LDS loads
+// global_load_lds_dwordx4: every lane reads 16 bytes at its own global address; lane L's bytes land
+// at lds + 16 L (lds is wave-uniform). Completion is counted by vmcnt like any vector load.
+__device__ __forceinline__ void dma16(const float* g, float* lds) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                   (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// The same load issued from inline assembly: the compiler then tracks no LDS write for it and adds
+// no wait of its own before later LDS reads (it would wait for every load in flight); the caller
+// orders the data with wait_vmcnt and a barrier. The memory clobber keeps the compiler from moving
+// LDS accesses across it; s_nop 0 covers the M0-write to LDS-DMA wait state.
+__device__ __forceinline__ void dma16_untracked(const float* g, float* lds) {
+  const uint32_t off = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)lds;
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(off);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0v)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) with expcnt / lgkmcnt unconstrained (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 }  // namespace cdclq

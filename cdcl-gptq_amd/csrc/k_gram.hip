@@ -198,18 +198,6 @@ constexpr int DNB = 3;                   // stages in the ring
 constexpr int DSTAGE = KT * (TI + TJ);   // floats per stage: X [32][128], Y [32][64]
 constexpr int DPW = DSTAGE / 256 / 4;    // 1 KB load instructions per wave and stage (6)
 
-__device__ __forceinline__ void dma16(const float* g, float* lds) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                   (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-}
-
-// s_waitcnt vmcnt(N) with expcnt / lgkmcnt unconstrained (gfx9 encoding)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
 __global__ __launch_bounds__(256, 2) void k_gram_dma(const GramJob* __restrict__ jobs,
                                                      const int4* __restrict__ tiles) {
   __shared__ float R[DNB][DSTAGE];

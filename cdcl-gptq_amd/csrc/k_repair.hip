@@ -176,6 +176,121 @@ __global__ __launch_bounds__(256) void k_panel_gemm(int m, int wd, int k, const 
   }
 }
 
+// Direct-to-LDS variant of k_panel_gemm, used when k % 32 == 0, wd % 4 == 0 and the rows of E and
+// H are 16-byte aligned. Stages are filled with global_load_lds_dwordx4 into a ring of three, two
+// stages in flight behind the one being multiplied, one bare barrier per stage; units, the MFMA
+// mapping and the outputs are those of k_panel_gemm. Stage layout: E as [128 rows][8 slots][4],
+// slot s of row r holding k-quad s ^ (r & 7) (load i: lane l -> row 8 i + (l >> 3), so each load
+// reads eight whole 128-byte row segments, and the XOR keeps the b128 reads of 32 rows free of bank
+// conflicts), then B as [32 k][64 cols] (load j: lane l -> k row 4 j + (l >> 4), columns
+// 4 (l & 15) .. +3). Rows past m and columns past wd are read from clamped addresses and only
+// reach outputs that are never stored.
+constexpr int DSK = 32;
+constexpr int DNB = 3;
+constexpr int DSTAGE = DSK * PR + DSK * PC;  // floats per stage (E 4096 + B 2048)
+constexpr int DPW = DSTAGE / 256 / 4;        // 1 KB loads per wave and stage (6)
+
+__global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const float* __restrict__ A, long lda,
+                                                   const float* __restrict__ B, long ldb, float* __restrict__ P,
+                                                   int nunits) {
+  __shared__ float R[DNB][DSTAGE];
+  const int np = k / CDCLQ_KC + (k % CDCLQ_KC != 0);
+  const int nrt = (m + PR - 1) / PR;
+  const int u0 = (int)((long)blockIdx.x * nunits / gridDim.x);
+  const int u1 = (int)((long)(blockIdx.x + 1) * nunits / gridDim.x);
+  if (u0 >= u1) return;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  struct Unit {
+    int r0, cb, p, k0, nst;
+  };
+  auto unit = [&](int u) {
+    Unit t;
+    const int ct = u / (nrt * np), rem = u % (nrt * np);
+    t.r0 = (rem / np) * PR;
+    t.p = rem % np;
+    t.cb = ct * PC;
+    t.k0 = t.p * CDCLQ_KC;
+    t.nst = min(CDCLQ_KC, k - t.k0) / DSK;
+    return t;
+  };
+  // issue cursor: unit iu_idx / stage is, ring slot fi % DNB
+  int iu_idx = u0, is = 0, fi = 0;
+  Unit iu = unit(u0);
+  bool ivalid = true;
+  auto issue_next = [&]() {
+    if (!ivalid) return;
+    float* buf = &R[fi % DNB][0];
+    const int ks = iu.k0 + is * DSK;
+#pragma unroll
+    for (int q = 0; q < DPW; ++q) {
+      const int ins = wv + 4 * q;
+      if (ins < 16) {  // E: rows 8 ins .. 8 ins + 7
+        const int rl = 8 * ins + (lane >> 3);
+        const int quad = (lane & 7) ^ (rl & 7);
+        const int row = min(iu.r0 + rl, m - 1);
+        dma16_untracked(A + (long)row * lda + ks + 4 * quad, buf + 256 * ins);
+      } else {  // B: k rows 4 j .. 4 j + 3
+        const int j = ins - 16;
+        const int c = min(iu.cb + 4 * (lane & 15), wd - 4);
+        dma16_untracked(B + (long)(ks + 4 * j + (lane >> 4)) * ldb + c, buf + DSK * PR + 256 * j);
+      }
+    }
+    ++fi;
+    if (++is >= iu.nst) {
+      if (++iu_idx < u1) {
+        iu = unit(iu_idx);
+        is = 0;
+      } else {
+        ivalid = false;
+      }
+    }
+  };
+  issue_next();
+  issue_next();
+  v32f acc = {};
+  int cu_idx = u0, cs = 0, fc = 0;
+  Unit cu = unit(u0);
+  bool stored = false;  // P stores of the previous stage may still be in flight
+  while (true) {
+    // this wave's part of stage fc has landed once at most the next stage's loads are outstanding
+    if (fi - fc >= 2 && !stored)
+      wait_vmcnt<DPW>();
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();  // publishes all parts; all reads of stage fc - 1 are done
+    issue_next();                  // into the slot of stage fc - 1
+    const float* buf = &R[fc % DNB][0];
+    const int er = 32 * wv + (lane & 31);
+    const float* es = buf + 32 * er;
+    const float* hs = buf + DSK * PR + lane;
+#pragma unroll
+    for (int q = 0; q < DSK / 4; ++q) {
+      const float4 a = *reinterpret_cast<const float4*>(es + 4 * (q ^ (er & 7)));
+      acc = mfma32(a.x, hs[(4 * q + 0) * PC], acc);
+      acc = mfma32(a.y, hs[(4 * q + 1) * PC], acc);
+      acc = mfma32(a.z, hs[(4 * q + 2) * PC], acc);
+      acc = mfma32(a.w, hs[(4 * q + 3) * PC], acc);
+    }
+    stored = false;
+    if (cs == cu.nst - 1) {  // the unit's last stage: write its chains and start the next unit
+#pragma unroll
+      for (int r = 0; r < 32; ++r) {
+        const int row = cu.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
+        const int col = cu.cb + 32 * (r >> 4) + (lane & 31);
+        if (row < m && col < wd) P[((long)cu.p * m + row) * wd + col] = acc[r];
+      }
+      acc = v32f{};
+      stored = true;
+      if (++cu_idx >= u1) break;
+      cu = unit(cu_idx);
+      cs = 0;
+    } else {
+      ++cs;
+    }
+    ++fc;
+  }
+}
+
 // G[r][c] = ordered fold of the panel chains (alpha 1, beta 0): C = fma(1, P_p, C) for p = 0, 1, ...
 // One thread per entry, panel loads unrolled so many are in flight.
 __global__ __launch_bounds__(256) void k_fold(long count, int np, const float* __restrict__ P, float* __restrict__ G) {
@@ -492,6 +607,21 @@ hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long
     sl = std::max(1, cus * std::max(1, per));
   }
   const int grid = (int)std::min<long>(nunits, sl);
+  const bool dma = vec4 && k % DSK == 0 && wd % 4 == 0 && wd >= 4 && ldb % 4 == 0 && (uintptr_t)B % 16 == 0;
+  if (dma) {
+    static int dslots = 0;
+    if (dslots == 0) {
+      int dev = 0, cus = 0, per = 0;
+      hipError_t err = hipGetDevice(&dev);
+      if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+      if (err == hipSuccess) err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_panel_dma, 256, 0);
+      if (err != hipSuccess) return err;
+      dslots = std::max(1, cus * std::max(1, per));
+    }
+    hipLaunchKernelGGL(k_panel_dma, dim3((int)std::min<long>(nunits, dslots)), dim3(256), 0, st, m, wd, k, A, lda,
+                       B, ldb, P, (int)nunits);
+    return hipGetLastError();
+  }
   if (vec4)
     hipLaunchKernelGGL((k_panel_gemm<SK, true>), dim3(grid), dim3(256), 0, st, m, wd, k, A, lda, B, ldb, P,
                        (int)nunits);
