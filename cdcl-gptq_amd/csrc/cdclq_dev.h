@@ -146,12 +146,15 @@ __device__ __forceinline__ void dma16(const float* g, float* lds) {
 // no wait of its own before later LDS reads (it would wait for every load in flight); the caller
 // orders the data with wait_vmcnt and a barrier. The memory clobber keeps the compiler from moving
 // LDS accesses across it; s_nop 0 covers the M0-write to LDS-DMA wait state.
-__device__ __forceinline__ void dma16_untracked(const float* g, float* lds) {
-  const uint32_t off = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)lds;
-  const uint32_t m0v = __builtin_amdgcn_readfirstlane(off);
+__device__ __forceinline__ void dma16_untracked(const float* g, uint32_t lds_byte_offset) {
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_byte_offset);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0v)
                : "memory", "m0");
 }
+
+// LDS byte offset of a generic pointer into LDS (the low 32 bits of a generic address in the LDS
+// aperture are the offset).
+__device__ __forceinline__ uint32_t lds_offset(const void* p) { return (uint32_t)(uintptr_t)p; }
 
 // s_waitcnt vmcnt(N) with expcnt / lgkmcnt unconstrained (gfx9 encoding)
 template <int N>

@@ -199,7 +199,8 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
   const int u0 = (int)((long)blockIdx.x * nunits / gridDim.x);
   const int u1 = (int)((long)(blockIdx.x + 1) * nunits / gridDim.x);
   if (u0 >= u1) return;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   struct Unit {
     int r0, cb, p, k0, nst;
   };
@@ -213,33 +214,43 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
     t.nst = min(CDCLQ_KC, k - t.k0) / DSK;
     return t;
   };
-  // issue cursor: unit iu_idx / stage is, ring slot fi % DNB
+  const uint32_t lds0 = lds_offset(&R[0][0]);
+  // Issue cursor (unit iu_idx, stage is; ring slot fi % DNB). Per-lane source offsets are fixed for
+  // a unit (relative to a uniform base), so a stage's loads cost one address add each.
   int iu_idx = u0, is = 0, fi = 0;
   Unit iu = unit(u0);
   bool ivalid = true;
-  auto issue_next = [&]() {
-    if (!ivalid) return;
-    float* buf = &R[fi % DNB][0];
-    const int ks = iu.k0 + is * DSK;
+  int off[DPW];
+  auto unit_offsets = [&]() {
 #pragma unroll
     for (int q = 0; q < DPW; ++q) {
-      const int ins = wv + 4 * q;
-      if (ins < 16) {  // E: rows 8 ins .. 8 ins + 7
+      const int ins = wv + 4 * q;  // loads 0..15 are E (q < 4), 16..23 are B (q >= 4)
+      if (q < 4) {  // E rows 8 ins .. 8 ins + 7, relative to row r0 and column k0 + ks
         const int rl = 8 * ins + (lane >> 3);
-        const int quad = (lane & 7) ^ (rl & 7);
-        const int row = min(iu.r0 + rl, m - 1);
-        dma16_untracked(A + (long)row * lda + ks + 4 * quad, buf + 256 * ins);
-      } else {  // B: k rows 4 j .. 4 j + 3
-        const int j = ins - 16;
-        const int c = min(iu.cb + 4 * (lane & 15), wd - 4);
-        dma16_untracked(B + (long)(ks + 4 * j + (lane >> 4)) * ldb + c, buf + DSK * PR + 256 * j);
+        off[q] = (min(iu.r0 + rl, m - 1) - iu.r0) * (int)lda + 4 * ((lane & 7) ^ (rl & 7));
+      } else {  // B k rows 4 j .. 4 j + 3, relative to row k0 + ks and column 0
+        off[q] = (4 * (ins - 16) + (lane >> 4)) * (int)ldb + min(iu.cb + 4 * (lane & 15), wd - 4);
       }
+    }
+  };
+  unit_offsets();
+  auto issue_next = [&]() {
+    if (!ivalid) return;
+    const uint32_t buf = lds0 + (uint32_t)((fi % DNB) * DSTAGE * 4);
+    const int ks = iu.k0 + is * DSK;
+    const float* ea = A + (long)iu.r0 * lda + ks;
+    const float* hb = B + (long)ks * ldb;
+#pragma unroll
+    for (int q = 0; q < DPW; ++q) {
+      const int ins = wv + 4 * q;  // each load fills 1 KB: stage slot 256 ins (floats)
+      dma16_untracked((q < 4 ? ea : hb) + off[q], buf + 1024u * (uint32_t)ins);
     }
     ++fi;
     if (++is >= iu.nst) {
       if (++iu_idx < u1) {
         iu = unit(iu_idx);
         is = 0;
+        unit_offsets();
       } else {
         ivalid = false;
       }
@@ -247,47 +258,42 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
   };
   issue_next();
   issue_next();
-  v32f acc = {};
-  int cu_idx = u0, cs = 0, fc = 0;
-  Unit cu = unit(u0);
-  bool stored = false;  // P stores of the previous stage may still be in flight
-  while (true) {
-    // this wave's part of stage fc has landed once at most the next stage's loads are outstanding
-    if (fi - fc >= 2 && !stored)
-      wait_vmcnt<DPW>();
-    else
-      wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();  // publishes all parts; all reads of stage fc - 1 are done
-    issue_next();                  // into the slot of stage fc - 1
-    const float* buf = &R[fc % DNB][0];
-    const int er = 32 * wv + (lane & 31);
-    const float* es = buf + 32 * er;
-    const float* hs = buf + DSK * PR + lane;
+  const int er = 32 * wv + (lane & 31);
+  int fc = 0;
+  bool stored = false;  // P stores of the previous unit may still be in flight
+  for (int cu_idx = u0; cu_idx < u1; ++cu_idx) {
+    const Unit cu = unit(cu_idx);
+    v32f acc = {};
+    for (int cs = 0; cs < cu.nst; ++cs) {
+      // this wave's part of stage fc has landed once at most the next stage's loads are outstanding
+      if (fi - fc >= 2 && !stored)
+        wait_vmcnt<DPW>();
+      else
+        wait_vmcnt<0>();
+      stored = false;
+      __builtin_amdgcn_s_barrier();  // publishes all parts; all reads of stage fc - 1 are done
+      issue_next();                  // into the slot of stage fc - 1
+      const float* buf = &R[fc % DNB][0];
+      const float* es = buf + 32 * er;
+      const float* hs = buf + DSK * PR + lane;
 #pragma unroll
-    for (int q = 0; q < DSK / 4; ++q) {
-      const float4 a = *reinterpret_cast<const float4*>(es + 4 * (q ^ (er & 7)));
-      acc = mfma32(a.x, hs[(4 * q + 0) * PC], acc);
-      acc = mfma32(a.y, hs[(4 * q + 1) * PC], acc);
-      acc = mfma32(a.z, hs[(4 * q + 2) * PC], acc);
-      acc = mfma32(a.w, hs[(4 * q + 3) * PC], acc);
-    }
-    stored = false;
-    if (cs == cu.nst - 1) {  // the unit's last stage: write its chains and start the next unit
-#pragma unroll
-      for (int r = 0; r < 32; ++r) {
-        const int row = cu.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
-        const int col = cu.cb + 32 * (r >> 4) + (lane & 31);
-        if (row < m && col < wd) P[((long)cu.p * m + row) * wd + col] = acc[r];
+      for (int q = 0; q < DSK / 4; ++q) {
+        const float4 a = *reinterpret_cast<const float4*>(es + 4 * (q ^ (er & 7)));
+        acc = mfma32(a.x, hs[(4 * q + 0) * PC], acc);
+        acc = mfma32(a.y, hs[(4 * q + 1) * PC], acc);
+        acc = mfma32(a.z, hs[(4 * q + 2) * PC], acc);
+        acc = mfma32(a.w, hs[(4 * q + 3) * PC], acc);
       }
-      acc = v32f{};
-      stored = true;
-      if (++cu_idx >= u1) break;
-      cu = unit(cu_idx);
-      cs = 0;
-    } else {
-      ++cs;
+      ++fc;
     }
-    ++fc;
+    // block b = r >> 4 (cols 32b..), row i = (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), col j = lane & 31
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+      const int row = cu.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
+      const int col = cu.cb + 32 * (r >> 4) + (lane & 31);
+      if (row < m && col < wd) P[((long)cu.p * m + row) * wd + col] = acc[r];
+    }
+    stored = true;
   }
 }
 
