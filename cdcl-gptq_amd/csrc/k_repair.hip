@@ -259,20 +259,22 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
   issue_next();
   issue_next();
   const int er = 32 * wv + (lane & 31);
+  // Vector memory operations complete in issue order, so "at most the newest DPW outstanding"
+  // means everything older -- stage fc and any P stores issued before stage fc + 1 -- is done. At
+  // a unit's last stage the next load is issued after the unit's P stores, so the wait that
+  // follows does not also hold back the stage after.
   int fc = 0;
-  bool stored = false;  // P stores of the previous unit may still be in flight
   for (int cu_idx = u0; cu_idx < u1; ++cu_idx) {
     const Unit cu = unit(cu_idx);
     v32f acc = {};
     for (int cs = 0; cs < cu.nst; ++cs) {
       // this wave's part of stage fc has landed once at most the next stage's loads are outstanding
-      if (fi - fc >= 2 && !stored)
+      if (fi - fc >= 2)
         wait_vmcnt<DPW>();
       else
         wait_vmcnt<0>();
-      stored = false;
       __builtin_amdgcn_s_barrier();  // publishes all parts; all reads of stage fc - 1 are done
-      issue_next();                  // into the slot of stage fc - 1
+      if (cs + 1 < cu.nst) issue_next();  // into the slot of stage fc - 1
       const float* buf = &R[fc % DNB][0];
       const float* es = buf + 32 * er;
       const float* hs = buf + DSK * PR + lane;
@@ -293,7 +295,7 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
       const int col = cu.cb + 32 * (r >> 4) + (lane & 31);
       if (row < m && col < wd) P[((long)cu.p * m + row) * wd + col] = acc[r];
     }
-    stored = true;
+    issue_next();  // the load deferred at the unit's last stage
   }
 }
 
