@@ -116,7 +116,7 @@ def test_gram_batch_matches_single_calls(ctx):
 
 
 # ---------------------------------------------------------------- U
-@pytest.mark.parametrize("n", [1, 5, 96, 150, 200, 400])
+@pytest.mark.parametrize("n", [1, 5, 96, 150, 200, 400, 700])
 def test_upper_chol_bitexact(ctx, n):
     h = rand_spd(n, n + 2)
     ug = cdclq.upper_chol_of_inverse(h, n, ctx)
