@@ -250,7 +250,7 @@ def main():
         "phases_ms_per_step": phases,
         "roofline": {
             "bound": "mfma",
-            "kernel": "k_gram_mfma (H += X^T X for the layer's 4 inputs, K=1 f32 MFMA chains, f64 chunks)",
+            "kernel": "k_gram_dma (H += X^T X for the layer's 4 inputs, K=1 f32 MFMA chains, f64 chunks)",
             "achieved": round(achieved, 2),
             "peak": FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
