@@ -145,7 +145,9 @@ __device__ __forceinline__ void dma16(const float* g, float* lds) {
 // The same load issued from inline assembly: the compiler then tracks no LDS write for it and adds
 // no wait of its own before later LDS reads (it would wait for every load in flight); the caller
 // orders the data with wait_vmcnt and a barrier. The memory clobber keeps the compiler from moving
-// LDS accesses across it; s_nop 0 covers the M0-write to LDS-DMA wait state.
+// LDS accesses across it; s_nop 0 covers the M0-write to LDS-DMA wait state. M0 is clobbered:
+// only for kernels whose compiled code does not otherwise keep a value in M0 (checked for
+// k_panel_dma, where these blocks are M0's only writers and nothing else reads it).
 __device__ __forceinline__ void dma16_untracked(const float* g, uint32_t lds_byte_offset) {
   const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_byte_offset);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0v)

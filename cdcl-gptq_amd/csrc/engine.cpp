@@ -62,7 +62,7 @@ struct cdclq_ctx {
   // workspace (grow-only)
   DevBuf w_in, h_in, m_in, x_in, y_in, h64_in, u_out, codes_o, scales_o, zeros_o;
   DevBuf wp, wwork, wq, ebuf, gbits_d, perm_d, deadp_d, dead_d, diag_d, colsq_d, invd, colloss_d;
-  DevBuf G, part, rlog, rcnt, clog, ccnt, active_d, sel_d, ld_d, upd_d, mp, t1, t2, a64, y64, tbuf, tpart, status_d,
+  DevBuf G, part, rlog, rcnt, clog, ccnt, active_d, sel_d, ld_d, upd_d, mp, t1, t2, a64, y64, tbuf, tpart, status_d, rtiles_d,
       tiles_d, proxy_p, cs_d;
   // one-entry PrepCache (src/engine.rs:207-223): key, perm, damping and the device factors
   bool cache_valid = false;
@@ -242,9 +242,11 @@ int factor(cdclq_ctx* ctx, int n, double* a, double* y, float* u) {
 
 // The G = E H[:, c0:c0+wd] GEMM of phase 2 (src/engine.rs:548, :608): per-panel chains into
 // ctx->part, then folded in panel order into ctx->G.
-int grad_gemm(cdclq_ctx* ctx, int rows, int n, int c0, int wd, const float* e, const float* h32) {
-  hipError_t err = panel_gemm(ctx->st, rows, wd, n, e, n, h32 + c0, n, P<float>(ctx->part));
-  if (err == hipSuccess) err = fold_panels(ctx->st, rows, wd, (n + 255) / 256, P<float>(ctx->part), P<float>(ctx->G));
+int grad_gemm(cdclq_ctx* ctx, int rows, int n, int c0, int wd, const float* e, const float* h32, const int* rtiles,
+              int ntiles) {
+  hipError_t err = panel_gemm(ctx->st, rows, wd, n, e, n, h32 + c0, n, P<float>(ctx->part), rtiles, ntiles);
+  if (err == hipSuccess)
+    err = fold_panels(ctx->st, rows, wd, (n + 255) / 256, P<float>(ctx->part), P<float>(ctx->G), rtiles, ntiles);
   return err == hipSuccess ? CDCLQ_OK : fail(ctx, CDCLQ_DEVICE, std::string("gradient GEMM: ") + hipGetErrorString(err));
 }
 
@@ -483,11 +485,35 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
     HIPCK(hipMemcpyAsync(ctx->active_d.p, act.data(), nchunks, hipMemcpyHostToDevice, st));
     std::vector<double> prev(nchunks, 0.0);
     std::vector<uint64_t> upd(nchunks);
+    // The gradient GEMM runs only over the 128-row tiles that hold rows of a chunk still being
+    // repaired: list 0 for the refit steps (active chunks), list 1 + s for CD sub-block s (active
+    // chunks that selected it). A null list means every tile (the final refit).
+    const int rt = panel_row_tile(), ntile = (d_out + rt - 1) / rt;
+    std::vector<int> tl((size_t)(1 + n_sb) * ntile), tcnt(1 + n_sb);
+    CK(ensure(ctx, ctx->rtiles_d, tl.size() * sizeof(int)));
+    int* rtiles = P<int>(ctx->rtiles_d);
+    auto build_tiles = [&]() -> int {
+      for (int l = 0; l <= n_sb; ++l) {
+        int cnt = 0;
+        for (int t = 0; t < ntile; ++t) {
+          const int c_lo = (t * rt) / rc, c_hi = (std::min((t + 1) * rt, d_out) - 1) / rc;
+          bool need = false;
+          for (int c = c_lo; c <= c_hi && !need; ++c)
+            need = act[c] && (l == 0 || sel[(size_t)c * n_sb + (l - 1)]);
+          if (need) tl[(size_t)l * ntile + cnt++] = t;
+        }
+        tcnt[l] = cnt;
+      }
+      HIPCK(hipMemcpyAsync(rtiles, tl.data(), tl.size() * sizeof(int), hipMemcpyHostToDevice, st));
+      return CDCLQ_OK;
+    };
+    CK(build_tiles());
+    bool all_tiles = false;
     auto refit_all = [&]() -> int {
       HIPCK(hipMemsetAsync(rcnt, 0, (size_t)ng * d_out * 4, st));
       for (int gi = 0; gi < ng; ++gi) {
         const int c0 = gi * g, wd = std::min(c0 + g, n) - c0;
-        CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32));
+        CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32, all_tiles ? nullptr : rtiles, all_tiles ? ntile : tcnt[0]));
         HIPCK(refit_group(st, d_out, n, ng, g, gi, rc, P<float>(ctx->G), H32, codes, scales, zeros, wq, eb,
                           P<uint8_t>(ctx->active_d), rlog + (size_t)gi * d_out, rcnt + (size_t)gi * d_out));
       }
@@ -504,7 +530,7 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
           for (int c = 0; c < nchunks && !any; ++c) any = act[c] && sel[(size_t)c * n_sb + s];
           if (!any) continue;
           const int c0 = s * sbw, wd = std::min(c0 + sbw, n) - c0;
-          CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32));
+          CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32, rtiles + (size_t)(1 + s) * ntile, tcnt[1 + s]));
           HIPCK(cd_subblock(st, d_out, n, ng, g, c0, wd, s, n_sb, rc, (int)cfg->cd_sweeps, P<float>(ctx->G), H32,
                             P<uint8_t>(ctx->gbits_d), scales, zeros, codes, wq, eb, P<uint8_t>(ctx->active_d),
                             P<uint8_t>(ctx->sel_d), clog + (size_t)s * d_out * cap, ccnt + (size_t)s * d_out, cap));
@@ -528,9 +554,11 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
       }
       if (!any_active) break;
       HIPCK(hipMemcpyAsync(ctx->active_d.p, act.data(), nchunks, hipMemcpyHostToDevice, st));
+      CK(build_tiles());
     }
     if (do_refit) {  // final refit (src/engine.rs:668-670)
       std::fill(act.begin(), act.end(), 1);
+      all_tiles = true;
       HIPCK(hipMemcpyAsync(ctx->active_d.p, act.data(), nchunks, hipMemcpyHostToDevice, st));
       HIPCK(hipMemsetAsync(ctx->upd_d.p, 0, (size_t)nchunks * 8, st));
       CK(refit_all());
@@ -716,7 +744,7 @@ void cdclq_ctx_destroy(cdclq_ctx* ctx) {
   DevBuf* bufs[] = {&ctx->w_in, &ctx->h_in, &ctx->m_in, &ctx->x_in, &ctx->y_in, &ctx->h64_in, &ctx->u_out,
                     &ctx->codes_o, &ctx->scales_o, &ctx->zeros_o, &ctx->wp, &ctx->wwork, &ctx->wq, &ctx->ebuf,
                     &ctx->gbits_d, &ctx->perm_d, &ctx->deadp_d, &ctx->dead_d, &ctx->diag_d, &ctx->colsq_d,
-                    &ctx->invd, &ctx->colloss_d, &ctx->G, &ctx->part, &ctx->rlog, &ctx->rcnt, &ctx->clog, &ctx->ccnt, &ctx->active_d,
+                    &ctx->invd, &ctx->colloss_d, &ctx->G, &ctx->part, &ctx->rlog, &ctx->rcnt, &ctx->clog, &ctx->ccnt, &ctx->active_d, &ctx->rtiles_d,
                     &ctx->sel_d, &ctx->ld_d, &ctx->upd_d, &ctx->mp, &ctx->t1, &ctx->t2, &ctx->a64, &ctx->y64,
                     &ctx->tbuf, &ctx->tpart, &ctx->status_d, &ctx->tiles_d, &ctx->proxy_p, &ctx->cs_d,
                     &ctx->cache_u, &ctx->cache_h32};

@@ -44,7 +44,7 @@ __device__ __forceinline__ v32f mfma32(float a, float b, v32f c) {
 template <int SK, bool VEC4>
 __global__ __launch_bounds__(256) void k_panel_gemm(int m, int wd, int k, const float* __restrict__ A, long lda,
                                                     const float* __restrict__ B, long ldb, float* __restrict__ P,
-                                                    int nunits) {
+                                                    int nunits, const int* __restrict__ rtiles, int nrt) {
   constexpr int ES = SK + 4;
   constexpr int EQ = PR * SK / 4 / 256;  // float4 of E per thread per stage
   constexpr int HQ = SK * PC / 4 / 256;  // float4 of B per thread per stage
@@ -53,7 +53,6 @@ __global__ __launch_bounds__(256) void k_panel_gemm(int m, int wd, int k, const 
   __shared__ float Es[2][PR * ES];
   __shared__ float Hs[2][SK * PC];
   const int np = (k + CDCLQ_KC - 1) / CDCLQ_KC;
-  const int nrt = (m + PR - 1) / PR;
   const int u0 = (int)((long)blockIdx.x * nunits / gridDim.x);
   const int u1 = (int)((long)(blockIdx.x + 1) * nunits / gridDim.x);
   if (u0 >= u1) return;
@@ -64,7 +63,7 @@ __global__ __launch_bounds__(256) void k_panel_gemm(int m, int wd, int k, const 
   auto unit = [&](int u) {
     Unit t;
     const int ct = u / (nrt * np), rem = u % (nrt * np);
-    t.r0 = (rem / np) * PR;
+    t.r0 = (rtiles ? rtiles[rem / np] : rem / np) * PR;
     t.p = rem % np;
     t.cb = ct * PC;
     t.k0 = t.p * CDCLQ_KC;
@@ -192,10 +191,9 @@ constexpr int DPW = DSTAGE / 256 / 4;        // 1 KB loads per wave and stage (6
 
 __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const float* __restrict__ A, long lda,
                                                    const float* __restrict__ B, long ldb, float* __restrict__ P,
-                                                   int nunits) {
+                                                   int nunits, const int* __restrict__ rtiles, int nrt) {
   __shared__ float R[DNB][DSTAGE];
   const int np = k / CDCLQ_KC + (k % CDCLQ_KC != 0);
-  const int nrt = (m + PR - 1) / PR;
   const int u0 = (int)((long)blockIdx.x * nunits / gridDim.x);
   const int u1 = (int)((long)(blockIdx.x + 1) * nunits / gridDim.x);
   if (u0 >= u1) return;
@@ -207,7 +205,7 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
   auto unit = [&](int u) {
     Unit t;
     const int ct = u / (nrt * np), rem = u % (nrt * np);
-    t.r0 = (rem / np) * PR;
+    t.r0 = (rtiles ? rtiles[rem / np] : rem / np) * PR;
     t.p = rem % np;
     t.cb = ct * PC;
     t.k0 = t.p * CDCLQ_KC;
@@ -300,22 +298,29 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
 }
 
 // G[r][c] = ordered fold of the panel chains (alpha 1, beta 0): C = fma(1, P_p, C) for p = 0, 1, ...
-// One thread per entry, panel loads unrolled so many are in flight.
-__global__ __launch_bounds__(256) void k_fold(long count, int np, const float* __restrict__ P, float* __restrict__ G) {
+// One thread per element of the listed 128-row tiles, panel loads unrolled so many are in flight.
+__global__ __launch_bounds__(256) void k_fold(int m, int wd, int np, const int* __restrict__ rtiles, long count,
+                                              const float* __restrict__ P, float* __restrict__ G) {
   const long idx = (long)blockIdx.x * 256 + threadIdx.x;
   if (idx >= count) return;
-  const float* src = P + idx;
-  float g = 0.0f;
+  const long tw = (long)PR * wd;
+  const int t = (int)(idx / tw), within = (int)(idx % tw);
+  const int row = (rtiles ? rtiles[t] : t) * PR + within / wd;
+  if (row >= m) return;
+  const long g = (long)row * wd + within % wd;
+  const long pstride = (long)m * wd;
+  const float* src = P + g;
+  float acc = 0.0f;
   int p = 0;
   for (; p + 8 <= np; p += 8) {
     float v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = src[(long)(p + u) * count];
+    for (int u = 0; u < 8; ++u) v[u] = src[(long)(p + u) * pstride];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) g = __builtin_fmaf(1.0f, v[u], g);
+    for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(1.0f, v[u], acc);
   }
-  for (; p < np; ++p) g = __builtin_fmaf(1.0f, src[(long)p * count], g);
-  G[idx] = g;
+  for (; p < np; ++p) acc = __builtin_fmaf(1.0f, src[(long)p * pstride], acc);
+  G[g] = acc;
 }
 
 // Closed-form f16 scale refit of group gi (src/engine.rs:543-587). One wavefront advances RW rows
@@ -594,12 +599,16 @@ size_t panel_partials_elems(int m, int wd, int k) {
   return (size_t)((k + CDCLQ_KC - 1) / CDCLQ_KC) * (size_t)m * (size_t)wd;
 }
 
+int panel_row_tile() { return PR; }
+
 hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long lda, const float* B, long ldb,
-                      float* P) {
+                      float* P, const int* rtiles, int ntiles) {
   if (m <= 0 || wd <= 0 || k <= 0) return hipSuccess;
+  if (!rtiles) ntiles = (m + PR - 1) / PR;
+  if (ntiles <= 0) return hipSuccess;
   const bool vec4 = (lda % 4 == 0) && ((uintptr_t)A % 16 == 0) && k % 4 == 0;
   constexpr int SK = 32;
-  const long nunits = (long)((m + PR - 1) / PR) * ((k + CDCLQ_KC - 1) / CDCLQ_KC) * ((wd + PC - 1) / PC);
+  const long nunits = (long)ntiles * ((k + CDCLQ_KC - 1) / CDCLQ_KC) * ((wd + PC - 1) / PC);
   if (nunits > INT32_MAX) return hipErrorInvalidValue;
   // one workgroup per resident slot (occupancy is a property of the kernel, cached per process)
   static int slots[2] = {0, 0};
@@ -627,22 +636,24 @@ hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long
       dslots = std::max(1, cus * std::max(1, per));
     }
     hipLaunchKernelGGL(k_panel_dma, dim3((int)std::min<long>(nunits, dslots)), dim3(256), 0, st, m, wd, k, A, lda,
-                       B, ldb, P, (int)nunits);
+                       B, ldb, P, (int)nunits, rtiles, ntiles);
     return hipGetLastError();
   }
   if (vec4)
     hipLaunchKernelGGL((k_panel_gemm<SK, true>), dim3(grid), dim3(256), 0, st, m, wd, k, A, lda, B, ldb, P,
-                       (int)nunits);
+                       (int)nunits, rtiles, ntiles);
   else
     hipLaunchKernelGGL((k_panel_gemm<SK, false>), dim3(grid), dim3(256), 0, st, m, wd, k, A, lda, B, ldb, P,
-                       (int)nunits);
+                       (int)nunits, rtiles, ntiles);
   return hipGetLastError();
 }
 
-hipError_t fold_panels(hipStream_t st, int m, int wd, int np, const float* P, float* G) {
-  const long count = (long)m * wd;
-  if (count <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_fold, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st, count, np, P, G);
+hipError_t fold_panels(hipStream_t st, int m, int wd, int np, const float* P, float* G, const int* rtiles,
+                       int ntiles) {
+  if (!rtiles) ntiles = (m + PR - 1) / PR;
+  const long count = (long)ntiles * PR * wd;
+  if (count <= 0 || m <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fold, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st, m, wd, np, rtiles, count, P, G);
   return hipGetLastError();
 }
 

@@ -60,11 +60,15 @@ hipError_t gptq_block(hipStream_t st, int rows, int n, int i1, int cnt, int g, i
 hipError_t colloss(hipStream_t st, int rows, int n, int rc, const float* err, double* out);
 hipError_t sub_f32(hipStream_t st, size_t count, const float* a, const float* b, float* out);
 // ---- k_repair.hip: phase 2
-// P[p][r][c] = chain over panel p of A[r][k] B[k][c] (r < m, c < wd); the sweeps fold the panels.
+// P[p][r][c] = chain over panel p of A[r][k] B[k][c] (r < m, c < wd)
 size_t panel_partials_elems(int m, int wd, int k);
+// Repair gradient: per-panel chains of G = A B into P (np x m x wd), for the listed 128-row tiles
+// of A (all tiles when rtiles is null), then their ordered fold into G (d_out x wd).
+int panel_row_tile();
 hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long lda, const float* B, long ldb,
-                      float* P);
-hipError_t fold_panels(hipStream_t st, int m, int wd, int np, const float* P, float* G);
+                      float* P, const int* rtiles, int ntiles);
+hipError_t fold_panels(hipStream_t st, int m, int wd, int np, const float* P, float* G, const int* rtiles,
+                       int ntiles);
 hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, int rc, const float* G,
                        const float* h32, const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
                        const uint8_t* active, double* dlog, uint32_t* dcnt);
