@@ -150,8 +150,12 @@ __device__ __forceinline__ void dma16(const float* g, float* lds) {
 // k_panel_dma, where these blocks are M0's only writers and nothing else reads it).
 __device__ __forceinline__ void dma16_untracked(const float* g, uint32_t lds_byte_offset) {
   const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_byte_offset);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0v)
-               : "memory", "m0");
+  uint32_t m0out;  // M0 is written by the block: declared as an output so the compiler knows
+  asm volatile("s_mov_b32 %0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               : "={m0}"(m0out)
+               : "v"(g), "s"(m0v)
+               : "memory");
+  (void)m0out;
 }
 
 // LDS byte offset of a generic pointer into LDS (the low 32 bits of a generic address in the LDS

@@ -325,7 +325,7 @@ __global__ __launch_bounds__(256) void k_fold(int m, int wd, int np, const int* 
 
 // Closed-form f16 scale refit of group gi (src/engine.rs:543-587). One wavefront advances RW rows
 // together (columns over lanes), so every H_CC element read from LDS feeds RW independent chains;
-// H_CC is staged once per workgroup as a zero-padded WP x WP tile.
+// H_CC is staged once per workgroup (4 RW rows) as a zero-padded WP x WP tile.
 template <int NPL>
 constexpr int refit_rows_per_wave() {
   return NPL <= 2 ? 4 : 1;
@@ -430,16 +430,24 @@ __global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, i
         }
     }
   }
-  // num = sum_k u_k g_k, den = sum_k u_k hu_k, sequential in k (src/engine.rs:562-566)
+  // num = sum_k u_k g_k, den = sum_k u_k hu_k, sequential in k (src/engine.rs:562-566). The
+  // products are rounded on their own before each add, so every lane forms its column's products
+  // at once and the sequential part is one broadcast and one add per term.
+#pragma unroll
+  for (int q = 0; q < RW; ++q)
+#pragma unroll
+    for (int s = 0; s < NPL; ++s) {
+      gg[q][s] = uu[q][s] * gg[q][s];    // u_k g_k
+      cvh[q][s] = uu[q][s] * cvh[q][s];  // u_k hu_k
+    }
   float num[RW], den[RW];
 #pragma unroll
   for (int q = 0; q < RW; ++q) num[q] = den[q] = 0.0f;
   auto nd_step = [&](int s1, int kl) {
 #pragma unroll
     for (int q = 0; q < RW; ++q) {
-      const float uk = readlane(uu[q][s1], kl);
-      num[q] = num[q] + uk * readlane(gg[q][s1], kl);
-      den[q] = den[q] + uk * readlane(cvh[q][s1], kl);
+      num[q] = num[q] + readlane(gg[q][s1], kl);
+      den[q] = den[q] + readlane(cvh[q][s1], kl);
     }
   };
 #pragma unroll
