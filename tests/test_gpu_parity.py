@@ -293,3 +293,122 @@ def test_proxy_loss(ctx):
     lo = O.proxy_loss(w, q.dequantize(), hd)
     assert abs(lg - lo) <= 1e-9 * abs(lo)
     assert abs(lg - s.loss_final) / lg < 5e-3  # src/engine.rs:929 bookkeeping bar
+
+
+# ---------------------------------------------------------------- the other BASELINE configurations
+def test_config2_shaped_layer_set(ctx):
+    """BASELINE config 2's parameters (INT3, g128, act-order, passes 10, tol 1e-3) on a scaled-down
+    layer set with the reference pipeline's sharing: q/k/v share one input and one factorisation,
+    gate/up share another, o and down have their own (n = 512; down n = 1408)."""
+    t = 3000
+    kw = dict(bits=3, group=128, block=128, act_order=True, passes=10, tol=1e-3, row_chunk=64)
+    gcfg, ocfg = cfgs(**kw)
+    ins = {key: synth_layer(90 + i, 8, nn, t)[2] for i, (key, nn) in
+           enumerate((("qkv", 512), ("o", 512), ("gu", 512), ("down", 1408)))}
+    layers = [("q", 512, "qkv"), ("k", 64, "qkv"), ("v", 64, "qkv"), ("o", 512, "o"), ("gate", 1408, "gu"),
+              ("up", 1408, "gu"), ("down", 512, "down")]
+    gcache, ocache = cdclq.PrepCache(ctx=ctx), O.Cache()
+    ctx.clear_cache()
+    for li, (name, d_out, key) in enumerate(layers):
+        h = ins[key]
+        nn = h.shape[0]
+        w = O.synth_normal(200 + li, d_out * nn, 0.02).reshape(d_out, nn)
+        print(f"[parity] c2 {name} {d_out}x{nn}", flush=True)
+        qg, sg = cdclq.quantize_layer(w, d_out, nn, h, None, key, gcfg, gcache)
+        qo = O.quantize_layer(w, h, ocfg, hkey=key, cache=ocache)
+        assert_same(qg, sg, qo, label=f"c2 {name}")
+
+
+def test_config3_shaped_layers(ctx):
+    """BASELINE config 3's parameters: INT2, g64, mse_grid, act-order, passes 8, skeleton 5% at 8 bits
+    (the saliency-dependent permutation is rebuilt for every layer)."""
+    kw = dict(bits=2, group=64, block=128, act_order=True, mse_grid=True, passes=8, skeleton_pct=5.0,
+              skeleton_bits=8, row_chunk=32)
+    for seed, d_out, n in ((101, 256, 512), (102, 128, 704)):
+        w, x, h, _ = synth_layer(seed, d_out, n, 2500)
+        qg, sg, qo = run_both(ctx, w, h, **kw)
+        assert_same(qg, sg, qo, label=f"c3 {d_out}x{n}")
+
+
+def test_config5_shaped_asymmetric(ctx):
+    """BASELINE config 5's parameters: INT3, g128, passes 6, asymmetric target. H~ = X~^T X~ and
+    M = X^T X~ with X~ = X + N(0, 0.05^2), both accumulated on the GPU and compared bit for bit."""
+    n, d_out, t = 512, 768, 2048
+    cs = O.synth_outlier_scales(111, n, 0.01, 20.0)
+    x = O.synth_tokens(112, t, n, cs)
+    xt = (x + O.synth_normal(113, t * n, 0.05).reshape(t, n)).astype(np.float32)
+    hg, mg = np.zeros((n, n)), np.zeros((n, n))
+    cdclq.gram_accumulate(xt, xt, t, n, hg, ctx)
+    cdclq.gram_accumulate(x, xt, t, n, mg, ctx)
+    assert np.array_equal(hg.view(np.uint64), O.gram_accumulate(xt).view(np.uint64))
+    assert np.array_equal(mg.view(np.uint64), O.gram_accumulate(x, xt).view(np.uint64))
+    w = O.synth_normal(114, d_out * n, 0.01).reshape(d_out, n)
+    assert_same(*run_both(ctx, w, hg.astype(np.float32), m=mg.astype(np.float32), bits=3, group=128, block=128,
+                          passes=6, row_chunk=64), label="c5 asymmetric")
+
+
+def test_config4_full_size_properties(ctx):
+    """Config 4 at full size, where the oracle would need minutes: gate_proj (14336 x 4096) on 524288
+    synthetic tokens, and the factor of the n = 14336 input. Size-independent checks: H bitwise
+    symmetric; two runs bit-identical; codes inside the 4-bit grid; scales f16-exact and positive;
+    repair never raises the loss; perm a permutation; U upper triangular with a positive diagonal and
+    U^T U H x = x on random probes."""
+    T = 256 * 2048
+    cfg = cdclq.Config(bits=4, group=128, block=128, damp=0.01, act_order=True)
+    n, d_out = 4096, 14336
+    print(f"[parity] c4 full size: gate_proj {d_out}x{n}, T={T}", flush=True)
+    cs = cdclq.synth_outlier_scales(1000, n, 0.01, 30.0)
+    x = cdclq.DeviceArray(ctx, (T, n), np.float32)
+    ctx.check(cdclq.lib().cdclq_synth_tokens_device(ctx.ptr, 2000, 0, T, n, cs.ctypes.data, x.ptr))
+    h64 = cdclq.DeviceArray(ctx, (n, n), np.float64)
+    h64.zero()
+    cdclq.gram_accumulate_batch_device(ctx, [x], [x], [T], [n], [h64])
+    x.free()
+    hh = h64.download()
+    assert np.array_equal(hh, hh.T)
+    h32 = cdclq.DeviceArray(ctx, (n, n), np.float32)
+    ctx.check(cdclq.lib().cdclq_f64_to_f32_device(ctx.ptr, h64.ptr, n * n, h32.ptr))
+    w = cdclq.DeviceArray(ctx, (d_out, n), np.float32)
+    ctx.check(cdclq.lib().cdclq_synth_normal_device(ctx.ptr, 3004, 0, d_out * n, 0.015, w.ptr))
+    ng = n // 128
+    runs = []
+    for _ in range(2):
+        ctx.clear_cache()
+        c = cdclq.DeviceArray(ctx, (d_out, n), np.uint8)
+        s = cdclq.DeviceArray(ctx, (d_out, ng), np.float32)
+        z = cdclq.DeviceArray(ctx, (d_out, ng), np.float32)
+        perm, gbits, st = cdclq.quantize_layer_device(ctx, w, d_out, n, h32, None, "mlp_in", cfg, c, s, z,
+                                                      nthreads=24)
+        runs.append((perm, gbits, st, c.download(), s.download(), z.download()))
+        for a in (c, s, z):
+            a.free()
+    (p1, g1, s1, c1, sc1, z1), (p2, g2, s2, c2, sc2, z2) = runs
+    assert np.array_equal(p1, p2) and np.array_equal(g1, g2)
+    assert np.array_equal(c1, c2) and np.array_equal(sc1.view(np.uint32), sc2.view(np.uint32))
+    assert np.array_equal(z1, z2) and s1.loss_final == s2.loss_final and s1.code_updates == s2.code_updates
+    assert np.array_equal(np.sort(p1), np.arange(n))
+    assert int(c1.max()) <= 15 and np.all(g1 == 4)
+    assert np.all(sc1 > 0) and np.array_equal(sc1.astype(np.float16).astype(np.float32), sc1)
+    assert np.all((z1 >= 0) & (z1 <= 15) & (z1 == np.round(z1)))
+    assert 0 < s1.loss_final <= s1.loss_gptq
+    for a in (w, h32, h64):
+        a.free()
+
+    nd = 14336
+    print(f"[parity] c4 full size: U of the n={nd} input", flush=True)
+    cs2 = cdclq.synth_outlier_scales(1021, nd, 0.01, 30.0)
+    x2 = cdclq.DeviceArray(ctx, (T, nd), np.float32)
+    ctx.check(cdclq.lib().cdclq_synth_tokens_device(ctx.ptr, 2021, 0, T, nd, cs2.ctypes.data, x2.ptr))
+    hd = cdclq.DeviceArray(ctx, (nd, nd), np.float64)
+    hd.zero()
+    cdclq.gram_accumulate_batch_device(ctx, [x2], [x2], [T], [nd], [hd])
+    x2.free()
+    hh2 = hd.download()
+    hd.free()
+    u = cdclq.upper_chol_of_inverse(hh2, nd, ctx)
+    assert not np.any(np.tril(u, -1)) and np.all(np.diag(u) > 0)
+    rng = np.random.default_rng(7)
+    for _ in range(2):
+        v = rng.standard_normal(nd)
+        back = u.T @ (u @ (hh2 @ v))  # U^T U = H^-1 (U in f32)
+        assert np.linalg.norm(back - v) <= 5e-3 * np.linalg.norm(v)  # f32 U, cond(H) ~ 2e3
