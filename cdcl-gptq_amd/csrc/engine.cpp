@@ -417,9 +417,13 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
       const int i2 = std::min(i1 + bsz, n), cnt = i2 - i1;
       HIPCK(gptq_block(st, d_out, n, i1, cnt, g, ng, wwork, U, P<float>(ctx->invd), P<uint8_t>(ctx->gbits_d),
                        cfg->mse_grid, scales, zeros, codes, wq, eb));
-      if (i2 < n)
-        HIPCK(gemm_chain<float>(st, d_out, n - i2, cnt, -1.0f, 1, eb + i1, n, 1, U + (long)i1 * n + i2, n, 1,
-                                wwork + i2, n, 1, false, nullptr));
+      if (i2 < n) {  // lazy update W[:, i2:] -= E[:, i1:i2] U[i1:i2, i2:] (src/engine.rs:452-471)
+        if (chain_gemm_mfma_ok(d_out, n - i2, cnt, eb + i1, n, U + (long)i1 * n + i2, n))
+          HIPCK(chain_gemm_mfma(st, d_out, n - i2, cnt, -1.0f, 1, eb + i1, n, U + (long)i1 * n + i2, n, wwork + i2, n));
+        else
+          HIPCK(gemm_chain<float>(st, d_out, n - i2, cnt, -1.0f, 1, eb + i1, n, 1, U + (long)i1 * n + i2, n, 1,
+                                  wwork + i2, n, 1, false, nullptr));
+      }
     }
     HIPCK(cdclq::colloss(st, d_out, n, rc, eb, P<double>(ctx->colloss_d)));
   }

@@ -189,9 +189,12 @@ constexpr int DNB = 3;
 constexpr int DSTAGE = DSK * PR + DSK * PC;  // floats per stage (E 4096 + B 2048)
 constexpr int DPW = DSTAGE / 256 / 4;        // 1 KB loads per wave and stage (6)
 
+// With C != null (k <= 256, one panel) the unit's chain is final and is folded straight into C:
+// C = fma(alpha, chain, beta_one ? C : 0), the single-panel case of the GEMM fold.
 __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const float* __restrict__ A, long lda,
                                                    const float* __restrict__ B, long ldb, float* __restrict__ P,
-                                                   int nunits, const int* __restrict__ rtiles, int nrt) {
+                                                   int nunits, const int* __restrict__ rtiles, int nrt,
+                                                   float* __restrict__ C, long ldc, float alpha, int beta_one) {
   __shared__ float R[DNB][DSTAGE];
   const int np = k / CDCLQ_KC + (k % CDCLQ_KC != 0);
   const int u0 = (int)((long)blockIdx.x * nunits / gridDim.x);
@@ -291,7 +294,14 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
     for (int r = 0; r < 32; ++r) {
       const int row = cu.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
       const int col = cu.cb + 32 * (r >> 4) + (lane & 31);
-      if (row < m && col < wd) P[((long)cu.p * m + row) * wd + col] = acc[r];
+      if (row < m && col < wd) {
+        if (C) {
+          float* cp = C + (long)row * ldc + col;
+          *cp = __builtin_fmaf(alpha, acc[r], beta_one ? *cp : 0.0f);
+        } else {
+          P[((long)cu.p * m + row) * wd + col] = acc[r];
+        }
+      }
     }
     issue_next();  // the load deferred at the unit's last stage
   }
@@ -644,7 +654,7 @@ hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long
       dslots = std::max(1, cus * std::max(1, per));
     }
     hipLaunchKernelGGL(k_panel_dma, dim3((int)std::min<long>(nunits, dslots)), dim3(256), 0, st, m, wd, k, A, lda,
-                       B, ldb, P, (int)nunits, rtiles, ntiles);
+                       B, ldb, P, (int)nunits, rtiles, ntiles, (float*)nullptr, 0L, 0.0f, 0);
     return hipGetLastError();
   }
   if (vec4)
@@ -653,6 +663,30 @@ hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long
   else
     hipLaunchKernelGGL((k_panel_gemm<SK, false>), dim3(grid), dim3(256), 0, st, m, wd, k, A, lda, B, ldb, P,
                        (int)nunits, rtiles, ntiles);
+  return hipGetLastError();
+}
+
+bool chain_gemm_mfma_ok(int m, int n, int k, const float* A, long lda, const float* B, long ldb) {
+  return m > 0 && n >= 4 && k > 0 && k <= CDCLQ_KC && k % DSK == 0 && n % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0 &&
+         (uintptr_t)A % 16 == 0 && (uintptr_t)B % 16 == 0;
+}
+
+hipError_t chain_gemm_mfma(hipStream_t st, int m, int n, int k, float alpha, int beta_one, const float* A, long lda,
+                           const float* B, long ldb, float* C, long ldc) {
+  if (!chain_gemm_mfma_ok(m, n, k, A, lda, B, ldb)) return hipErrorInvalidValue;
+  static int dslots = 0;
+  if (dslots == 0) {
+    int dev = 0, cus = 0, per = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err == hipSuccess) err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_panel_dma, 256, 0);
+    if (err != hipSuccess) return err;
+    dslots = std::max(1, cus * std::max(1, per));
+  }
+  const int ntiles = (m + PR - 1) / PR;
+  const long nunits = (long)ntiles * ((n + PC - 1) / PC);
+  hipLaunchKernelGGL(k_panel_dma, dim3((int)std::min<long>(nunits, dslots)), dim3(256), 0, st, m, n, k, A, lda, B, ldb,
+                     (float*)nullptr, (int)nunits, (const int*)nullptr, ntiles, C, ldc, alpha, beta_one);
   return hipGetLastError();
 }
 

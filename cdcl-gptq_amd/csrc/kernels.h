@@ -69,6 +69,12 @@ hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long
                       float* P, const int* rtiles, int ntiles);
 hipError_t fold_panels(hipStream_t st, int m, int wd, int np, const float* P, float* G, const int* rtiles,
                        int ntiles);
+// Single-panel f32 chain GEMM on the matrix cores: C = fma(alpha, chain, beta_one ? C : 0) with
+// A m x k (row stride lda), B k x n (row stride ldb), k <= 256 and k % 32 == 0; the _ok test
+// lists every requirement (else use gemm_chain).
+bool chain_gemm_mfma_ok(int m, int n, int k, const float* A, long lda, const float* B, long ldb);
+hipError_t chain_gemm_mfma(hipStream_t st, int m, int n, int k, float alpha, int beta_one, const float* A, long lda,
+                           const float* B, long ldb, float* C, long ldc);
 hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, int rc, const float* G,
                        const float* h32, const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
                        const uint8_t* active, double* dlog, uint32_t* dcnt);
