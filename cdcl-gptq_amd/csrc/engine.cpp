@@ -58,6 +58,8 @@ std::string rust_lower_exp(double d) {
 struct cdclq_ctx {
   int device = 0;
   hipStream_t st = nullptr;
+  hipStream_t st2 = nullptr;  // side stream of the factorisation's look-ahead (default priority)
+  hipEvent_t ev_col = nullptr, ev_panel = nullptr;
   std::string err;
   // workspace (grow-only)
   DevBuf w_in, h_in, m_in, x_in, y_in, h64_in, u_out, codes_o, scales_o, zeros_o;
@@ -199,15 +201,34 @@ int factor(cdclq_ctx* ctx, int n, double* a, double* y, float* u) {
   int* status = P<int>(ctx->status_d);
   double* pivot = reinterpret_cast<double*>(P<char>(ctx->status_d) + 8);
   HIPCK(hipMemsetAsync(ctx->status_d.p, 0, 16, st));
+  // Right-looking blocked Cholesky with one block of look-ahead: after block k's panel, the main
+  // stream first applies block k to block column k + 1 only, then the side stream factors block
+  // k + 1 (diagonal block and panel) while the main stream applies block k to the rest of the
+  // trailing matrix. The two touch disjoint elements, and every element still receives block
+  // k's update (one k = 96 chain, src/linalg.rs:243-270) before block k + 1's.
+  hipStream_t st2 = ctx->st2;
+  HIPCK(chol_diag(st, n, a, 0, std::min(NB, n), status, pivot));
+  if (NB < n) HIPCK(chol_panel(st, n, a, 0, NB, status));
   for (int k = 0; k < n; k += NB) {
     const int kb = std::min(NB, n - k), kend = k + kb;
-    HIPCK(chol_diag(st, n, a, k, kb, status, pivot));
-    if (kend < n) {
-      HIPCK(chol_panel(st, n, a, k, kb, status));
-      const long off = (long)kend * n + k;
-      HIPCK(gemm_chain<double>(st, n - kend, n - kend, kb, -1.0, 1, a + off, n, 1, a + off, 1, n,
-                               a + (long)kend * n + kend, n, 1, true, (double*)nullptr));
+    if (kend >= n) break;
+    const int kb1 = std::min(NB, n - kend), knext = kend + kb1;
+    // block k applied to block column k + 1 (rows kend.., cols kend..knext)
+    const long off = (long)kend * n + k;
+    HIPCK(gemm_chain<double>(st, n - kend, kb1, kb, -1.0, 1, a + off, n, 1, a + off, 1, n, a + (long)kend * n + kend,
+                             n, 1, true, (double*)nullptr));
+    HIPCK(hipEventRecord(ctx->ev_col, st));
+    HIPCK(hipStreamWaitEvent(st2, ctx->ev_col, 0));
+    HIPCK(chol_diag(st2, n, a, kend, kb1, status, pivot));
+    if (knext < n) HIPCK(chol_panel(st2, n, a, kend, kb1, status));
+    HIPCK(hipEventRecord(ctx->ev_panel, st2));
+    // block k applied to the rest of the trailing matrix (rows and cols knext..)
+    if (knext < n) {
+      const long off2 = (long)knext * n + k;
+      HIPCK(gemm_chain<double>(st, n - knext, n - knext, kb, -1.0, 1, a + off2, n, 1, a + off2, 1, n,
+                               a + (long)knext * n + knext, n, 1, true, (double*)nullptr));
     }
+    HIPCK(hipStreamWaitEvent(st, ctx->ev_panel, 0));
   }
   struct {
     int status;
@@ -732,7 +753,13 @@ int cdclq_ctx_create(int device, cdclq_ctx** out) {
   cdclq_ctx* ctx = new (std::nothrow) cdclq_ctx();
   if (!ctx) return CDCLQ_OOM;
   ctx->device = device;
-  if (hipStreamCreateWithFlags(&ctx->st, hipStreamNonBlocking) != hipSuccess) {
+  if (hipStreamCreateWithFlags(&ctx->st, hipStreamNonBlocking) != hipSuccess ||
+      hipStreamCreateWithFlags(&ctx->st2, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_col, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_panel, hipEventDisableTiming) != hipSuccess) {
+    if (ctx->ev_col) (void)hipEventDestroy(ctx->ev_col);
+    if (ctx->st2) (void)hipStreamDestroy(ctx->st2);
+    if (ctx->st) (void)hipStreamDestroy(ctx->st);
     delete ctx;
     return CDCLQ_DEVICE;
   }
@@ -753,6 +780,10 @@ void cdclq_ctx_destroy(cdclq_ctx* ctx) {
                     &ctx->tbuf, &ctx->tpart, &ctx->status_d, &ctx->tiles_d, &ctx->proxy_p, &ctx->cs_d,
                     &ctx->cache_u, &ctx->cache_h32};
   for (DevBuf* b : bufs) free_buf(*b);
+  (void)hipStreamSynchronize(ctx->st2);
+  (void)hipEventDestroy(ctx->ev_col);
+  (void)hipEventDestroy(ctx->ev_panel);
+  (void)hipStreamDestroy(ctx->st2);
   (void)hipStreamDestroy(ctx->st);
   delete ctx;
 }
