@@ -7,6 +7,9 @@
 // exactly that per-element operation sequence -- which makes them bit-identical to the
 // reference -- and are free in everything else: tile shapes, thread mapping, and running the
 // panels of one element in parallel (the ordered fold then happens in k_combine).
+#include <cstdint>
+#include <type_traits>
+
 #include "cdclq_dev.h"
 #include "kernels.h"
 
@@ -130,6 +133,180 @@ __global__ __launch_bounds__(256) void k_gemm(int m, int n, int k, T alpha, int 
     }
 }
 
+// f64 chains on the matrix cores. v_mfma_f64_16x16x4f64 advances every element of a 16 x 16 block
+// by four chain steps, c = fma(a3, b3, fma(a2, b2, fma(a1, b1, fma(a0, b0, c)))) in k order, each
+// fma rounded once: a probe over 2^20 elements with operands spread over 2^+-60 (where the reverse
+// order differs in a third of the cases) matched that sequence bit for bit. Operand layout: lane l
+// supplies A[l % 16][l / 16] and B[l / 16][l % 16]; D[i][j] is register r of lane j + 16 (i % 4)
+// with i = l / 16 + 4 r. Slots past the end of k hold A = -0, B = +0, whose step c + (-0) = c is
+// exact. Workgroup tile 64 x 64, wave (wi, wj) owns rows 32 wi.., cols 32 wj.. as 2 x 2 blocks;
+// k is staged 16 at a time through double-buffered LDS. Operand loads are 16-byte pairs along the
+// contiguous dimension when the host found it aligned (mode 1: along k, mode 2: along i / j).
+typedef double v4d __attribute__((ext_vector_type(4)));
+typedef double v2d __attribute__((ext_vector_type(2)));
+constexpr int DBM = 64, DBN = 64, DKT = 16, DPAD = 16;
+
+template <bool SPLIT, bool LOWER>
+__global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double alpha, int beta_one,
+                                                    const double* __restrict__ A, long rsa, long csa, int amode,
+                                                    const double* __restrict__ B, long rsb, long csb, int bmode,
+                                                    double* __restrict__ C, long rsc, long csc, double* __restrict__ P,
+                                                    int b_tri) {
+  __shared__ double As[2][DKT][DBM + DPAD];  // As[.][k][i]
+  __shared__ double Bs[2][DKT][DBN + DPAD];  // Bs[.][k][j]
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wi = wv >> 1, wj = wv & 1;
+  const int i0 = blockIdx.y * DBM, j0 = blockIdx.x * DBN;
+  if (LOWER && j0 > i0 + DBM - 1) return;  // tile strictly above the diagonal
+  int kbeg = 0, kend = k;
+  if (SPLIT) {
+    kbeg = blockIdx.z * CDCLQ_KC;
+    kend = min(k, kbeg + CDCLQ_KC);
+  }
+  const int kfirst = b_tri ? max(kbeg, (j0 / DKT) * DKT) : kbeg;
+  v2d ra[2], rb[2];
+  // pair p = tid + 256 q of the A tile (64 x 16) / B tile (16 x 64); 2 doubles each
+  auto a_at = [&](int i, int kk) -> double {
+    return (i < m && kk < kend) ? A[(long)i * rsa + (long)kk * csa] : -0.0;
+  };
+  auto b_at = [&](int kk, int j) -> double {
+    return (kk < kend && j < n) ? B[(long)kk * rsb + (long)j * csb] : 0.0;
+  };
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int pr = tid + 256 * q;
+      if (amode == 2) {  // along i
+        const int kk = pr >> 5, i = (pr & 31) * 2, gi = i0 + i, gk = k0 + kk;
+        if (gi + 1 < m && gk < kend)
+          ra[q] = *reinterpret_cast<const v2d*>(A + (long)gi * rsa + (long)gk * csa);
+        else
+          ra[q] = v2d{a_at(gi, gk), a_at(gi + 1, gk)};
+      } else {  // along k (vector when amode == 1)
+        const int i = pr >> 3, kk = (pr & 7) * 2, gi = i0 + i, gk = k0 + kk;
+        if (amode == 1 && gi < m && gk + 1 < kend)
+          ra[q] = *reinterpret_cast<const v2d*>(A + (long)gi * rsa + (long)gk * csa);
+        else
+          ra[q] = v2d{a_at(gi, gk), a_at(gi, gk + 1)};
+      }
+      if (bmode == 2) {  // along j
+        const int kk = pr >> 5, j = (pr & 31) * 2, gj = j0 + j, gk = k0 + kk;
+        if (gj + 1 < n && gk < kend)
+          rb[q] = *reinterpret_cast<const v2d*>(B + (long)gk * rsb + (long)gj * csb);
+        else
+          rb[q] = v2d{b_at(gk, gj), b_at(gk, gj + 1)};
+      } else {  // along k (vector when bmode == 1)
+        const int j = pr >> 3, kk = (pr & 7) * 2, gj = j0 + j, gk = k0 + kk;
+        if (bmode == 1 && gj < n && gk + 1 < kend)
+          rb[q] = *reinterpret_cast<const v2d*>(B + (long)gk * rsb + (long)gj * csb);
+        else
+          rb[q] = v2d{b_at(gk, gj), b_at(gk + 1, gj)};
+      }
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int pr = tid + 256 * q;
+      if (amode == 2) {
+        const int kk = pr >> 5, i = (pr & 31) * 2;
+        As[buf][kk][i] = ra[q].x;
+        As[buf][kk][i + 1] = ra[q].y;
+      } else {
+        const int i = pr >> 3, kk = (pr & 7) * 2;
+        As[buf][kk][i] = ra[q].x;
+        As[buf][kk + 1][i] = ra[q].y;
+      }
+      if (bmode == 2) {
+        const int kk = pr >> 5, j = (pr & 31) * 2;
+        Bs[buf][kk][j] = rb[q].x;
+        Bs[buf][kk][j + 1] = rb[q].y;
+      } else {
+        const int j = pr >> 3, kk = (pr & 7) * 2;
+        Bs[buf][kk][j] = rb[q].x;
+        Bs[buf][kk + 1][j] = rb[q].y;
+      }
+    }
+  };
+  v4d acc[2][2], cv[2][2];
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        acc[bi][bj][r] = 0.0;
+        cv[bi][bj][r] = 0.0;
+        if (!SPLIT && beta_one) {
+          const int gi = i0 + 32 * wi + 16 * bi + (lane >> 4) + 4 * r, gj = j0 + 32 * wj + 16 * bj + (lane & 15);
+          if (gi < m && gj < n) cv[bi][bj][r] = C[(long)gi * rsc + (long)gj * csc];
+        }
+      }
+  const int nst = kend > kfirst ? (kend - kfirst + DKT - 1) / DKT : 0;
+  if (nst > 0) {
+    gload(kfirst);
+    lstore(0);
+    __syncthreads();
+  }
+  for (int s = 0; s < nst; ++s) {
+    const int buf = s & 1, k0 = kfirst + s * DKT;
+    if (s + 1 < nst) gload(k0 + DKT);
+#pragma unroll
+    for (int k4 = 0; k4 < DKT; k4 += 4) {
+      double a[2], b[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        a[x] = As[buf][k4 + (lane >> 4)][32 * wi + 16 * x + (lane & 15)];
+        b[x] = Bs[buf][k4 + (lane >> 4)][32 * wj + 16 * x + (lane & 15)];
+      }
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj)
+          acc[bi][bj] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[bi], b[bj], acc[bi][bj], 0, 0, 0);
+    }
+    if (s + 1 < nst) lstore(buf ^ 1);
+    __syncthreads();
+    if (!SPLIT) {
+      const int kn = k0 + DKT;
+      if ((kn % CDCLQ_KC) == 0 || kn >= kend) {
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+          for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              cv[bi][bj][r] = __builtin_fma(alpha, acc[bi][bj][r], cv[bi][bj][r]);
+              acc[bi][bj][r] = 0.0;
+            }
+      }
+    }
+  }
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int gi = i0 + 32 * wi + 16 * bi + (lane >> 4) + 4 * r, gj = j0 + 32 * wj + 16 * bj + (lane & 15);
+        if (gi < m && gj < n) {
+          if (SPLIT)
+            P[((long)blockIdx.z * m + gi) * n + gj] = acc[bi][bj][r];
+          else
+            C[(long)gi * rsc + (long)gj * csc] = cv[bi][bj][r];
+        }
+      }
+}
+
+// operand load mode for k_dgemm_mfma from the strides along k and along the other index:
+// 1 = 16-byte pairs along k, 2 = pairs along the other index, 0 = scalar loads
+inline int dmode(const double* p, long k_stride, long other_stride) {
+  if ((uintptr_t)p % 16 != 0) return 0;
+  if (k_stride == 1 && other_stride % 2 == 0) return 1;
+  if (other_stride == 1 && k_stride % 2 == 0) return 2;
+  return 0;
+}
+
 // Ordered fold of per-panel chains: C = fma(alpha, P_p, C') for p = 0, 1, ... (see file header).
 template <typename T>
 __global__ __launch_bounds__(256) void k_combine(int m, int n, int np, T alpha, int beta_one, const T* __restrict__ P,
@@ -167,6 +344,28 @@ hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, int beta_one
   }
   const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM, 1);
   const int np = (k + CDCLQ_KC - 1) / CDCLQ_KC;
+  if constexpr (std::is_same<T, double>::value) {
+    static_assert(DBM == BM && DBN == BN, "same tiling as the VALU kernel");
+    const int am = dmode(A, csa, rsa), bm = dmode(B, rsb, csb);
+    if (np > 1 && partials != nullptr && !lower) {
+      dim3 g3 = grid;
+      g3.z = np;
+      hipLaunchKernelGGL((k_dgemm_mfma<true, false>), g3, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa, am,
+                         B, rsb, csb, bm, C, rsc, csc, partials, bt);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL((k_combine<T>), dim3((unsigned)(((long)m * n + 255) / 256)), dim3(256), 0, st, m, n, np,
+                         alpha, beta_one, (const T*)partials, C, rsc, csc);
+      return hipGetLastError();
+    }
+    if (lower)
+      hipLaunchKernelGGL((k_dgemm_mfma<false, true>), grid, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa,
+                         am, B, rsb, csb, bm, C, rsc, csc, (double*)nullptr, bt);
+    else
+      hipLaunchKernelGGL((k_dgemm_mfma<false, false>), grid, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa,
+                         am, B, rsb, csb, bm, C, rsc, csc, (double*)nullptr, bt);
+    return hipGetLastError();
+  }
   if (np > 1 && partials != nullptr && !lower) {
     dim3 g3 = grid;
     g3.z = np;
