@@ -103,10 +103,11 @@ def cpu_baseline(spec: dict, cores: int) -> dict:
             "phases_s": {"gram": round(gram_full, 2), "factor": round(fac_full, 2), "quant": round(quant_full, 2)}}
 
 
-def recorded_traffic(config: str):
+def recorded_traffic(summary: str):
     """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE, calibrated against a copy of known size); None if not recorded."""
-    path = os.path.join(ROOT, "profiles", f"gram_{config}_traffic.md")
+    profiles/<summary>.md (FETCH_SIZE + WRITE_SIZE, calibrated against a copy of known size);
+    None if not recorded."""
+    path = os.path.join(ROOT, "profiles", f"{summary}.md")
     try:
         with open(path) as f:
             for line in f:
@@ -142,6 +143,152 @@ def profile_gram(ctx, spec, xs, h64s):
                       "algorithmic_read_bytes": x_bytes + h_bytes, "algorithmic_write_bytes": h_bytes}), flush=True)
 
 
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E (AMD published)
+
+
+def container_layers(spec):
+    """(name, d_out, d_in) of the layer's quantized matrices."""
+    return [(name, d_out, spec["inputs"][key]) for name, d_out, key in spec["layers"]]
+
+
+def container_inputs(spec, seed=77):
+    """Synthetic engine outputs of one layer in the engine's form: 4-bit codes, f16-exact scales,
+    integer zero points, a random act-order permutation, group 128 (what quantize_layer writes)."""
+    rng = np.random.default_rng(seed)
+    g, bits = spec["cfg"]["group"], spec["cfg"]["bits"]
+    out = {}
+    for name, d_out, n in container_layers(spec):
+        ng = (n + g - 1) // g
+        codes = rng.integers(0, 1 << bits, (d_out, n), dtype=np.uint8)
+        scales = rng.uniform(2e-4, 2e-2, (d_out, ng)).astype(np.float16).astype(np.float32)
+        zeros = rng.integers(0, 1 << bits, (d_out, ng)).astype(np.float32)
+        perm = rng.permutation(n).astype(np.uint32)
+        out[name] = (codes, scales, zeros, perm, np.full(ng, bits, np.uint8))
+    return out
+
+
+def container_bytes(d_out, n, g, bits, out_bytes=2):
+    """Algorithmic HBM bytes of one dequantization launch: packed rows, f16 scales and u8 zeros
+    read once, the output written once, plus the per-column map (8 B per column)."""
+    ng = (n + g - 1) // g
+    rb = (n * bits + 7) // 8
+    return d_out * rb + d_out * ng * 3 + d_out * n * out_bytes + 8 * n
+
+
+def container_bench(args, spec):
+    import cdclq
+
+    ctx = cdclq.Context(0)
+    L = cdclq.lib()
+    g, bits = spec["cfg"]["group"], spec["cfg"]["bits"]
+    host = container_inputs(spec)
+    dev = {}
+    for name, d_out, n in container_layers(spec):
+        codes, scales, zeros, perm, gbits = host[name]
+        ng = gbits.size
+        rb = cdclq.row_bytes(n, g, gbits)
+        dev[name] = dict(
+            codes=cdclq.DeviceArray.from_host(ctx, codes), scales=cdclq.DeviceArray.from_host(ctx, scales),
+            zeros=cdclq.DeviceArray.from_host(ctx, zeros), perm=cdclq.DeviceArray.from_host(ctx, perm),
+            gbits=gbits, rb=rb, qw=cdclq.DeviceArray(ctx, (d_out, rb), np.uint8),
+            s16=cdclq.DeviceArray(ctx, (d_out, ng), np.uint16), qz=cdclq.DeviceArray(ctx, (d_out, ng), np.uint8),
+            p32=cdclq.DeviceArray(ctx, (n,), np.int32), out=cdclq.DeviceArray(ctx, (d_out, n), np.uint16))
+
+    def step():
+        for name, d_out, n in container_layers(spec):
+            d = dev[name]
+            ng = d["gbits"].size
+            ctx.check(L.cdclq_pack_layer_device(ctx.ptr, d_out, n, g, d["gbits"].ctypes.data, ng, d["codes"].ptr,
+                                                d["scales"].ptr, d["zeros"].ptr, d["perm"].ptr, d["qw"].ptr,
+                                                d_out * d["rb"], d["s16"].ptr, d["qz"].ptr, d["p32"].ptr))
+            ctx.check(L.cdclq_dequantize_packed_device(ctx.ptr, d_out, n, g, d["gbits"].ctypes.data, ng, d["qw"].ptr,
+                                                       d_out * d["rb"], d["s16"].ptr, d["qz"].ptr, d["p32"].ptr,
+                                                       cdclq.DTYPE_BF16, d["out"].ptr))
+
+    if args.profile:
+        # counter-collection run: 1 GiB device-to-device copy (byte-counter calibration), one step
+        import ctypes
+        hip = ctypes.CDLL("libamdhip64.so")
+        nb = 1 << 30
+        a, b = cdclq.DeviceArray(ctx, (nb,), np.uint8), cdclq.DeviceArray(ctx, (nb,), np.uint8)
+        assert hip.hipMemcpy(b.ptr, a.ptr, ctypes.c_size_t(nb), 3) == 0
+        assert hip.hipDeviceSynchronize() == 0
+        step()
+        print(json.dumps({"profile": "container", "copy_bytes": nb}), flush=True)
+        ctx.close()
+        return
+    for i in range(args.warmup):
+        step()
+    ctx.set_timing(True)
+    ctx.reset_timing()
+    times = []
+    for i in range(args.steps):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+        log(f"[bench] container step {i} {times[-1] * 1e3:.3f} ms")
+    ph = ctx.timing()
+    ctx.set_timing(False)
+    ms_per_step = 1000.0 * sum(times) / len(times)
+    byts = args.steps * sum(container_bytes(d_out, n, g, bits) for _, d_out, n in container_layers(spec))
+    pack_bytes = args.steps * sum(d_out * n + d_out * ((n * bits + 7) // 8) + d_out * ((n + g - 1) // g) * 11
+                                  for _, d_out, n in container_layers(spec))
+    dq_ms, pk_ms = ph["dequant"]["ms"], ph["pack"]["ms"]
+    achieved = byts / (dq_ms * 1e-3) / 1e9 if dq_ms > 0 else 0.0
+    log(f"[bench] device ms per step: pack {pk_ms / args.steps:.3f} dequant {dq_ms / args.steps:.3f}")
+    result = {
+        "metric": "sec per Llama-3-8B-shaped layer: pack to cdclq-v1 + dequantize to bf16 (7 matrices)",
+        "value": round(ms_per_step / 1000.0, 6),
+        "unit": "s/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic engine outputs (4-bit codes, f16 scales, integer zeros, random act-order perm)",
+        "config": {"workload": "llama3-8b decoder layer container (" + spec["workload"] + ")",
+                   "layers": {name: [d_out, n] for name, d_out, n in container_layers(spec)},
+                   "bits": bits, "group": g, "out_dtype": "bf16", "parallelism": "1 GPU"},
+        "phases_ms_per_step": {"pack": round(pk_ms / args.steps, 4), "dequant": round(dq_ms / args.steps, 4)},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k_dequant_rows (packed rows -> bf16, original column order)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": recorded_traffic("dequant_container_traffic"),
+            "traffic_unit": "bytes per launch, mean over the 7 launches (profiles/dequant_container_traffic.md)",
+            "launches": ph["dequant"]["launches"],
+            "pack_kernels_gbs": round(pack_bytes / (pk_ms * 1e-3) / 1e9, 1) if pk_ms > 0 else None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        import oracle as O
+
+        cores = min(os.cpu_count() or 1, 16)
+        O.set_threads(cores)
+        name, d_out, n = container_layers(spec)[0]
+        codes, scales, zeros, perm, gbits = host[name]
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 10.0 or reps == 0:
+            qw, s16, qz, p32 = O.pack_layer(codes, scales, zeros, perm, gbits, g)
+            O.dequantize_packed(qw, s16, qz, p32, gbits, g, "BF16")
+            reps += 1
+        t_one = (time.perf_counter() - t0) / reps
+        total = sum(do * nn for _, do, nn in container_layers(spec))
+        result["cpu_baseline"] = {
+            "value": round(t_one * total / (d_out * n), 4), "unit": "s/layer", "cores": cores, "kind": "port",
+            "sample": f"oracle pack_layer + dequantize_packed (BF16) of {name} ({d_out}x{n}), {reps} reps, "
+                      f"scaled by element count to the layer's 7 matrices"}
+    print(json.dumps(result), flush=True)
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -152,6 +299,11 @@ def main():
     ap.add_argument("--profile-gram", action="store_true",
                     help="counter-collection run: one 1 GiB device-to-device copy (calibration of the HBM "
                          "byte counters), then one launch of the dominant kernel on this config's inputs")
+    ap.add_argument("--workload", default="layer", choices=["layer", "container"],
+                    help="layer: the headline quantization step; container: pack + dequantize of the "
+                         "layer's quantized matrices (cdclq-v1)")
+    ap.add_argument("--profile", action="store_true",
+                    help="with --workload container: counter-collection run (1 GiB copy + one step)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
@@ -162,6 +314,9 @@ def main():
     import cdclq
 
     spec = CONFIGS[args.config]
+    if args.workload == "container":
+        container_bench(args, spec)
+        return
     T = spec["tokens"]
     ctx = cdclq.Context(0)
     log(f"[bench] {spec['workload']}: generating inputs in HBM")
@@ -255,7 +410,7 @@ def main():
             "peak": FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
-            "traffic": recorded_traffic(args.config),
+            "traffic": recorded_traffic(f"gram_{args.config}_traffic"),
             "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, profiles/gram_c4_traffic.md)",
             "launches": gram_launches,
         },

@@ -30,7 +30,7 @@ LIB_PATH = os.path.join(_HERE, "libcdclq_hip.so")
 
 OK, INVALID_ARG, NOT_PD, NON_FINITE, DEVICE, OOM = range(6)
 PHASE_GRAM, PHASE_FACTOR, PHASE_GPTQ, PHASE_REPAIR, PHASE_TARGET = range(5)
-PHASE_NAMES = ["gram", "factor", "gptq", "repair", "target"]
+PHASE_NAMES = ["gram", "factor", "gptq", "repair", "target", "pack", "dequant"]
 
 
 class CdclqError(RuntimeError):
@@ -92,6 +92,13 @@ def lib() -> C.CDLL:
         "cdclq_upper_chol_of_inverse": ([vp, vp, sz, vp], i32),
         "cdclq_upper_chol_of_inverse_device": ([vp, vp, sz, vp], i32),
         "cdclq_proxy_loss": ([vp, vp, vp, sz, sz, vp, C.POINTER(C.c_double)], i32),
+        "cdclq_row_bytes": ([sz, sz, vp, sz, C.POINTER(sz)], i32),
+        "cdclq_pack_layer": ([vp, sz, sz, sz, vp, sz, vp, vp, vp, vp, vp, sz, vp, vp, vp], i32),
+        "cdclq_pack_layer_device": ([vp, sz, sz, sz, vp, sz, vp, vp, vp, vp, vp, sz, vp, vp, vp], i32),
+        "cdclq_dequantize_packed": ([vp, sz, sz, sz, vp, sz, vp, sz, vp, vp, vp, i32, vp], i32),
+        "cdclq_dequantize_packed_device": ([vp, sz, sz, sz, vp, sz, vp, sz, vp, vp, vp, i32, vp], i32),
+        "cdclq_dequantize_layer": ([vp, sz, sz, sz, sz, vp, vp, vp, vp, i32, vp], i32),
+        "cdclq_dequantize_layer_device": ([vp, sz, sz, sz, sz, vp, vp, vp, vp, i32, vp], i32),
         "cdclq_device_alloc": ([vp, sz, C.POINTER(vp)], i32),
         "cdclq_device_free": ([vp, vp], i32),
         "cdclq_memcpy_h2d": ([vp, vp, vp, sz], i32),
@@ -126,6 +133,8 @@ def exported_symbols() -> list[str]:
         "cdclq_proxy_loss", "cdclq_device_alloc", "cdclq_device_free", "cdclq_memcpy_h2d", "cdclq_memcpy_d2h",
         "cdclq_memset_device", "cdclq_synth_normal_device", "cdclq_synth_outlier_scales", "cdclq_synth_tokens_device", "cdclq_f64_to_f32_device",
         "cdclq_ctx_set_timing", "cdclq_ctx_reset_timing", "cdclq_ctx_get_timing",
+        "cdclq_row_bytes", "cdclq_pack_layer", "cdclq_pack_layer_device", "cdclq_dequantize_packed",
+        "cdclq_dequantize_packed_device", "cdclq_dequantize_layer", "cdclq_dequantize_layer_device",
     ]
 
 
@@ -415,6 +424,104 @@ def synth_outlier_scales(seed: int, n: int, frac: float, factor: float) -> np.nd
     rc = lib().cdclq_synth_outlier_scales(seed, n, frac, factor, out.ctypes.data)
     if rc != OK:
         raise CdclqError(rc, "cdclq_synth_outlier_scales failed")
+    return out
+
+
+# ---------------------------------------------------------------- packed container cdclq-v1
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+_DTYPE_CODE = {"F32": DTYPE_F32, "F16": DTYPE_F16, "BF16": DTYPE_BF16}
+_DTYPE_NP = {DTYPE_F32: np.float32, DTYPE_F16: np.uint16, DTYPE_BF16: np.uint16}
+
+
+def _dtype_code(dtype) -> int:
+    return _DTYPE_CODE[dtype.upper()] if isinstance(dtype, str) else int(dtype)
+
+
+def row_bytes(n: int, g: int, gbits) -> int:
+    """quant::row_bytes (src/quant.rs:102-104)."""
+    gbits = np.ascontiguousarray(gbits, np.uint8)
+    out = C.c_size_t()
+    rc = lib().cdclq_row_bytes(n, g, gbits.ctypes.data, gbits.size, C.byref(out))
+    if rc != OK:
+        raise CdclqError(rc, f"invalid packed layout (n={n}, group={g}, gbits={gbits.tolist()[:8]}...)")
+    return out.value
+
+
+def pack_layer(ctx: Context, ql: QLayer):
+    """QLayer::pack + io::packed_tensors (src/quant.rs:207-214, src/io.rs:244-264) on the GPU:
+    (qweight u8 [d_out, row_bytes], scales f16 bits u16 [d_out, ng], qzeros u8 [d_out, ng],
+    perm i32 [d_in])."""
+    gbits = np.ascontiguousarray(ql.gbits, np.uint8)
+    ng = gbits.size
+    rb = row_bytes(ql.d_in, ql.group, gbits)
+    codes = np.ascontiguousarray(ql.codes, np.uint8)
+    scales, zeros = _f32(ql.scales), _f32(ql.zeros)
+    perm = np.ascontiguousarray(ql.perm, np.uint32)
+    qw = np.zeros((ql.d_out, rb), np.uint8)
+    s16 = np.zeros((ql.d_out, ng), np.uint16)
+    qz = np.zeros((ql.d_out, ng), np.uint8)
+    p32 = np.zeros(ql.d_in, np.int32)
+    ctx.check(lib().cdclq_pack_layer(ctx.ptr, ql.d_out, ql.d_in, ql.group, gbits.ctypes.data, ng, codes.ctypes.data,
+                                     scales.ctypes.data, zeros.ctypes.data, perm.ctypes.data, qw.ctypes.data, qw.size,
+                                     s16.ctypes.data, qz.ctypes.data, p32.ctypes.data))
+    return qw, s16, qz, p32
+
+
+def packed_tensors(layer: str, ql: QLayer, ctx: Context) -> dict:
+    """io::packed_tensors (src/io.rs:244-264): the six tensors of one packed layer, name ->
+    (safetensors dtype, numpy array). F16 scales are carried as their uint16 bit patterns."""
+    qw, s16, qz, p32 = pack_layer(ctx, ql)
+    return {
+        f"{layer}.qweight": ("U8", qw),
+        f"{layer}.scales": ("F16", s16),
+        f"{layer}.qzeros": ("U8", qz),
+        f"{layer}.perm": ("I32", p32),
+        f"{layer}.gbits": ("U8", np.ascontiguousarray(ql.gbits, np.uint8).copy()),
+        f"{layer}.gsize": ("I32", np.array([ql.group], np.int32)),
+    }
+
+
+def dequantize_packed(ctx: Context, qweight, scales_f16, qzeros, perm_i32, gbits, group: int, dtype="F32"):
+    """io::read_packed_layer + QLayer::dequantize + io::f32_to_bytes (src/io.rs:270-293,
+    src/quant.rs:189-236, src/io.rs:50-57) on the GPU. Returns d_out x d_in in the original column
+    order: float32 for F32, uint16 bit patterns for F16 / BF16."""
+    dt = _dtype_code(dtype)
+    qweight = np.ascontiguousarray(qweight, np.uint8)
+    s16 = np.ascontiguousarray(scales_f16, np.uint16)
+    qz = np.ascontiguousarray(qzeros, np.uint8)
+    p32 = np.ascontiguousarray(perm_i32, np.int32)
+    gbits = np.ascontiguousarray(gbits, np.uint8)
+    d_out, d_in = qweight.shape[0], p32.size
+    out = np.zeros((d_out, d_in), _DTYPE_NP.get(dt, np.float32))
+    ctx.check(lib().cdclq_dequantize_packed(ctx.ptr, d_out, d_in, group, gbits.ctypes.data, gbits.size,
+                                            qweight.ctypes.data, qweight.size, s16.ctypes.data, qz.ctypes.data,
+                                            p32.ctypes.data, dt, out.ctypes.data))
+    return out
+
+
+def read_packed_dequantized(tensors: dict, layer: str, ctx: Context, dtype="F32"):
+    """The `cdclq dequant` expansion of one layer (src/pipeline.rs:239-262) from a dict in the
+    packed_tensors() form; a missing companion tensor raises with its name (src/io.rs:271-274)."""
+    def get(suffix):
+        key = f"{layer}.{suffix}"
+        if key not in tensors:
+            raise KeyError(f"{key}: missing")
+        v = tensors[key]
+        return v[1] if isinstance(v, tuple) else v
+    qw, s16, qz, p32, gb, gs = (get(x) for x in ("qweight", "scales", "qzeros", "perm", "gbits", "gsize"))
+    return dequantize_packed(ctx, qw, s16, qz, p32, gb, int(np.asarray(gs).ravel()[0]), dtype)
+
+
+def dequantize_layer(ctx: Context, ql: QLayer, dtype="F32"):
+    """QLayer::dequantize + io::f32_to_bytes (src/quant.rs:189-202, src/io.rs:50-57) on the GPU."""
+    dt = _dtype_code(dtype)
+    codes = np.ascontiguousarray(ql.codes, np.uint8)
+    scales, zeros = _f32(ql.scales), _f32(ql.zeros)
+    perm = np.ascontiguousarray(ql.perm, np.uint32)
+    out = np.zeros((ql.d_out, ql.d_in), _DTYPE_NP.get(dt, np.float32))
+    ctx.check(lib().cdclq_dequantize_layer(ctx.ptr, ql.d_out, ql.d_in, ql.group, int(np.asarray(ql.gbits).size),
+                                           codes.ctypes.data, scales.ctypes.data, zeros.ctypes.data, perm.ctypes.data,
+                                           dt, out.ctypes.data))
     return out
 
 

@@ -17,21 +17,12 @@
 
 #include "cdclq.h"
 #include "cdclq_dev.h"
+#include "ctx.h"
 #include "kernels.h"
 
 namespace {
 
 using namespace cdclq;
-
-struct DevBuf {
-  void* p = nullptr;
-  size_t cap = 0;
-};
-
-struct TimedRegion {
-  int phase;
-  hipEvent_t a, b;
-};
 
 double now_secs() {
   using namespace std::chrono;
@@ -53,101 +44,6 @@ std::string rust_lower_exp(double d) {
   return std::string(buf) + "e" + std::to_string(ex);
 }
 
-}  // namespace
-
-struct cdclq_ctx {
-  int device = 0;
-  hipStream_t st = nullptr;
-  hipStream_t st2 = nullptr;  // side stream of the factorisation's look-ahead (default priority)
-  hipEvent_t ev_col = nullptr, ev_panel = nullptr;
-  std::string err;
-  // workspace (grow-only)
-  DevBuf w_in, h_in, m_in, x_in, y_in, h64_in, u_out, codes_o, scales_o, zeros_o;
-  DevBuf wp, wwork, wq, ebuf, gbits_d, perm_d, deadp_d, dead_d, diag_d, colsq_d, invd, colloss_d;
-  DevBuf G, part, rlog, rcnt, clog, ccnt, active_d, sel_d, ld_d, upd_d, mp, t1, t2, a64, y64, tbuf, tpart, status_d, rtiles_d,
-      tiles_d, proxy_p, cs_d;
-  // one-entry PrepCache (src/engine.rs:207-223): key, perm, damping and the device factors
-  bool cache_valid = false;
-  std::string cache_key;
-  std::vector<uint32_t> cache_perm;
-  size_t cache_n = 0;
-  double cache_damp = 0.0;
-  DevBuf cache_u, cache_h32;
-  // timing
-  bool timing = false;
-  std::vector<TimedRegion> pending;
-  double ms[CDCLQ_PHASE_COUNT] = {};
-  uint64_t launches[CDCLQ_PHASE_COUNT] = {};
-};
-
-namespace {
-
-int fail(cdclq_ctx* ctx, int code, const std::string& msg) {
-  ctx->err = msg;
-  return code;
-}
-
-#define HIPCK(expr)                                                                                   \
-  do {                                                                                                \
-    hipError_t e_ = (expr);                                                                           \
-    if (e_ != hipSuccess)                                                                             \
-      return fail(ctx, CDCLQ_DEVICE, std::string("HIP error '") + hipGetErrorString(e_) + "' in " #expr); \
-  } while (0)
-#define CK(expr)                       \
-  do {                                 \
-    int rc_ = (expr);                  \
-    if (rc_ != CDCLQ_OK) return rc_;   \
-  } while (0)
-
-int ensure(cdclq_ctx* ctx, DevBuf& b, size_t bytes) {
-  if (bytes == 0) bytes = 256;
-  if (b.cap >= bytes) return CDCLQ_OK;
-  if (b.p) {
-    hipError_t e = hipFree(b.p);
-    b.p = nullptr;
-    b.cap = 0;
-    if (e != hipSuccess) return fail(ctx, CDCLQ_DEVICE, std::string("hipFree failed: ") + hipGetErrorString(e));
-  }
-  hipError_t e = hipMalloc(&b.p, bytes);
-  if (e != hipSuccess) {
-    b.p = nullptr;
-    (void)hipGetLastError();
-    return fail(ctx, CDCLQ_OOM, "device allocation of " + std::to_string(bytes) + " bytes failed (" +
-                                    hipGetErrorString(e) + ")");
-  }
-  b.cap = bytes;
-  return CDCLQ_OK;
-}
-
-template <class T>
-T* P(DevBuf& b) {
-  return static_cast<T*>(b.p);
-}
-
-void free_buf(DevBuf& b) {
-  if (b.p) (void)hipFree(b.p);
-  b.p = nullptr;
-  b.cap = 0;
-}
-
-struct PhaseScope {
-  cdclq_ctx* ctx;
-  int phase;
-  hipEvent_t a = nullptr;
-  PhaseScope(cdclq_ctx* c, int ph) : ctx(c), phase(ph) {
-    if (ctx->timing && hipEventCreate(&a) == hipSuccess) (void)hipEventRecord(a, ctx->st);
-  }
-  ~PhaseScope() {
-    if (!ctx->timing || !a) return;
-    hipEvent_t b = nullptr;
-    if (hipEventCreate(&b) == hipSuccess) {
-      (void)hipEventRecord(b, ctx->st);
-      ctx->pending.push_back({phase, a, b});
-    } else {
-      (void)hipEventDestroy(a);
-    }
-  }
-};
 
 void drain_timing(cdclq_ctx* ctx) {
   for (auto& r : ctx->pending) {
@@ -156,8 +52,8 @@ void drain_timing(cdclq_ctx* ctx) {
       ctx->ms[r.phase] += ms;
       ctx->launches[r.phase] += 1;
     }
-    (void)hipEventDestroy(r.a);
-    (void)hipEventDestroy(r.b);
+    ctx->event_pool.push_back(r.a);
+    ctx->event_pool.push_back(r.b);
   }
   ctx->pending.clear();
 }
@@ -778,8 +674,12 @@ void cdclq_ctx_destroy(cdclq_ctx* ctx) {
                     &ctx->invd, &ctx->colloss_d, &ctx->G, &ctx->part, &ctx->rlog, &ctx->rcnt, &ctx->clog, &ctx->ccnt, &ctx->active_d, &ctx->rtiles_d,
                     &ctx->sel_d, &ctx->ld_d, &ctx->upd_d, &ctx->mp, &ctx->t1, &ctx->t2, &ctx->a64, &ctx->y64,
                     &ctx->tbuf, &ctx->tpart, &ctx->status_d, &ctx->tiles_d, &ctx->proxy_p, &ctx->cs_d,
-                    &ctx->cache_u, &ctx->cache_h32};
+                    &ctx->cache_u, &ctx->cache_h32, &ctx->pk_flag};
   for (DevBuf* b : bufs) free_buf(*b);
+  for (DevBuf& b : ctx->pk_in) free_buf(b);
+  for (DevBuf& b : ctx->pk_out) free_buf(b);
+  for (DevBuf& b : ctx->pk_tab) free_buf(b);
+  for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
   (void)hipStreamSynchronize(ctx->st2);
   (void)hipEventDestroy(ctx->ev_col);
   (void)hipEventDestroy(ctx->ev_panel);

@@ -87,6 +87,27 @@ hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, i
 hipError_t pass_accum(hipStream_t st, int rows, int rc, int nchunks, int nref, const double* rlog,
                       const uint32_t* rcnt, int ncd, int cap, const double* clog, const uint32_t* ccnt,
                       const uint8_t* active, double* ld, uint64_t* upd);
+// ---- k_pack.hip: packed container cdclq-v1 (bit streams LSB first, per-group widths)
+// qw (d_out x rb) from codes (d_out x n); coff[j] = bit offset of code j (coff[n] = total bits),
+// wfirst[w] = first code whose 8-bit window reaches bit 32 w of a row. With only_if non-null the
+// launch does nothing unless *only_if == epoch.
+hipError_t pack_rows(hipStream_t st, long d_out, int n, int rb, const uint8_t* codes, const uint32_t* coff,
+                     const int* wfirst, uint8_t* qw, const uint32_t* only_if, uint32_t epoch);
+// fast path when every run of 8 columns lies in one group (rdesc[k] = byte offset of run k << 4 |
+// width); *spill is set to epoch if a code exceeds its width (then pack_rows redoes the layer)
+hipError_t pack_runs(hipStream_t st, long d_out, int n, int rb, const uint8_t* codes, const uint32_t* rdesc,
+                     uint8_t* qw, uint32_t* spill, uint32_t epoch);
+hipError_t pack_meta(hipStream_t st, long count, const float* scales, const float* zeros, uint16_t* s16, uint8_t* z8);
+// output column map: last[c] = max j with perm[j] == c (-1: none), cdesc[c] = bit offset << 4 |
+// width (packed) or last[c] (unpacked), cgrp[c] = last[c] / g; *bad is set to epoch if some
+// perm[j] >= n.
+hipError_t column_map(hipStream_t st, int n, int g, bool packed, const uint32_t* perm, const uint32_t* coff,
+                      const uint8_t* cwid, int* last, uint32_t* cdesc, int* cgrp, uint32_t* bad, uint32_t epoch);
+// out (d_out x n, dtype) from packed rows (srcb = row bytes) or u8 code rows (srcb = n)
+hipError_t dequant_rows(hipStream_t st, bool packed, int dtype, long d_out, int n, int ng, int srcb,
+                        const uint8_t* src, const uint32_t* cdesc, const int* cgrp, const void* scales,
+                        const void* zeros, void* out);
+
 hipError_t synth_normal(hipStream_t st, uint64_t seed, uint64_t offset, size_t count, float sigma, float* out);
 hipError_t synth_tokens(hipStream_t st, uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale,
                         float* x);

@@ -137,6 +137,54 @@ int cdclq_upper_chol_of_inverse_device(cdclq_ctx* ctx, const double* h, size_t n
 int cdclq_proxy_loss(cdclq_ctx* ctx, const float* w_t, const float* w_hat, size_t rows, size_t n, const float* h,
                      double* out);
 
+/* ---- Packed container "cdclq-v1" (src/io.rs:227-293, src/quant.rs:98-236) ----
+ * A packed layer is six tensors: .qweight u8 [d_out, row_bytes] (each row the codes of that row in
+ * permuted column order, appended low bit first with the width of their group, last byte
+ * zero-filled), .scales f16 [d_out, ngroups], .qzeros u8 [d_out, ngroups], .perm i32 [d_in],
+ * .gbits u8 [ngroups], .gsize i32 [1]. Column j of the permuted order belongs to group j / group.
+ * Group widths must be in 1..=8 (the engine writes 2..=8) and ngroups >= ceil(d_in / group). */
+typedef enum cdclq_dtype { CDCLQ_DTYPE_F32 = 0, CDCLQ_DTYPE_F16 = 1, CDCLQ_DTYPE_BF16 = 2 } cdclq_dtype;
+
+/* quant::row_bytes (src/quant.rs:102-104): ceil(sum over j < d_in of gbits[j / group] / 8). */
+int cdclq_row_bytes(size_t d_in, size_t group, const uint8_t* gbits, size_t ngroups, size_t* row_bytes);
+
+/* io::packed_tensors (src/io.rs:244-264) with QLayer::pack / pack_row (src/quant.rs:207-214,
+ * :113-131): the bytes of .qweight (qweight_bytes >= d_out * row_bytes), .scales (f16 bit
+ * patterns, half::f16::from_f32), .qzeros (`zero as u8`) and .perm (`perm as i32`) for one layer.
+ * codes d_out x d_in (permuted order), scales / zeros d_out x ngroups f32, perm d_in. */
+int cdclq_pack_layer(cdclq_ctx* ctx, size_t d_out, size_t d_in, size_t group, const uint8_t* gbits, size_t ngroups,
+                     const uint8_t* codes, const float* scales, const float* zeros, const uint32_t* perm,
+                     uint8_t* qweight, size_t qweight_bytes, uint16_t* scales_f16, uint8_t* qzeros, int32_t* perm_i32);
+/* Same contract; every array except gbits is device memory (codes never leave the GPU). */
+int cdclq_pack_layer_device(cdclq_ctx* ctx, size_t d_out, size_t d_in, size_t group, const uint8_t* gbits,
+                            size_t ngroups, const uint8_t* codes, const float* scales, const float* zeros,
+                            const uint32_t* perm, uint8_t* qweight, size_t qweight_bytes, uint16_t* scales_f16,
+                            uint8_t* qzeros, int32_t* perm_i32);
+
+/* The `cdclq dequant` expansion of one layer: io::read_packed_layer (src/io.rs:270-293), i.e.
+ * QLayer::from_packed (src/quant.rs:219-236) + QLayer::dequantize (src/quant.rs:189-202), then
+ * io::f32_to_bytes (src/io.rs:50-57) into `dtype` (cdclq_dtype). out is d_out x d_in in the
+ * original column order: 4-byte floats for F32, 16-bit patterns for F16 / BF16 (bit-identical to
+ * the reference for every non-NaN value; a NaN stays a NaN, its payload is platform-defined as in
+ * the reference). Every perm entry must be in 0..d_in (the reference panics otherwise); a repeated
+ * entry keeps the reference's scatter result (the later column wins, unwritten columns are 0). */
+int cdclq_dequantize_packed(cdclq_ctx* ctx, size_t d_out, size_t d_in, size_t group, const uint8_t* gbits,
+                            size_t ngroups, const uint8_t* qweight, size_t qweight_bytes, const uint16_t* scales_f16,
+                            const uint8_t* qzeros, const int32_t* perm_i32, int dtype, void* out);
+int cdclq_dequantize_packed_device(cdclq_ctx* ctx, size_t d_out, size_t d_in, size_t group, const uint8_t* gbits,
+                                   size_t ngroups, const uint8_t* qweight, size_t qweight_bytes,
+                                   const uint16_t* scales_f16, const uint8_t* qzeros, const int32_t* perm_i32,
+                                   int dtype, void* out);
+/* QLayer::dequantize (src/quant.rs:189-202) + io::f32_to_bytes (src/io.rs:50-57) on the engine's
+ * unpacked output (the pipeline's dequant/ tensors, src/pipeline.rs:153-162): codes d_out x d_in,
+ * scales / zeros d_out x ngroups f32, perm d_in. */
+int cdclq_dequantize_layer(cdclq_ctx* ctx, size_t d_out, size_t d_in, size_t group, size_t ngroups,
+                           const uint8_t* codes, const float* scales, const float* zeros, const uint32_t* perm,
+                           int dtype, void* out);
+int cdclq_dequantize_layer_device(cdclq_ctx* ctx, size_t d_out, size_t d_in, size_t group, size_t ngroups,
+                                  const uint8_t* codes, const float* scales, const float* zeros, const uint32_t* perm,
+                                  int dtype, void* out);
+
 /* ---- Device memory staging for callers without their own GPU runtime binding. ---- */
 int cdclq_device_alloc(cdclq_ctx* ctx, size_t bytes, void** ptr);
 int cdclq_device_free(cdclq_ctx* ctx, void* ptr);
@@ -164,7 +212,9 @@ enum {
   CDCLQ_PHASE_GPTQ = 2,     /* phase 1: block sweeps + lazy GEMM */
   CDCLQ_PHASE_REPAIR = 3,   /* phase 2: refit + coordinate descent */
   CDCLQ_PHASE_TARGET = 4,   /* asymmetric target GEMMs */
-  CDCLQ_PHASE_COUNT = 5
+  CDCLQ_PHASE_PACK = 5,     /* packed container: bit-packing and metadata kernels */
+  CDCLQ_PHASE_DEQUANT = 6,  /* packed container: dequantization kernel */
+  CDCLQ_PHASE_COUNT = 7
 };
 int cdclq_ctx_set_timing(cdclq_ctx* ctx, int enable);
 int cdclq_ctx_reset_timing(cdclq_ctx* ctx);

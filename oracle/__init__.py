@@ -108,6 +108,21 @@ def lib():
         L.orc_proxy_loss.restype = C.c_double
         L.orc_rtn_layer.argtypes = [f32p, sz, sz, C.POINTER(OrcConfig), f32p]
         L.orc_dequantize.argtypes = [sz, sz, sz, u32p, sz, u8p, f32p, f32p, f32p]
+        u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+        i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+        L.orc_f32_to_f16_bits.argtypes = [C.c_float]
+        L.orc_f32_to_f16_bits.restype = C.c_uint16
+        L.orc_f16_bits_to_f32.argtypes = [C.c_uint16]
+        L.orc_f16_bits_to_f32.restype = C.c_float
+        L.orc_f32_to_bf16_bits.argtypes = [C.c_float]
+        L.orc_f32_to_bf16_bits.restype = C.c_uint16
+        L.orc_narrow.argtypes = [f32p, sz, C.c_int, C.c_void_p]
+        L.orc_row_bytes.argtypes = [sz, sz, u8p]
+        L.orc_row_bytes.restype = sz
+        L.orc_pack_row.argtypes = [u8p, sz, sz, u8p, u8p]
+        L.orc_unpack_row.argtypes = [u8p, sz, sz, u8p, u8p]
+        L.orc_pack_layer.argtypes = [sz, sz, sz, u8p, sz, u8p, f32p, f32p, u32p, u8p, u16p, u8p, i32p]
+        L.orc_dequantize_packed.argtypes = [sz, sz, sz, u8p, sz, u8p, u16p, u8p, i32p, C.c_int, C.c_void_p]
         L.orc_rng_new.argtypes = [C.c_void_p, C.c_uint64]
         L.orc_rng_next_u64.argtypes = [C.c_void_p]
         L.orc_rng_next_u64.restype = C.c_uint64
@@ -308,6 +323,75 @@ def round_f16(x: np.ndarray) -> np.ndarray:
     y = np.empty_like(x)
     lib().orc_round_f16_array(x.ravel(), y.ravel(), x.size)
     return y
+
+
+# ---------------------------------------------------------------- packed container (cdclq-v1)
+DTYPES = {"F32": 0, "F16": 1, "BF16": 2}
+_NP_OUT = {0: np.float32, 1: np.uint16, 2: np.uint16}
+
+
+def row_bytes(n: int, g: int, gbits) -> int:
+    """quant::row_bytes (src/quant.rs:102-104)."""
+    gbits = np.ascontiguousarray(gbits, np.uint8)
+    return lib().orc_row_bytes(n, g, gbits)
+
+
+def pack_row(codes, g: int, gbits) -> np.ndarray:
+    """quant::pack_row (src/quant.rs:113-131)."""
+    codes = np.ascontiguousarray(codes, np.uint8)
+    gbits = np.ascontiguousarray(gbits, np.uint8)
+    out = np.zeros(row_bytes(codes.size, g, gbits), np.uint8)
+    lib().orc_pack_row(codes, codes.size, g, gbits, out)
+    return out
+
+
+def unpack_row(data, n: int, g: int, gbits) -> np.ndarray:
+    """quant::unpack_row (src/quant.rs:136-151)."""
+    data = np.ascontiguousarray(data, np.uint8)
+    gbits = np.ascontiguousarray(gbits, np.uint8)
+    codes = np.zeros(n, np.uint8)
+    lib().orc_unpack_row(data, n, g, gbits, codes)
+    return codes
+
+
+def pack_layer(codes, scales, zeros, perm, gbits, g: int):
+    """io::packed_tensors (src/io.rs:244-264): (qweight, scales f16 bits, qzeros, perm i32)."""
+    codes = np.ascontiguousarray(codes, np.uint8)
+    d_out, n = codes.shape
+    gbits = np.ascontiguousarray(gbits, np.uint8)
+    ng = gbits.size
+    rb = row_bytes(n, g, gbits)
+    qw = np.zeros((d_out, rb), np.uint8)
+    s16 = np.zeros((d_out, ng), np.uint16)
+    qz = np.zeros((d_out, ng), np.uint8)
+    p32 = np.zeros(n, np.int32)
+    lib().orc_pack_layer(d_out, n, g, gbits, ng, codes, np.ascontiguousarray(scales, np.float32),
+                         np.ascontiguousarray(zeros, np.float32), np.ascontiguousarray(perm, np.uint32), qw, s16, qz,
+                         p32)
+    return qw, s16, qz, p32
+
+
+def dequantize_packed(qweight, scales16, qzeros, perm32, gbits, g: int, dtype: str = "F32") -> np.ndarray:
+    """io::read_packed_layer + QLayer::dequantize + io::f32_to_bytes (src/io.rs:270-293,
+    src/quant.rs:189-236, src/io.rs:50-57). F16/BF16 results are returned as uint16 bit patterns."""
+    qweight = np.ascontiguousarray(qweight, np.uint8)
+    gbits = np.ascontiguousarray(gbits, np.uint8)
+    perm32 = np.ascontiguousarray(perm32, np.int32)
+    d_out, n = qweight.shape[0], perm32.size
+    dt = DTYPES[dtype]
+    out = np.zeros((d_out, n), _NP_OUT[dt])
+    lib().orc_dequantize_packed(d_out, n, g, gbits, gbits.size, qweight, np.ascontiguousarray(scales16, np.uint16),
+                                np.ascontiguousarray(qzeros, np.uint8), perm32, dt, out.ctypes.data)
+    return out
+
+
+def narrow(v, dtype: str) -> np.ndarray:
+    """io::f32_to_bytes (src/io.rs:50-57); F16/BF16 as uint16 bit patterns."""
+    v = np.ascontiguousarray(v, np.float32)
+    dt = DTYPES[dtype]
+    out = np.zeros(v.shape, _NP_OUT[dt])
+    lib().orc_narrow(v.ravel(), v.size, dt, out.ctypes.data)
+    return out
 
 
 class Rng:

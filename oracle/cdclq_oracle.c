@@ -120,7 +120,8 @@ static float f16_bits_to_f32(uint16_t h) {
       u = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
     }
   } else if (exp == 0x1f) {
-    u = sign | 0x7f800000u | (man << 13);
+    /* infinity, or NaN with the payload kept and the quiet bit set (half 2.4.1 f16::to_f32) */
+    u = sign | 0x7f800000u | (man << 13) | (man ? 0x400000u : 0u);
   } else {
     u = sign | ((exp - 15 + 127) << 23) | (man << 13);
   }
@@ -1183,4 +1184,129 @@ void orc_synth_tokens(uint64_t seed, uint64_t row0, size_t t, size_t n, const fl
   for (size_t r = 0; r < t; ++r)
     for (size_t j = 0; j < n; ++j)
       x[r * n + j] = orc_synth_normal_at(seed, (row0 + r) * (uint64_t)n + j) * (ch_scale ? ch_scale[j] : 1.0f);
+}
+
+/* ------------------------------------------------------------------ packed container (cdclq-v1)
+ * The dtype conversions below restate the `half` crate (2.4.1, a Cargo.lock dependency that is not
+ * vendored in the reference): f16::from_f32 / bf16::from_f32 are IEEE round-to-nearest-even
+ * narrowings (overflow to infinity; NaN keeps its sign and upper payload bits and gets the quiet
+ * bit), f16::to_f32 widens exactly (NaN quieted the same way). */
+uint16_t orc_f32_to_f16_bits(float x) { return f32_to_f16_bits(x); }
+float orc_f16_bits_to_f32(uint16_t h) { return f16_bits_to_f32(h); }
+
+uint16_t orc_f32_to_bf16_bits(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  uint32_t q = u >> 16, rem = u & 0xffffu;
+  if (rem > 0x8000u || (rem == 0x8000u && (q & 1u))) q++;
+  return (uint16_t)q;
+}
+
+/* io::f32_to_bytes (src/io.rs:50-57): dtype 0 = F32 (bytes as is), 1 = F16, 2 = BF16. */
+void orc_narrow(const float* v, size_t count, int dtype, void* out) {
+  if (dtype == 0) {
+    memcpy(out, v, count * 4);
+  } else {
+    uint16_t* o = (uint16_t*)out;
+    for (size_t i = 0; i < count; ++i) o[i] = dtype == 1 ? f32_to_f16_bits(v[i]) : orc_f32_to_bf16_bits(v[i]);
+  }
+}
+
+/* quant::row_bits / row_bytes (src/quant.rs:98-104) */
+size_t orc_row_bytes(size_t n, size_t g, const uint8_t* gbits) {
+  size_t bits = 0;
+  for (size_t j = 0; j < n; ++j) bits += gbits[j / g];
+  return (bits + 7) / 8;
+}
+
+/* quant::pack_row (src/quant.rs:113-131): codes appended low bit first into a 64-bit
+ * accumulator (OR, no masking), flushed a byte at a time; the trailing partial byte is written. */
+void orc_pack_row(const uint8_t* codes, size_t n, size_t g, const uint8_t* gbits, uint8_t* out) {
+  uint64_t acc = 0;
+  uint32_t nacc = 0;
+  size_t o = 0;
+  for (size_t j = 0; j < n; ++j) {
+    uint32_t b = gbits[j / g];
+    uint64_t c = codes[j];
+    if (g_mut == 9) c &= (1u << b) - 1u; /* planted: codes masked to their width (no spill) */
+    if (g_mut == 10 && b > 1) c = ((c & 1u) << (b - 1)) | (c >> 1); /* planted: bit order rotated */
+    acc |= c << nacc;
+    nacc += b;
+    while (nacc >= 8) {
+      out[o++] = (uint8_t)(acc & 0xffu);
+      acc >>= 8;
+      nacc -= 8;
+    }
+  }
+  if (nacc > 0) out[o] = (uint8_t)(acc & 0xffu);
+}
+
+/* quant::unpack_row (src/quant.rs:136-151) */
+void orc_unpack_row(const uint8_t* data, size_t n, size_t g, const uint8_t* gbits, uint8_t* codes) {
+  uint64_t acc = 0;
+  uint32_t nacc = 0;
+  size_t o = 0;
+  for (size_t j = 0; j < n; ++j) {
+    uint32_t b = gbits[j / g];
+    while (nacc < b) {
+      acc |= (uint64_t)data[o++] << nacc;
+      nacc += 8;
+    }
+    codes[j] = (uint8_t)(acc & ((1ull << b) - 1ull));
+    acc >>= b;
+    nacc -= b;
+  }
+}
+
+/* `z as u8` in Rust: truncation toward zero, saturating at 0 and 255, NaN -> 0. */
+static uint8_t rs_f32_as_u8(float z) {
+  if (!(z > 0.0f)) return 0;
+  if (z >= 255.0f) return 255;
+  return (uint8_t)z;
+}
+
+/* io::packed_tensors (src/io.rs:244-264) with QLayer::pack (src/quant.rs:207-214): the byte
+ * contents of .qweight (d_out x row_bytes), .scales (f16 bits), .qzeros (u8) and .perm (i32);
+ * .gbits and .gsize are the inputs themselves. */
+void orc_pack_layer(size_t d_out, size_t n, size_t g, const uint8_t* gbits, size_t ng, const uint8_t* codes,
+                    const float* scales, const float* zeros, const uint32_t* perm, uint8_t* qweight, uint16_t* scales16,
+                    uint8_t* qzeros, int32_t* perm32) {
+  const size_t rb = orc_row_bytes(n, g, gbits);
+  memset(qweight, 0, d_out * rb);
+#pragma omp parallel for schedule(static)
+  for (size_t r = 0; r < d_out; ++r) orc_pack_row(codes + r * n, n, g, gbits, qweight + r * rb);
+  for (size_t i = 0; i < d_out * ng; ++i) {
+    scales16[i] = f32_to_f16_bits(scales[i]);
+    qzeros[i] = rs_f32_as_u8(zeros[i]);
+  }
+  memcpy(perm32, perm, n * 4); /* `p as i32`: same bits */
+}
+
+/* The `cdclq dequant` path for one layer: io::read_packed_layer (src/io.rs:270-293), i.e.
+ * QLayer::from_packed (src/quant.rs:219-236) and QLayer::dequantize (src/quant.rs:189-202), then
+ * io::f32_to_bytes (src/io.rs:50-57) into `dtype`. perm32[j] must be in 0..n. */
+void orc_dequantize_packed(size_t d_out, size_t n, size_t g, const uint8_t* gbits, size_t ng, const uint8_t* qweight,
+                           const uint16_t* scales16, const uint8_t* qzeros, const int32_t* perm32, int dtype,
+                           void* out) {
+  const size_t rb = orc_row_bytes(n, g, gbits);
+  uint8_t* codes = (uint8_t*)xcalloc(d_out * n + 1, 1);
+  float* sc = (float*)xcalloc(d_out * ng + 1, 4);
+  float* z = (float*)xcalloc(d_out * ng + 1, 4);
+  uint32_t* perm = (uint32_t*)xcalloc(n + 1, 4);
+  float* deq = (float*)xcalloc(d_out * n + 1, 4);
+#pragma omp parallel for schedule(static)
+  for (size_t r = 0; r < d_out; ++r) orc_unpack_row(qweight + r * rb, n, g, gbits, codes + r * n);
+  for (size_t i = 0; i < d_out * ng; ++i) {
+    sc[i] = f16_bits_to_f32(scales16[i]);
+    z[i] = (float)qzeros[i];
+  }
+  memcpy(perm, perm32, n * 4); /* `i32 as u32` */
+  orc_dequantize(d_out, n, g, perm, ng, codes, sc, z, deq);
+  orc_narrow(deq, d_out * n, dtype, out);
+  free(codes);
+  free(sc);
+  free(z);
+  free(perm);
+  free(deq);
 }

@@ -14,6 +14,10 @@
  *
  * Pinning status (what checks each function; see tests/test_oracle_*.py):
  *   round_f16          exhaustive over all 2^32 f32 patterns vs numpy float16 (IEEE RNE)
+ *   pack/unpack/dequant  the reference's own round trip (src/quant.rs:262-275, Rng(9) codes),
+ *                      an independent big-integer / numpy.packbits bit-stream formulation,
+ *                      numpy float32 dequantization; f16/bf16 narrowing vs numpy float16 and
+ *                      torch bfloat16 (non-NaN), NaN rule by construction only
  *   find_params/quant  closed form + brute force + src/quant.rs:279-286 properties
  *   gram_accumulate    f64 brute force, exact symmetry, chunk edges (T = 2047/2048/2049)
  *   cholesky/tri_inv   numpy/scipy Cholesky and inverse; src/linalg.rs:447-504 properties
@@ -119,6 +123,27 @@ void orc_rtn_layer(const float* w, size_t d_out, size_t n, const orc_config* cfg
 /* QLayer::dequantize (src/quant.rs:189-202) */
 void orc_dequantize(size_t d_out, size_t n, size_t g, const uint32_t* perm, size_t ng, const uint8_t* codes,
                     const float* scales, const float* zeros, float* out);
+
+/* Packed container cdclq-v1. dtype: 0 = F32, 1 = F16, 2 = BF16.
+ * half 2.4.1 conversions (IEEE RNE narrowing; NaN keeps sign and upper payload, quiet bit set). */
+uint16_t orc_f32_to_f16_bits(float x);
+float orc_f16_bits_to_f32(uint16_t h);
+uint16_t orc_f32_to_bf16_bits(float x);
+/* io::f32_to_bytes (src/io.rs:50-57) */
+void orc_narrow(const float* v, size_t count, int dtype, void* out);
+/* quant::row_bytes (src/quant.rs:102-104) */
+size_t orc_row_bytes(size_t n, size_t g, const uint8_t* gbits);
+/* quant::pack_row / unpack_row (src/quant.rs:113-151) */
+void orc_pack_row(const uint8_t* codes, size_t n, size_t g, const uint8_t* gbits, uint8_t* out);
+void orc_unpack_row(const uint8_t* data, size_t n, size_t g, const uint8_t* gbits, uint8_t* codes);
+/* io::packed_tensors + QLayer::pack (src/io.rs:244-264, src/quant.rs:207-214) */
+void orc_pack_layer(size_t d_out, size_t n, size_t g, const uint8_t* gbits, size_t ng, const uint8_t* codes,
+                    const float* scales, const float* zeros, const uint32_t* perm, uint8_t* qweight, uint16_t* scales16,
+                    uint8_t* qzeros, int32_t* perm32);
+/* io::read_packed_layer + QLayer::dequantize + f32_to_bytes (src/io.rs:270-293, src/quant.rs:189-236) */
+void orc_dequantize_packed(size_t d_out, size_t n, size_t g, const uint8_t* gbits, size_t ng, const uint8_t* qweight,
+                           const uint16_t* scales16, const uint8_t* qzeros, const int32_t* perm32, int dtype,
+                           void* out);
 
 /* rng.rs restatement (src/rng.rs:22-57). normal() uses the platform libm (glibc logf/sinf/cosf). */
 typedef struct orc_rng {
