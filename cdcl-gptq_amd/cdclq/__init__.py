@@ -60,6 +60,20 @@ class _Stats(C.Structure):
     ]
 
 
+class _BenchArgs(C.Structure):
+    """bench::BenchArgs (src/bench.rs:19-32) + the rayon thread count."""
+
+    _fields_ = [("rows", C.c_size_t), ("cols", C.c_size_t), ("tokens", C.c_size_t), ("test_tokens", C.c_size_t),
+                ("seed", C.c_uint64), ("asym_noise", C.c_float), ("nthreads", C.c_uint32), ("cfg", _Config)]
+
+
+class _BenchRow(C.Structure):
+    """One report row (src/bench.rs:124-128)."""
+
+    _fields_ = [("name", C.c_char * 96), ("loss", C.c_double), ("calib", C.c_double), ("test", C.c_double),
+                ("secs", C.c_double), ("bpw", C.c_double)]
+
+
 _lib = None
 
 
@@ -99,6 +113,13 @@ def lib() -> C.CDLL:
         "cdclq_dequantize_packed_device": ([vp, sz, sz, sz, vp, sz, vp, sz, vp, vp, vp, i32, vp], i32),
         "cdclq_dequantize_layer": ([vp, sz, sz, sz, sz, vp, vp, vp, vp, i32, vp], i32),
         "cdclq_dequantize_layer_device": ([vp, sz, sz, sz, sz, vp, vp, vp, vp, i32, vp], i32),
+        "cdclq_rtn_layer": ([vp, vp, sz, sz, cfgp, vp], i32),
+        "cdclq_rtn_layer_device": ([vp, vp, sz, sz, cfgp, vp], i32),
+        "cdclq_proxy_loss_device": ([vp, vp, vp, sz, sz, vp, C.POINTER(C.c_double)], i32),
+        "cdclq_rel_err": ([vp, vp, vp, vp, vp, sz, sz, sz, C.POINTER(C.c_double)], i32),
+        "cdclq_rel_err_device": ([vp, vp, vp, vp, vp, sz, sz, sz, C.POINTER(C.c_double)], i32),
+        "cdclq_bench_run": ([vp, C.POINTER(_BenchArgs), C.POINTER(_BenchRow), sz, C.POINTER(sz), C.c_char_p, sz,
+                             C.POINTER(sz)], i32),
         "cdclq_device_alloc": ([vp, sz, C.POINTER(vp)], i32),
         "cdclq_device_free": ([vp, vp], i32),
         "cdclq_memcpy_h2d": ([vp, vp, vp, sz], i32),
@@ -135,6 +156,8 @@ def exported_symbols() -> list[str]:
         "cdclq_ctx_set_timing", "cdclq_ctx_reset_timing", "cdclq_ctx_get_timing",
         "cdclq_row_bytes", "cdclq_pack_layer", "cdclq_pack_layer_device", "cdclq_dequantize_packed",
         "cdclq_dequantize_packed_device", "cdclq_dequantize_layer", "cdclq_dequantize_layer_device",
+        "cdclq_rtn_layer", "cdclq_rtn_layer_device", "cdclq_proxy_loss_device", "cdclq_rel_err",
+        "cdclq_rel_err_device", "cdclq_bench_run",
     ]
 
 
@@ -523,6 +546,52 @@ def dequantize_layer(ctx: Context, ql: QLayer, dtype="F32"):
                                            codes.ctypes.data, scales.ctypes.data, zeros.ctypes.data, perm.ctypes.data,
                                            dt, out.ctypes.data))
     return out
+
+
+# ---------------------------------------------------------------- evaluation / synthetic benchmark
+def rtn_layer(ctx: Context, w, cfg: Config) -> np.ndarray:
+    """engine::rtn_layer (src/engine.rs:822-838) on the GPU."""
+    w = _f32(w)
+    out = np.zeros_like(w)
+    c = cfg._c()
+    ctx.check(lib().cdclq_rtn_layer(ctx.ptr, w.ctypes.data, w.shape[0], w.shape[1], C.byref(c), out.ctypes.data))
+    return out
+
+
+def rel_err(ctx: Context, w, w_hat, x, x_t=None) -> float:
+    """bench::rel_err (src/bench.rs:106-121): ||W x - W_hat x~||^2 / ||W x||^2 (x: t x n tokens)."""
+    w, w_hat, x = _f32(w), _f32(w_hat), _f32(x)
+    xt = x if x_t is None else _f32(x_t)
+    out = C.c_double()
+    ctx.check(lib().cdclq_rel_err(ctx.ptr, w.ctypes.data, w_hat.ctypes.data, x.ctypes.data, xt.ctypes.data,
+                                  w.shape[0], w.shape[1], x.shape[0], C.byref(out)))
+    return out.value
+
+
+@dataclass
+class BenchRow:
+    name: str
+    loss: float
+    calib: float
+    test: float
+    secs: float
+    bpw: float
+
+
+def bench_run(ctx: Context, cfg: Config, rows: int = 1024, cols: int = 2048, tokens: int = 16384,
+              test_tokens: int = 4096, seed: int = 1, asym_noise: float = 0.0, nthreads: int = 1):
+    """bench::run (src/bench.rs:164-340) on the GPU: (markdown report, [BenchRow]). Defaults are the
+    `cdclq bench` CLI defaults (src/main.rs:171-190)."""
+    a = _BenchArgs(rows=rows, cols=cols, tokens=tokens, test_tokens=test_tokens, seed=seed, asym_noise=asym_noise,
+                   nthreads=nthreads, cfg=cfg._c())
+    cap_rows = 32
+    out = (_BenchRow * cap_rows)()
+    nrows, rlen = C.c_size_t(), C.c_size_t()
+    buf = C.create_string_buffer(1 << 16)
+    ctx.check(lib().cdclq_bench_run(ctx.ptr, C.byref(a), out, cap_rows, C.byref(nrows), buf, len(buf), C.byref(rlen)))
+    res = [BenchRow(out[i].name.decode(), out[i].loss, out[i].calib, out[i].test, out[i].secs, out[i].bpw)
+           for i in range(min(nrows.value, cap_rows))]
+    return buf.value.decode(), res
 
 
 def default_config() -> Config:

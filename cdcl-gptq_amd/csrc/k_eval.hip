@@ -1,0 +1,175 @@
+// Evaluation kernels of the synthetic benchmark harness: round-to-nearest quantization
+// (engine::rtn_layer), the held-out output error (bench::rel_err) reduction, and the element-wise
+// steps of the benchmark's input generator.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "cdclq_dev.h"
+#include "kernels.h"
+
+namespace cdclq {
+namespace {
+
+__device__ __forceinline__ int readlane_int(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+
+// engine::rtn_layer (src/engine.rs:822-838): one wave per (row, group). The group's grid is
+// quant::find_params (src/quant.rs:40-83) on the group's values -- min/max from 0, the all-zero
+// fallback, the optional 24-step clip search with each lane running one candidate's error sum in
+// column order, first minimum wins -- then every value is rounded onto that grid.
+__global__ __launch_bounds__(256) void k_rtn(long d_out, int n, int g, int ng, int bits, int mse,
+                                             const float* __restrict__ w, float* __restrict__ out) {
+  const long wid = ((long)blockIdx.x * 256 + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (wid >= d_out * ng) return;
+  const long r = wid / ng;
+  const int gi = (int)(wid - r * ng);
+  const int j0 = gi * g, j1 = min(j0 + g, n);
+  const float* src = w + r * n;
+  const float maxq = (float)((1u << bits) - 1u);
+  float lmin = INFINITY, lmax = -INFINITY;
+  for (int j = j0 + lane; j < j1; j += 64) {
+    lmin = rs_minf(lmin, src[j]);
+    lmax = rs_maxf(lmax, src[j]);
+  }
+  float xmin = rs_minf(0.0f, wave_min(lmin));
+  float xmax = rs_maxf(0.0f, wave_max(lmax));
+  if (xmin == 0.0f && xmax == 0.0f) {
+    xmin = -1.0f;
+    xmax = 1.0f;
+  }
+  float sc, zr;
+  grid_mk(xmin, xmax, maxq, &sc, &zr);
+  if (mse) {
+    const int cand = lane < 24 ? lane : 0;
+    const float p = 1.0f - 0.02f * (float)cand;
+    float cs, cz;
+    grid_mk(p * xmin, p * xmax, maxq, &cs, &cz);
+    float errs = 0.0f;
+    for (int j = j0; j < j1; ++j) {  // wave-uniform: every lane reads the same value
+      const float v = src[j];
+      float qq;
+      const float e = quant_dq(v, cs, cz, maxq, &qq) - v;
+      errs = errs + e * e;
+    }
+    float be = (lane < 24 && errs == errs) ? errs : INFINITY;
+    int bc = lane < 24 ? lane : (1 << 20);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float oe = __shfl_xor(be, o, 64);
+      const int oc = __shfl_xor(bc, o, 64);
+      if (oe < be || (oe == be && oc < bc)) {
+        be = oe;
+        bc = oc;
+      }
+    }
+    bc = readlane_int(bc, 0);
+    sc = readlane(cs, bc);
+    zr = readlane(cz, bc);
+  }
+  float* dst = out + r * n;
+  for (int j = j0 + lane; j < j1; j += 64) {
+    float qq;
+    dst[j] = quant_dq(src[j], sc, zr, maxq, &qq);
+  }
+}
+
+// bench::rel_err's sums (src/bench.rs:114-119): per-block f64 partials of (o1 - o2)^2 and o1^2.
+__global__ __launch_bounds__(256) void k_err_reduce(long count, const float* __restrict__ o1,
+                                                    const float* __restrict__ o2, double* __restrict__ partial) {
+  __shared__ double rn[256], rd[256];
+  double num = 0.0, den = 0.0;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < count; i += (long)gridDim.x * 256) {
+    const double d = (double)(o1[i] - o2[i]);
+    num += d * d;
+    den += (double)o1[i] * (double)o1[i];
+  }
+  rn[threadIdx.x] = num;
+  rd[threadIdx.x] = den;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) {
+      rn[threadIdx.x] += rn[threadIdx.x + o];
+      rd[threadIdx.x] += rd[threadIdx.x + o];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    partial[2 * blockIdx.x] = rn[0];
+    partial[2 * blockIdx.x + 1] = rd[0];
+  }
+}
+
+// ActGen::sample's per-token step (src/bench.rs:71-78): x = (x + noise) * scale[j] * massive[t],
+// with noise = 0.3 * normal drawn on the host in the reference's order.
+__global__ __launch_bounds__(256) void k_act_scale(long tokens, int n, const float* __restrict__ noise,
+                                                   const float* __restrict__ scale, const float* __restrict__ massive,
+                                                   float* __restrict__ x) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= tokens * n) return;
+  const long t = i / n;
+  const int j = (int)(i - t * n);
+  x[i] = (x[i] + noise[i]) * scale[j] * massive[t];
+}
+
+// Per-channel RMS of bench::run's asymmetric experiment (src/bench.rs:276-284): f32 sums in token
+// order, one thread per channel.
+__global__ __launch_bounds__(256) void k_channel_rms(long tokens, int n, const float* __restrict__ x,
+                                                     float* __restrict__ rms) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= n) return;
+  float s = 0.0f;
+  for (long t = 0; t < tokens; ++t) {
+    const float v = x[t * n + j];
+    s += v * v;
+  }
+  rms[j] = sqrtf(s / (float)tokens);
+}
+
+// xt = x + asym_noise * rms[j] * normal (src/bench.rs:286-292), normals drawn on the host in order.
+__global__ __launch_bounds__(256) void k_add_noise(long tokens, int n, float a, const float* __restrict__ rms,
+                                                   const float* __restrict__ nrm, const float* __restrict__ x,
+                                                   float* __restrict__ xt) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= tokens * n) return;
+  const int j = (int)(i % n);
+  xt[i] = x[i] + a * rms[j] * nrm[i];
+}
+
+unsigned blocks_for(long count) { return (unsigned)((count + 255) / 256); }
+
+}  // namespace
+
+hipError_t rtn_rows(hipStream_t st, long d_out, int n, int g, int bits, int mse, const float* w, float* out) {
+  const int ng = (n + g - 1) / g;
+  const long waves = d_out * ng;
+  if (waves <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_rtn, dim3(blocks_for(waves * 64)), dim3(256), 0, st, d_out, n, g, ng, bits, mse, w, out);
+  return hipGetLastError();
+}
+
+hipError_t err_reduce(hipStream_t st, size_t count, const float* o1, const float* o2, double* partial, int nblocks) {
+  hipLaunchKernelGGL(k_err_reduce, dim3(nblocks), dim3(256), 0, st, (long)count, o1, o2, partial);
+  return hipGetLastError();
+}
+
+hipError_t act_scale(hipStream_t st, long tokens, int n, const float* noise, const float* scale, const float* massive,
+                     float* x) {
+  if (tokens * n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_act_scale, dim3(blocks_for(tokens * n)), dim3(256), 0, st, tokens, n, noise, scale, massive, x);
+  return hipGetLastError();
+}
+
+hipError_t channel_rms(hipStream_t st, long tokens, int n, const float* x, float* rms) {
+  hipLaunchKernelGGL(k_channel_rms, dim3(blocks_for(n)), dim3(256), 0, st, tokens, n, x, rms);
+  return hipGetLastError();
+}
+
+hipError_t add_noise(hipStream_t st, long tokens, int n, float a, const float* rms, const float* nrm, const float* x,
+                     float* xt) {
+  if (tokens * n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_add_noise, dim3(blocks_for(tokens * n)), dim3(256), 0, st, tokens, n, a, rms, nrm, x, xt);
+  return hipGetLastError();
+}
+
+}  // namespace cdclq

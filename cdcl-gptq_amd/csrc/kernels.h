@@ -108,6 +108,20 @@ hipError_t dequant_rows(hipStream_t st, bool packed, int dtype, long d_out, int 
                         const uint8_t* src, const uint32_t* cdesc, const int* cgrp, const void* scales,
                         const void* zeros, void* out);
 
+// ---- k_eval.hip: benchmark-harness evaluation
+// out (d_out x n) = engine::rtn_layer of w with group g
+hipError_t rtn_rows(hipStream_t st, long d_out, int n, int g, int bits, int mse, const float* w, float* out);
+// partial[2b] = sum (o1 - o2)^2, partial[2b+1] = sum o1^2 over block b's share (f64)
+hipError_t err_reduce(hipStream_t st, size_t count, const float* o1, const float* o2, double* partial, int nblocks);
+// x = (x + noise) * scale[j] * massive[t]
+hipError_t act_scale(hipStream_t st, long tokens, int n, const float* noise, const float* scale, const float* massive,
+                     float* x);
+// rms[j] = sqrt(sum_t x[t][j]^2 / tokens), f32 sums in token order
+hipError_t channel_rms(hipStream_t st, long tokens, int n, const float* x, float* rms);
+// xt = x + a * rms[j] * nrm
+hipError_t add_noise(hipStream_t st, long tokens, int n, float a, const float* rms, const float* nrm, const float* x,
+                     float* xt);
+
 hipError_t synth_normal(hipStream_t st, uint64_t seed, uint64_t offset, size_t count, float sigma, float* out);
 hipError_t synth_tokens(hipStream_t st, uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale,
                         float* x);

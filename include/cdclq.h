@@ -185,6 +185,53 @@ int cdclq_dequantize_layer_device(cdclq_ctx* ctx, size_t d_out, size_t d_in, siz
                                   const uint8_t* codes, const float* scales, const float* zeros, const uint32_t* perm,
                                   int dtype, void* out);
 
+/* ---- Evaluation and the synthetic benchmark (src/engine.rs:808-838, src/bench.rs) ---- */
+/* engine::rtn_layer (src/engine.rs:822-838): round-to-nearest on each group's find_params grid,
+ * no compensation, original column order; out is d_out x n f32 (dequantized values). Uses
+ * cfg->bits, cfg->group and cfg->mse_grid. */
+int cdclq_rtn_layer(cdclq_ctx* ctx, const float* w, size_t d_out, size_t n, const cdclq_config* cfg, float* out);
+int cdclq_rtn_layer_device(cdclq_ctx* ctx, const float* w, size_t d_out, size_t n, const cdclq_config* cfg,
+                           float* out);
+/* engine::proxy_loss (src/engine.rs:808-815) on device memory. */
+int cdclq_proxy_loss_device(cdclq_ctx* ctx, const float* w_t, const float* w_hat, size_t rows, size_t n,
+                            const float* h, double* out);
+/* bench::rel_err (src/bench.rs:106-121): ||W x - W_hat x~||^2 / ||W x||^2 over t tokens; x and x_t
+ * are t x n token-major (pass x for x_t to measure the weight error alone). The f32 products are the
+ * reference's chains; the two f64 sums run in parallel (not in element order). */
+int cdclq_rel_err(cdclq_ctx* ctx, const float* w, const float* w_hat, const float* x, const float* x_t, size_t rows,
+                  size_t n, size_t t, double* out);
+int cdclq_rel_err_device(cdclq_ctx* ctx, const float* w, const float* w_hat, const float* x, const float* x_t,
+                         size_t rows, size_t n, size_t t, double* out);
+
+/* bench::BenchArgs (src/bench.rs:19-32); nthreads stands in for rayon::current_num_threads() (the
+ * automatic row chunk and the report header). md / dump outputs are the caller's (the report text
+ * is returned). */
+typedef struct cdclq_bench_args {
+  size_t rows;
+  size_t cols;
+  size_t tokens;
+  size_t test_tokens;
+  uint64_t seed;
+  float asym_noise;
+  uint32_t nthreads;
+  cdclq_config cfg;
+} cdclq_bench_args;
+/* One row of the report (src/bench.rs:124-128). */
+typedef struct cdclq_bench_row {
+  char name[96];
+  double loss;  /* proxy loss after the repair (0: not reported) */
+  double calib; /* relative output error on the first min(tokens, 4096) calibration tokens */
+  double test;  /* relative output error on the held-out tokens */
+  double secs;
+  double bpw;
+} cdclq_bench_row;
+/* bench::run (src/bench.rs:164-340) on the GPU: the same generator stream, method variants and
+ * markdown report (times are this GPU's). rows_out receives up to max_rows rows in report order
+ * (equal-bits table, then the skeleton rows, then the asymmetric rows); *nrows the total. report
+ * (may be NULL) receives the markdown, truncated to report_cap - 1 bytes; *report_len its length. */
+int cdclq_bench_run(cdclq_ctx* ctx, const cdclq_bench_args* args, cdclq_bench_row* rows_out, size_t max_rows,
+                    size_t* nrows, char* report, size_t report_cap, size_t* report_len);
+
 /* ---- Device memory staging for callers without their own GPU runtime binding. ---- */
 int cdclq_device_alloc(cdclq_ctx* ctx, size_t bytes, void** ptr);
 int cdclq_device_free(cdclq_ctx* ctx, void* ptr);

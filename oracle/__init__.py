@@ -123,6 +123,10 @@ def lib():
         L.orc_unpack_row.argtypes = [u8p, sz, sz, u8p, u8p]
         L.orc_pack_layer.argtypes = [sz, sz, sz, u8p, sz, u8p, f32p, f32p, u32p, u8p, u16p, u8p, i32p]
         L.orc_dequantize_packed.argtypes = [sz, sz, sz, u8p, sz, u8p, u16p, u8p, i32p, C.c_int, C.c_void_p]
+        L.orc_bench_inputs.argtypes = [C.c_uint64, sz, sz, sz, sz, C.c_float, f32p, f32p, f32p, C.c_void_p,
+                                       C.c_void_p]
+        L.orc_rel_err.argtypes = [f32p, f32p, f32p, f32p, sz, sz, sz]
+        L.orc_rel_err.restype = C.c_double
         L.orc_rng_new.argtypes = [C.c_void_p, C.c_uint64]
         L.orc_rng_next_u64.argtypes = [C.c_void_p]
         L.orc_rng_next_u64.restype = C.c_uint64
@@ -392,6 +396,27 @@ def narrow(v, dtype: str) -> np.ndarray:
     out = np.zeros(v.shape, _NP_OUT[dt])
     lib().orc_narrow(v.ravel(), v.size, dt, out.ctypes.data)
     return out
+
+
+# ---------------------------------------------------------------- synthetic benchmark (src/bench.rs)
+def bench_inputs(seed: int, rows: int, n: int, tokens: int, test_tokens: int, asym_noise: float = 0.0):
+    """(w, x, xte, xt, xte_t) of bench::run (src/bench.rs:41-97, :275-295); xt/xte_t None without noise."""
+    w = np.zeros((rows, n), np.float32)
+    x = np.zeros((tokens, n), np.float32)
+    xte = np.zeros((test_tokens, n), np.float32)
+    xt = xte_t = None
+    if asym_noise > 0:
+        xt = np.zeros((tokens, n), np.float32)
+        xte_t = np.zeros((test_tokens, n), np.float32)
+    lib().orc_bench_inputs(seed, rows, n, tokens, test_tokens, asym_noise, w, x, xte,
+                           xt.ctypes.data if xt is not None else None, xte_t.ctypes.data if xte_t is not None else None)
+    return w, x, xte, xt, xte_t
+
+
+def rel_err(w, wq, x, xt, rows: int, n: int, t: int) -> float:
+    """bench::rel_err (src/bench.rs:106-121)."""
+    f = lambda a: np.ascontiguousarray(a, np.float32)
+    return lib().orc_rel_err(f(w), f(wq), f(x), f(xt), rows, n, t)
 
 
 class Rng:

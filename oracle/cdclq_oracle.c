@@ -1310,3 +1310,82 @@ void orc_dequantize_packed(size_t d_out, size_t n, size_t g, const uint8_t* gbit
   free(perm);
   free(deq);
 }
+
+/* ------------------------------------------------------------------ synthetic benchmark (src/bench.rs) */
+/* ActGen::new + gen_weights + ActGen::sample x2 (src/bench.rs:41-97) and, when asym_noise > 0, the
+ * noisy copies of bench::run (src/bench.rs:275-295), all from one Rng(seed) stream in the
+ * reference's draw order. x: tokens x n, xte: test_tokens x n, w: rows x n; xt / xte_t may be NULL
+ * when asym_noise == 0. */
+static void bench_sample(orc_rng* rng, size_t n, size_t rank, const float* a, const float* scale, size_t tokens,
+                         float* x) {
+  float* z = (float*)xcalloc(tokens * rank + 1, sizeof(float));
+  for (size_t i = 0; i < tokens * rank; ++i) z[i] = orc_rng_normal(rng);
+  orc_sgemm(tokens, rank, n, 1.0f, z, (ptrdiff_t)rank, 1, a, (ptrdiff_t)n, 1, 0.0f, x, (ptrdiff_t)n, 1);
+  free(z);
+  for (size_t t = 0; t < tokens; ++t) {
+    float massive = orc_rng_uniform(rng) < 0.02f ? 4.0f : 1.0f;
+    float* row = x + t * n;
+    for (size_t j = 0; j < n; ++j) row[j] = (row[j] + 0.3f * orc_rng_normal(rng)) * scale[j] * massive;
+  }
+}
+
+void orc_bench_inputs(uint64_t seed, size_t rows, size_t n, size_t tokens, size_t test_tokens, float asym_noise,
+                      float* w, float* x, float* xte, float* xt, float* xte_t) {
+  orc_rng rng;
+  orc_rng_new(&rng, seed);
+  /* ActGen::new (src/bench.rs:49-61) */
+  size_t rank = n / 8 > 8 ? n / 8 : 8;
+  float* a = (float*)xcalloc(rank * n + 1, sizeof(float));
+  float rs = sqrtf((float)rank);
+  for (size_t i = 0; i < rank * n; ++i) a[i] = orc_rng_normal(&rng) / rs;
+  float* scale = (float*)xcalloc(n + 1, sizeof(float));
+  for (size_t j = 0; j < n; ++j) scale[j] = expf(0.6f * orc_rng_normal(&rng));
+  for (size_t j = 0; j < n; ++j)
+    if (orc_rng_uniform(&rng) < 0.005f) scale[j] *= 20.0f + 40.0f * orc_rng_uniform(&rng);
+  /* gen_weights (src/bench.rs:82-97) */
+  for (size_t r = 0; r < rows; ++r) {
+    float sigma = 0.02f * expf(0.3f * orc_rng_normal(&rng));
+    for (size_t j = 0; j < n; ++j) {
+      float v = orc_rng_normal(&rng) * sigma;
+      if (orc_rng_uniform(&rng) < 0.001f) v *= 8.0f;
+      w[r * n + j] = v;
+    }
+  }
+  bench_sample(&rng, n, rank, a, scale, tokens, x);
+  bench_sample(&rng, n, rank, a, scale, test_tokens, xte);
+  if (asym_noise > 0.0f && xt && xte_t) {
+    /* per-channel RMS in f32, token order (src/bench.rs:276-284) */
+    float* rms = (float*)xcalloc(n + 1, sizeof(float));
+    for (size_t t = 0; t < tokens; ++t)
+      for (size_t j = 0; j < n; ++j) rms[j] += x[t * n + j] * x[t * n + j];
+    for (size_t j = 0; j < n; ++j) rms[j] = sqrtf(rms[j] / (float)tokens);
+    memcpy(xt, x, tokens * n * sizeof(float));
+    for (size_t i = 0; i < tokens; ++i)
+      for (size_t j = 0; j < n; ++j) xt[i * n + j] += asym_noise * rms[j] * orc_rng_normal(&rng);
+    memcpy(xte_t, xte, test_tokens * n * sizeof(float));
+    for (size_t i = 0; i < test_tokens; ++i)
+      for (size_t j = 0; j < n; ++j) xte_t[i * n + j] += asym_noise * rms[j] * orc_rng_normal(&rng);
+    free(rms);
+  }
+  free(a);
+  free(scale);
+}
+
+/* bench::rel_err (src/bench.rs:106-121): ||W x - W_hat x~||^2 / ||W x||^2 over t tokens, f32 GEMMs,
+ * f64 sums in element order. */
+double orc_rel_err(const float* w, const float* wq, const float* x, const float* xt, size_t rows, size_t n,
+                   size_t t) {
+  float* o1 = (float*)xcalloc(rows * t + 1, sizeof(float));
+  float* o2 = (float*)xcalloc(rows * t + 1, sizeof(float));
+  orc_sgemm(rows, n, t, 1.0f, w, (ptrdiff_t)n, 1, x, 1, (ptrdiff_t)n, 0.0f, o1, (ptrdiff_t)t, 1);
+  orc_sgemm(rows, n, t, 1.0f, wq, (ptrdiff_t)n, 1, xt, 1, (ptrdiff_t)n, 0.0f, o2, (ptrdiff_t)t, 1);
+  double num = 0.0, den = 0.0;
+  for (size_t i = 0; i < rows * t; ++i) {
+    double d = (double)(o1[i] - o2[i]);
+    num += d * d;
+    den += (double)o1[i] * (double)o1[i];
+  }
+  free(o1);
+  free(o2);
+  return num / den;
+}

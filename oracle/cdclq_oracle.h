@@ -145,6 +145,14 @@ void orc_dequantize_packed(size_t d_out, size_t n, size_t g, const uint8_t* gbit
                            const uint16_t* scales16, const uint8_t* qzeros, const int32_t* perm32, int dtype,
                            void* out);
 
+/* Synthetic benchmark inputs (src/bench.rs:41-97, :275-295) from Rng(seed) in the reference's draw
+ * order; xt / xte_t (asymmetric-noise copies) may be NULL when asym_noise == 0. */
+void orc_bench_inputs(uint64_t seed, size_t rows, size_t n, size_t tokens, size_t test_tokens, float asym_noise,
+                      float* w, float* x, float* xte, float* xt, float* xte_t);
+/* bench::rel_err (src/bench.rs:106-121) */
+double orc_rel_err(const float* w, const float* wq, const float* x, const float* xt, size_t rows, size_t n,
+                   size_t t);
+
 /* rng.rs restatement (src/rng.rs:22-57). normal() uses the platform libm (glibc logf/sinf/cosf). */
 typedef struct orc_rng {
   uint64_t s;
