@@ -74,6 +74,16 @@ class _BenchRow(C.Structure):
                 ("secs", C.c_double), ("bpw", C.c_double)]
 
 
+class _QuantOpts(C.Structure):
+    """pipeline::QuantOpts (src/pipeline.rs:24-40) + thread count and verbosity."""
+
+    _fields_ = [("weights", C.POINTER(C.c_char_p)), ("n_weights", C.c_size_t), ("hessians", C.POINTER(C.c_char_p)),
+                ("n_hessians", C.c_size_t), ("out_dir", C.c_char_p), ("cfg", _Config),
+                ("only", C.POINTER(C.c_char_p)), ("n_only", C.c_size_t), ("skip", C.POINTER(C.c_char_p)),
+                ("n_skip", C.c_size_t), ("emit_packed", C.c_int32), ("emit_dequant", C.c_int32),
+                ("nthreads", C.c_uint32), ("verbose", C.c_int32)]
+
+
 _lib = None
 
 
@@ -120,6 +130,8 @@ def lib() -> C.CDLL:
         "cdclq_rel_err_device": ([vp, vp, vp, vp, vp, sz, sz, sz, C.POINTER(C.c_double)], i32),
         "cdclq_bench_run": ([vp, C.POINTER(_BenchArgs), C.POINTER(_BenchRow), sz, C.POINTER(sz), C.c_char_p, sz,
                              C.POINTER(sz)], i32),
+        "cdclq_quantize_model": ([vp, C.POINTER(_QuantOpts), C.c_char_p, sz, C.POINTER(sz)], i32),
+        "cdclq_dequantize_model": ([vp, C.c_char_p, C.c_char_p, i32, C.POINTER(sz)], i32),
         "cdclq_device_alloc": ([vp, sz, C.POINTER(vp)], i32),
         "cdclq_device_free": ([vp, vp], i32),
         "cdclq_memcpy_h2d": ([vp, vp, vp, sz], i32),
@@ -157,7 +169,7 @@ def exported_symbols() -> list[str]:
         "cdclq_row_bytes", "cdclq_pack_layer", "cdclq_pack_layer_device", "cdclq_dequantize_packed",
         "cdclq_dequantize_packed_device", "cdclq_dequantize_layer", "cdclq_dequantize_layer_device",
         "cdclq_rtn_layer", "cdclq_rtn_layer_device", "cdclq_proxy_loss_device", "cdclq_rel_err",
-        "cdclq_rel_err_device", "cdclq_bench_run",
+        "cdclq_rel_err_device", "cdclq_bench_run", "cdclq_quantize_model", "cdclq_dequantize_model",
     ]
 
 
@@ -592,6 +604,42 @@ def bench_run(ctx: Context, cfg: Config, rows: int = 1024, cols: int = 2048, tok
     res = [BenchRow(out[i].name.decode(), out[i].loss, out[i].calib, out[i].test, out[i].secs, out[i].bpw)
            for i in range(min(nrows.value, cap_rows))]
     return buf.value.decode(), res
+
+
+# ---------------------------------------------------------------- model pipeline
+def _cstrs(items):
+    items = [str(x).encode() for x in items]
+    return (C.c_char_p * max(len(items), 1))(*items), len(items)
+
+
+def quantize_model(ctx: Context, weights, hessians, out_dir, cfg: Config, only=(), skip=(), emit_packed: bool = True,
+                   emit_dequant: bool = True, nthreads: int = 24, verbose: bool = False) -> dict:
+    """pipeline::quantize_model (src/pipeline.rs:79-227) on the GPU; returns the parsed report.json."""
+    import json
+    w, nw = _cstrs(weights)
+    h, nh = _cstrs(hessians)
+    on, non = _cstrs(only)
+    sk, nsk = _cstrs(skip)
+    o = _QuantOpts(weights=w, n_weights=nw, hessians=h, n_hessians=nh, out_dir=str(out_dir).encode(), cfg=cfg._c(),
+                   only=on, n_only=non, skip=sk, n_skip=nsk, emit_packed=int(emit_packed),
+                   emit_dequant=int(emit_dequant), nthreads=nthreads, verbose=int(verbose))
+    need = C.c_size_t()
+    buf = C.create_string_buffer(1 << 20)
+    ctx.check(lib().cdclq_quantize_model(ctx.ptr, C.byref(o), buf, len(buf), C.byref(need)))
+    if need.value >= len(buf):
+        with open(os.path.join(str(out_dir), "report.json")) as f:
+            return json.load(f)
+    return json.loads(buf.value.decode())
+
+
+def dequantize_model(ctx: Context, input_path, output_path, dtype=None) -> int:
+    """pipeline::dequantize_packed (src/pipeline.rs:239-275): expands a packed shard; returns the
+    number of layers. dtype None = the header's orig_dtype (else F16)."""
+    n = C.c_size_t()
+    dt = -1 if dtype is None else _dtype_code(dtype)
+    ctx.check(lib().cdclq_dequantize_model(ctx.ptr, str(input_path).encode(), str(output_path).encode(), dt,
+                                           C.byref(n)))
+    return n.value
 
 
 def default_config() -> Config:

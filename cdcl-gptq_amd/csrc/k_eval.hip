@@ -1,10 +1,12 @@
 // Evaluation kernels of the synthetic benchmark harness: round-to-nearest quantization
 // (engine::rtn_layer), the held-out output error (bench::rel_err) reduction, and the element-wise
-// steps of the benchmark's input generator.
+// steps of the benchmark's input generator; and the checkpoint-tensor decode and non-finite scan of
+// the model pipeline.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 
+#include "cdclq.h"
 #include "cdclq_dev.h"
 #include "kernels.h"
 
@@ -169,6 +171,70 @@ hipError_t add_noise(hipStream_t st, long tokens, int n, float a, const float* r
                      float* xt) {
   if (tokens * n <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_add_noise, dim3(blocks_for(tokens * n)), dim3(256), 0, st, tokens, n, a, rms, nrm, x, xt);
+  return hipGetLastError();
+}
+
+}  // namespace cdclq
+
+// ---- checkpoint tensors (src/io.rs:37-45, :205-212)
+namespace cdclq {
+namespace {
+
+// io::tensor_to_f32: little-endian F32 / F16 / BF16 widened to f32 (exact; NaN payloads keep their
+// upper bits with the quiet bit set, as half's to_f32).
+__global__ __launch_bounds__(256) void k_decode(long count, int dtype, const uint8_t* __restrict__ src,
+                                                float* __restrict__ out) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= count) return;
+  if (dtype == CDCLQ_DTYPE_F32) {
+    out[i] = reinterpret_cast<const float*>(src)[i];
+  } else {
+    const uint32_t h = reinterpret_cast<const uint16_t*>(src)[i];
+    uint32_t u;
+    if (dtype == CDCLQ_DTYPE_BF16) {
+      u = ((h & 0x7fffu) > 0x7f80u ? (h | 0x0040u) : h) << 16;  // NaN quieted as half::bf16::to_f32
+    } else {
+      const uint32_t sign = (h & 0x8000u) << 16, exp = (h >> 10) & 0x1fu;
+      uint32_t man = h & 0x3ffu;
+      if (exp == 0x1fu) {
+        u = sign | 0x7f800000u | (man << 13) | (man ? 0x400000u : 0u);
+      } else if (exp == 0) {
+        if (man == 0) {
+          u = sign;
+        } else {
+          const int lz = __clz((int)man) - 21;
+          man = (man << lz) & 0x3ffu;
+          u = sign | ((uint32_t)(113 - lz) << 23) | (man << 13);
+        }
+      } else {
+        u = sign | ((exp + 112u) << 23) | (man << 13);
+      }
+    }
+    out[i] = __uint_as_float(u);
+  }
+}
+
+// Index of the first non-finite element (io.rs first_non_finite): atomicMin over the indices.
+__global__ __launch_bounds__(256) void k_first_non_finite(long count, const float* __restrict__ x,
+                                                          unsigned long long* __restrict__ first) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= count) return;
+  const uint32_t u = __float_as_uint(x[i]);
+  if ((u & 0x7f800000u) == 0x7f800000u) atomicMin(first, (unsigned long long)i);
+}
+
+}  // namespace
+
+hipError_t decode_to_f32(hipStream_t st, long count, int dtype, const void* src, float* out) {
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_decode, dim3(blocks_for(count)), dim3(256), 0, st, count, dtype,
+                     static_cast<const uint8_t*>(src), out);
+  return hipGetLastError();
+}
+
+hipError_t first_non_finite(hipStream_t st, long count, const float* x, unsigned long long* first) {
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_first_non_finite, dim3(blocks_for(count)), dim3(256), 0, st, count, x, first);
   return hipGetLastError();
 }
 

@@ -122,6 +122,11 @@ hipError_t channel_rms(hipStream_t st, long tokens, int n, const float* x, float
 hipError_t add_noise(hipStream_t st, long tokens, int n, float a, const float* rms, const float* nrm, const float* x,
                      float* xt);
 
+// io::tensor_to_f32 (dtype: CDCLQ_DTYPE_*) and io's first non-finite element (*first must start at
+// a value >= count; it ends at the smallest non-finite index, if any)
+hipError_t decode_to_f32(hipStream_t st, long count, int dtype, const void* src, float* out);
+hipError_t first_non_finite(hipStream_t st, long count, const float* x, unsigned long long* first);
+
 hipError_t synth_normal(hipStream_t st, uint64_t seed, uint64_t offset, size_t count, float sigma, float* out);
 hipError_t synth_tokens(hipStream_t st, uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale,
                         float* x);

@@ -232,6 +232,41 @@ typedef struct cdclq_bench_row {
 int cdclq_bench_run(cdclq_ctx* ctx, const cdclq_bench_args* args, cdclq_bench_row* rows_out, size_t max_rows,
                     size_t* nrows, char* report, size_t report_cap, size_t* report_len);
 
+/* ---- Model pipeline (src/pipeline.rs) ---- */
+/* pipeline::QuantOpts (src/pipeline.rs:24-40): shard and Hessian safetensors paths, output
+ * directory, config, --only / --skip substrings, the two outputs; nthreads stands in for
+ * rayon::current_num_threads() (automatic row chunks); verbose prints the reference's per-layer
+ * progress line on stderr. */
+typedef struct cdclq_quant_opts {
+  const char* const* weights;
+  size_t n_weights;
+  const char* const* hessians;
+  size_t n_hessians;
+  const char* out_dir;
+  cdclq_config cfg;
+  const char* const* only;
+  size_t n_only;
+  const char* const* skip;
+  size_t n_skip;
+  int32_t emit_packed;
+  int32_t emit_dequant;
+  uint32_t nthreads;
+  int32_t verbose;
+} cdclq_quant_opts;
+/* pipeline::quantize_model (src/pipeline.rs:79-227): every 2-D `*.weight` tensor that passes the
+ * filters and has a Hessian (directly or through the store's aliases) is quantized on the GPU, jobs
+ * ordered by (Hessian owner, layer) so q/k/v and gate/up share one factorisation; everything else is
+ * passed through. Writes <out_dir>/dequant/<shard> (checkpoint dtypes), <out_dir>/packed/<shard>
+ * (cdclq-v1; metadata quantization, orig_dtype, bits) and <out_dir>/report.json, whose text is also
+ * returned (truncated to report_cap - 1; *report_len = full length). Error texts follow
+ * src/io.rs / src/pipeline.rs (missing Hessian, non-square or non-finite H, width mismatch). */
+int cdclq_quantize_model(cdclq_ctx* ctx, const cdclq_quant_opts* opts, char* report_json, size_t report_cap,
+                         size_t* report_len);
+/* pipeline::dequantize_packed (src/pipeline.rs:239-275): every `X.qweight` layer of a packed shard
+ * becomes `X.weight` (original column order) in `dtype` (cdclq_dtype; -1 = the header's orig_dtype,
+ * else F16); other tensors pass through. *nlayers = layers expanded. */
+int cdclq_dequantize_model(cdclq_ctx* ctx, const char* input, const char* output, int dtype, size_t* nlayers);
+
 /* ---- Device memory staging for callers without their own GPU runtime binding. ---- */
 int cdclq_device_alloc(cdclq_ctx* ctx, size_t bytes, void** ptr);
 int cdclq_device_free(cdclq_ctx* ctx, void* ptr);
