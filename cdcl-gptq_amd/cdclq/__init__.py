@@ -132,6 +132,8 @@ def lib() -> C.CDLL:
                              C.POINTER(sz)], i32),
         "cdclq_quantize_model": ([vp, C.POINTER(_QuantOpts), C.c_char_p, sz, C.POINTER(sz)], i32),
         "cdclq_dequantize_model": ([vp, C.c_char_p, C.c_char_p, i32, C.POINTER(sz)], i32),
+        "cdclq_hessian_accumulate_device": ([vp, vp, vp, vp, sz, sz, vp], i32),
+        "cdclq_hessian_finalize_device": ([vp, vp, sz, u64, vp], i32),
         "cdclq_device_alloc": ([vp, sz, C.POINTER(vp)], i32),
         "cdclq_device_free": ([vp, vp], i32),
         "cdclq_memcpy_h2d": ([vp, vp, vp, sz], i32),
@@ -170,6 +172,7 @@ def exported_symbols() -> list[str]:
         "cdclq_dequantize_packed_device", "cdclq_dequantize_layer", "cdclq_dequantize_layer_device",
         "cdclq_rtn_layer", "cdclq_rtn_layer_device", "cdclq_proxy_loss_device", "cdclq_rel_err",
         "cdclq_rel_err_device", "cdclq_bench_run", "cdclq_quantize_model", "cdclq_dequantize_model",
+        "cdclq_hessian_accumulate_device", "cdclq_hessian_finalize_device",
     ]
 
 

@@ -776,6 +776,37 @@ int cdclq_gram_accumulate(cdclq_ctx* ctx, const float* x, const float* y, size_t
   return CDCLQ_OK;
 }
 
+int cdclq_hessian_accumulate_device(cdclq_ctx* ctx, const float* x, const float* y, const float* token_w, size_t t,
+                                    size_t n, double* acc) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  if (!x || !y || !acc) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+  if (t == 0 || n == 0) return CDCLQ_OK;
+  if (!token_w) return gram_device(ctx, x, y, t, n, acc);
+  // weighted tokens: both operands scaled by sqrt(w_t), then the plain accumulation
+  HIPCK(hipSetDevice(ctx->device));
+  CK(ensure(ctx, ctx->x_in, t * n * 4));
+  HIPCK(token_scale(ctx->st, (long)t, (int)n, x, token_w, P<float>(ctx->x_in)));
+  const float* ys = P<float>(ctx->x_in);
+  if (y != x) {
+    CK(ensure(ctx, ctx->y_in, t * n * 4));
+    HIPCK(token_scale(ctx->st, (long)t, (int)n, y, token_w, P<float>(ctx->y_in)));
+    ys = P<float>(ctx->y_in);
+  }
+  return gram_device(ctx, P<float>(ctx->x_in), ys, t, n, acc);
+}
+
+int cdclq_hessian_finalize_device(cdclq_ctx* ctx, const double* acc, size_t n, uint64_t tokens, float* h) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  if (!acc || !h) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+  if (tokens == 0) return fail(ctx, CDCLQ_INVALID_ARG, "no calibration token was accumulated");
+  HIPCK(hipSetDevice(ctx->device));
+  HIPCK(normalize_acc(ctx->st, (long)(n * n), acc, (double)tokens, h));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
 int cdclq_upper_chol_of_inverse_device(cdclq_ctx* ctx, const double* h, size_t n, float* u) {
   if (!ctx) return CDCLQ_INVALID_ARG;
   ctx->err.clear();

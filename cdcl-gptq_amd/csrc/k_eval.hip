@@ -239,3 +239,38 @@ hipError_t first_non_finite(hipStream_t st, long count, const float* x, unsigned
 }
 
 }  // namespace cdclq
+
+// ---- calibration capture (scripts/capture_hessians.py:233-245, :266)
+namespace cdclq {
+namespace {
+
+// xf = x * sqrt(w_t) per token (f32, as `xf * state["w"].sqrt().unsqueeze(1)`)
+__global__ __launch_bounds__(256) void k_token_scale(long t, int n, const float* __restrict__ x,
+                                                     const float* __restrict__ w, float* __restrict__ out) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= t * n) return;
+  out[i] = x[i] * sqrtf(w[i / n]);
+}
+
+// h = (f32)(acc / count): the 1/N normalisation, rounded once from f64
+__global__ __launch_bounds__(256) void k_normalize(long count, const double* __restrict__ acc, double tokens,
+                                                   float* __restrict__ h) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i < count) h[i] = (float)(acc[i] / tokens);
+}
+
+}  // namespace
+
+hipError_t token_scale(hipStream_t st, long t, int n, const float* x, const float* w, float* out) {
+  if (t * n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_token_scale, dim3((unsigned)((t * n + 255) / 256)), dim3(256), 0, st, t, n, x, w, out);
+  return hipGetLastError();
+}
+
+hipError_t normalize_acc(hipStream_t st, long count, const double* acc, double tokens, float* h) {
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_normalize, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st, count, acc, tokens, h);
+  return hipGetLastError();
+}
+
+}  // namespace cdclq

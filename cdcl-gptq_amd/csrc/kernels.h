@@ -127,6 +127,10 @@ hipError_t add_noise(hipStream_t st, long tokens, int n, float a, const float* r
 hipError_t decode_to_f32(hipStream_t st, long count, int dtype, const void* src, float* out);
 hipError_t first_non_finite(hipStream_t st, long count, const float* x, unsigned long long* first);
 
+// out = x * sqrt(w[t]) per token row; h = (float)(acc / tokens)
+hipError_t token_scale(hipStream_t st, long t, int n, const float* x, const float* w, float* out);
+hipError_t normalize_acc(hipStream_t st, long count, const double* acc, double tokens, float* h);
+
 hipError_t synth_normal(hipStream_t st, uint64_t seed, uint64_t offset, size_t count, float sigma, float* out);
 hipError_t synth_tokens(hipStream_t st, uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale,
                         float* x);

@@ -128,6 +128,17 @@ int cdclq_gram_accumulate_device(cdclq_ctx* ctx, const float* x, const float* y,
 int cdclq_gram_accumulate_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const float* const* ys,
                                        const size_t* ts, const size_t* ns, double* const* hs);
 
+/* Calibration capture (scripts/capture_hessians.py:233-245, :266), device memory: acc (n x n f64)
+ * += sum_t w_t x_t y_t^T over t tokens (token-major t x n f32). The token weight is applied as the
+ * reference does, x_t * sqrt(w_t) in f32 on both operands; token_w NULL = all 1. y == x gives the
+ * Hessian; y = the quantized model's layer input gives the cross-covariance M of the asymmetric
+ * target (src/engine.rs:690-699), which the reference's capture does not produce. Each call's
+ * tokens are summed exactly as cdclq_gram_accumulate (f32 chains over 2048-token chunks, f64 sums). */
+int cdclq_hessian_accumulate_device(cdclq_ctx* ctx, const float* x, const float* y, const float* token_w, size_t t,
+                                    size_t n, double* acc);
+/* The 1/N normalisation (scripts/capture_hessians.py:266): h = (f32)(acc / tokens), rounded once. */
+int cdclq_hessian_finalize_device(cdclq_ctx* ctx, const double* acc, size_t n, uint64_t tokens, float* h);
+
 /* linalg::upper_chol_of_inverse (src/linalg.rs:362-375): u (n x n f32, upper) with
  * h^-1 = u^T u. h is not modified. */
 int cdclq_upper_chol_of_inverse(cdclq_ctx* ctx, const double* h, size_t n, float* u);
