@@ -12,6 +12,7 @@
 // row, so a workgroup of 16 rows stages it in LDS when it fits; the descent evaluates all columns of
 // a sub-block at once and touches a row of H_sb only when a code moves, reading it from L2.
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 
 #include "cdclq_dev.h"
@@ -619,6 +620,23 @@ size_t panel_partials_elems(int m, int wd, int k) {
 
 int panel_row_tile() { return PR; }
 
+// resident workgroups of k_panel_dma on the whole device (cached per process)
+static hipError_t dma_slots(int* out) {
+  static std::atomic<int> cached{0};
+  int v = cached.load(std::memory_order_relaxed);
+  if (v == 0) {
+    int dev = 0, cus = 0, per = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err == hipSuccess) err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_panel_dma, 256, 0);
+    if (err != hipSuccess) return err;
+    v = std::max(1, cus * std::max(1, per));
+    cached.store(v, std::memory_order_relaxed);
+  }
+  *out = v;
+  return hipSuccess;
+}
+
 hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long lda, const float* B, long ldb,
                       float* P, const int* rtiles, int ntiles) {
   if (m <= 0 || wd <= 0 || k <= 0) return hipSuccess;
@@ -628,10 +646,11 @@ hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long
   constexpr int SK = 32;
   const long nunits = (long)ntiles * ((k + CDCLQ_KC - 1) / CDCLQ_KC) * ((wd + PC - 1) / PC);
   if (nunits > INT32_MAX) return hipErrorInvalidValue;
-  // one workgroup per resident slot (occupancy is a property of the kernel, cached per process)
-  static int slots[2] = {0, 0};
-  int& sl = slots[vec4 ? 1 : 0];
-  if (sl == 0) {
+  // one workgroup per resident slot (occupancy is a property of the kernel, cached per process;
+  // concurrent first calls compute the same value)
+  static std::atomic<int> slots[2] = {0, 0};
+  std::atomic<int>& sl = slots[vec4 ? 1 : 0];
+  if (sl.load(std::memory_order_relaxed) == 0) {
     int dev = 0, cus = 0, per = 0;
     hipError_t err = hipGetDevice(&dev);
     if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
@@ -639,20 +658,14 @@ hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long
       err = vec4 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_panel_gemm<SK, true>, 256, 0)
                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_panel_gemm<SK, false>, 256, 0);
     if (err != hipSuccess) return err;
-    sl = std::max(1, cus * std::max(1, per));
+    sl.store(std::max(1, cus * std::max(1, per)), std::memory_order_relaxed);
   }
-  const int grid = (int)std::min<long>(nunits, sl);
+  const int grid = (int)std::min<long>(nunits, sl.load(std::memory_order_relaxed));
   const bool dma = vec4 && k % DSK == 0 && wd % 4 == 0 && wd >= 4 && ldb % 4 == 0 && (uintptr_t)B % 16 == 0;
   if (dma) {
-    static int dslots = 0;
-    if (dslots == 0) {
-      int dev = 0, cus = 0, per = 0;
-      hipError_t err = hipGetDevice(&dev);
-      if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-      if (err == hipSuccess) err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_panel_dma, 256, 0);
-      if (err != hipSuccess) return err;
-      dslots = std::max(1, cus * std::max(1, per));
-    }
+    int dslots = 0;
+    const hipError_t err = dma_slots(&dslots);
+    if (err != hipSuccess) return err;
     hipLaunchKernelGGL(k_panel_dma, dim3((int)std::min<long>(nunits, dslots)), dim3(256), 0, st, m, wd, k, A, lda,
                        B, ldb, P, (int)nunits, rtiles, ntiles, (float*)nullptr, 0L, 0.0f, 0);
     return hipGetLastError();
@@ -674,15 +687,9 @@ bool chain_gemm_mfma_ok(int m, int n, int k, const float* A, long lda, const flo
 hipError_t chain_gemm_mfma(hipStream_t st, int m, int n, int k, float alpha, int beta_one, const float* A, long lda,
                            const float* B, long ldb, float* C, long ldc) {
   if (!chain_gemm_mfma_ok(m, n, k, A, lda, B, ldb)) return hipErrorInvalidValue;
-  static int dslots = 0;
-  if (dslots == 0) {
-    int dev = 0, cus = 0, per = 0;
-    hipError_t err = hipGetDevice(&dev);
-    if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (err == hipSuccess) err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_panel_dma, 256, 0);
-    if (err != hipSuccess) return err;
-    dslots = std::max(1, cus * std::max(1, per));
-  }
+  int dslots = 0;
+  const hipError_t err = dma_slots(&dslots);
+  if (err != hipSuccess) return err;
   const int ntiles = (m + PR - 1) / PR;
   const long nunits = (long)ntiles * ((n + PC - 1) / PC);
   hipLaunchKernelGGL(k_panel_dma, dim3((int)std::min<long>(nunits, dslots)), dim3(256), 0, st, m, n, k, A, lda, B, ldb,
@@ -703,12 +710,12 @@ hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, i
                        const float* h32, const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
                        const uint8_t* active, double* dlog, uint32_t* dcnt) {
   const int wd = std::min(gi * g + g, n) - gi * g;
-  static bool lds_raised = false;  // 64 KB of dynamic LDS for H_CC at wd = 128
-  if (!lds_raised) {
+  static std::atomic<bool> lds_raised{false};  // 64 KB of dynamic LDS for H_CC at wd = 128
+  if (!lds_raised.load(std::memory_order_acquire)) {
     const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_refit<2, true>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, 65536);
     if (err != hipSuccess) return err;
-    lds_raised = true;
+    lds_raised.store(true, std::memory_order_release);
   }
 #define REFIT_CASE(N, L)                                                                                               \
   do {                                                                                                                 \
