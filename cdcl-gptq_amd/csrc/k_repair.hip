@@ -8,9 +8,10 @@
 // element. Workgroup: 128 rows x 64 cols x one panel, E and the panel of H staged in
 // double-buffered LDS.
 //
-// Sweeps. One wavefront per row, columns spread over lanes. The refit needs all of H_CC for every
-// row, so a workgroup of 16 rows stages it in LDS when it fits; the descent evaluates all columns of
-// a sub-block at once and touches a row of H_sb only when a code moves, reading it from L2.
+// Sweeps. The refit of a group of at most 128 columns computes U H_CC for 64 rows on the matrix
+// cores from H_CC staged in LDS (wider groups: one wavefront per row, H_CC from L2). The descent
+// runs one wavefront per row, columns over lanes: it evaluates all columns of a sub-block at once
+// and touches a row of H_sb only when a code moves, reading it from L2.
 #include <algorithm>
 #include <atomic>
 #include <cstdint>
@@ -334,47 +335,19 @@ __global__ __launch_bounds__(256) void k_fold(int m, int wd, int np, const int* 
   G[g] = acc;
 }
 
-// Closed-form f16 scale refit of group gi (src/engine.rs:543-587). One wavefront advances RW rows
-// together (columns over lanes), so every H_CC element read from LDS feeds RW independent chains;
-// H_CC is staged once per workgroup (4 RW rows) as a zero-padded WP x WP tile.
+// Closed-form f16 scale refit of group gi (src/engine.rs:543-587) for groups wider than 128
+// columns (narrower ones take k_refit_mfma). One wavefront per row, columns over lanes; H_CC is
+// read from L2.
 template <int NPL>
-constexpr int refit_rows_per_wave() {
-  return NPL <= 2 ? 4 : 1;
-}
-
-template <int NPL, bool LDSH>
 __global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, int gi, int rc, const float* __restrict__ G,
                                                const float* __restrict__ h32,
                                                const uint8_t* __restrict__ codes, float* __restrict__ scales,
                                                const float* __restrict__ zeros, float* __restrict__ wq,
                                                float* __restrict__ e, const uint8_t* __restrict__ active,
                                                double* __restrict__ dlog, uint32_t* __restrict__ dcnt) {
-  constexpr int RW = refit_rows_per_wave<NPL>();
-  constexpr int WP = 64 * NPL;
-  extern __shared__ float hcc[];  // H_CC, WP x WP (zero outside wd x wd) when LDSH
+  constexpr int RW = 1;
   const int c0 = gi * g, wd = min(c0 + g, n) - c0;
   const int lane = threadIdx.x & 63;
-  if (LDSH) {
-    constexpr int PER = WP * WP / 256;
-    constexpr int BATCH = PER < 16 ? PER : 16;
-#pragma unroll
-    for (int b = 0; b < PER; b += BATCH) {
-      float v[BATCH];
-#pragma unroll
-      for (int u = 0; u < BATCH; ++u) {  // clamped addresses: every load is unconditional
-        const int x = threadIdx.x + 256 * (b + u);
-        const int k = x / WP, k2 = x % WP;
-        v[u] = h32[(long)(c0 + min(k, wd - 1)) * n + c0 + min(k2, wd - 1)];
-      }
-      __builtin_amdgcn_sched_barrier(0);  // keep the whole batch of loads in flight before any use
-#pragma unroll
-      for (int u = 0; u < BATCH; ++u) {
-        const int x = threadIdx.x + 256 * (b + u);
-        hcc[x] = (x / WP < wd && x % WP < wd) ? v[u] : 0.0f;
-      }
-    }
-    __syncthreads();
-  }
   const int rbase = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (threadIdx.x >> 6)) * RW);
   bool live[RW];
   bool any = false;
@@ -408,10 +381,7 @@ __global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, i
 #pragma unroll
     for (int s2 = 0; s2 < NPL; ++s2) {
       const int k2 = s2 * 64 + lane;
-      if (LDSH)
-        h[s2] = hcc[k * WP + k2];
-      else
-        h[s2] = k2 < wd ? h32[(long)(c0 + k) * n + c0 + k2] : 0.0f;
+      h[s2] = k2 < wd ? h32[(long)(c0 + k) * n + c0 + k2] : 0.0f;
     }
 #pragma unroll
     for (int q = 0; q < RW; ++q) {
@@ -502,6 +472,206 @@ __global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, i
       }
     }
     if (lane == 0) dcnt[r] = moved;
+  }
+}
+
+// Matrix-core refit for groups of at most 128 columns, 64 rows per workgroup, same results as
+// k_refit. hu = U H_CC (U = codes - zero, one row per row of the group) is a K = 1 chain per
+// element in k order (one KC panel), so v_mfma_f32_32x32x1_2b_f32 computes it as the sgemm does:
+// wave w takes rows 32 (w >> 1) .. +31 and columns 64 (w & 1) .. +63, A = u (read from the codes
+// staged in LDS), B = H_CC staged in LDS. The products u_k hu_k and u_k g_k are then formed in
+// parallel into LDS, the sequential sums num = sum u_k g_k and den = sum u_k hu_k run one lane per
+// row, and the accepted rows' e and W_hat are updated by the whole workgroup along the columns.
+constexpr int RF_ROWS = 64;
+constexpr int RF_CS = 132;  // byte stride of a staged code row (33 dwords: conflict-free by row)
+constexpr int RF_PS = 129;  // float stride of a staged product row (odd: conflict-free by row)
+
+__global__ __launch_bounds__(256) void k_refit_mfma(int rows, int n, int ng, int g, int gi, int rc,
+                                                    const float* __restrict__ G, const float* __restrict__ h32,
+                                                    const uint8_t* __restrict__ codes, float* __restrict__ scales,
+                                                    const float* __restrict__ zeros, float* __restrict__ wq,
+                                                    float* __restrict__ e, const uint8_t* __restrict__ active,
+                                                    double* __restrict__ dlog, uint32_t* __restrict__ dcnt) {
+  // H_CC (zero outside wd x wd), then the products: PH = S[0 ..], PG = S[RF_ROWS * RF_PS ..]
+  __shared__ float S[2 * RF_ROWS * RF_PS > 128 * 128 ? 2 * RF_ROWS * RF_PS : 128 * 128];
+  __shared__ uint32_t CB[RF_ROWS * RF_CS / 4];
+  __shared__ float zrow[RF_ROWS], snew[RF_ROWS];
+  __shared__ int mv[RF_ROWS];
+  __shared__ int nlive;
+  const int c0 = gi * g, wd = min(c0 + g, n) - c0;
+  const int r0 = blockIdx.x * RF_ROWS;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (tid == 0) nlive = 0;
+  __syncthreads();
+  if (tid < RF_ROWS) {
+    const int r = r0 + tid;
+    const bool live = r < rows && active[r / rc];
+    if (r < rows && !live) dcnt[r] = 0;
+    if (live) atomicAdd(&nlive, 1);
+    zrow[tid] = zeros[(long)min(r, rows - 1) * ng + gi];
+  }
+  __syncthreads();
+  if (nlive == 0) return;
+  const bool vec = wd == 128 && (n & 3) == 0 && (c0 & 3) == 0;  // whole, 16-byte aligned rows
+  if (vec) {  // stage H_CC with 16-byte loads (16 per thread, all in flight) and the codes by words
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int x = tid + 256 * u;  // float4 slot: row x >> 5, columns 4 (x & 31) ..
+      *reinterpret_cast<float4*>(&S[4 * x]) =
+          *reinterpret_cast<const float4*>(h32 + (long)(c0 + (x >> 5)) * n + c0 + 4 * (x & 31));
+    }
+#pragma unroll
+    for (int u = 0; u < RF_ROWS * 32 / 256; ++u) {
+      const int x = tid + 256 * u, rl = x >> 5, k4 = x & 31;
+      const int r = min(r0 + rl, rows - 1);
+      CB[rl * (RF_CS / 4) + k4] = *reinterpret_cast<const uint32_t*>(codes + (long)r * n + c0 + 4 * k4);
+    }
+  } else {  // clamped scalar loads, zero padding outside wd
+    constexpr int PER = 128 * 128 / 256, BATCH = 16;
+#pragma unroll
+    for (int b = 0; b < PER; b += BATCH) {
+      float v[BATCH];
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) {
+        const int x = tid + 256 * (b + u);
+        v[u] = h32[(long)(c0 + min(x >> 7, wd - 1)) * n + c0 + min(x & 127, wd - 1)];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) {
+        const int x = tid + 256 * (b + u);
+        S[x] = ((x >> 7) < wd && (x & 127) < wd) ? v[u] : 0.0f;
+      }
+    }
+    uint8_t* cb = reinterpret_cast<uint8_t*>(CB);
+#pragma unroll 8
+    for (int i = 0; i < RF_ROWS * 128 / 256; ++i) {
+      const int x = tid + 256 * i, rl = x >> 7, k = x & 127;
+      const int r = min(r0 + rl, rows - 1);
+      cb[rl * RF_CS + k] = k < wd ? codes[(long)r * n + c0 + k] : 0;
+    }
+  }
+  __syncthreads();
+  // hu chains on the matrix cores
+  const int wr = wv >> 1, wc = wv & 1;
+  const int arow = 32 * wr + (lane & 31);
+  const float za = zrow[arow];
+  const uint32_t* crow = CB + arow * (RF_CS / 4);
+  const float* hcol = S + 64 * wc + lane;
+  v32f acc = {};
+  int k0 = 0;
+  for (; k0 + 8 <= wd; k0 += 8) {
+    const uint32_t w0 = crow[k0 >> 2], w1 = crow[(k0 >> 2) + 1];
+    float hb[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) hb[j] = hcol[(k0 + j) * 128];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t w = j < 4 ? w0 : w1;
+      acc = mfma32((float)((w >> (8 * (j & 3))) & 0xffu) - za, hb[j], acc);
+    }
+  }
+  for (; k0 < wd; ++k0) {
+    const uint32_t w = crow[k0 >> 2];
+    acc = mfma32((float)((w >> (8 * (k0 & 3))) & 0xffu) - za, hcol[k0 * 128], acc);
+  }
+  __syncthreads();  // every wave is done with H_CC
+  const uint8_t* cb = reinterpret_cast<const uint8_t*>(CB);
+  float* PH = S;
+  float* PG = S + RF_ROWS * RF_PS;
+#pragma unroll
+  for (int r = 0; r < 32; ++r) {  // panel end C = fma(1, chain, 0), then u_k * hu_k
+    const int row = 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
+    const int col = 64 * wc + 32 * (r >> 4) + (lane & 31);
+    const float u = (float)cb[row * RF_CS + col] - zrow[row];
+    PH[row * RF_PS + col] = u * __builtin_fmaf(1.0f, acc[r], 0.0f);
+  }
+  {  // u_k * g_k: all of a thread's G loads in flight at once (clamped addresses)
+    constexpr int PER = RF_ROWS * 128 / 256;
+    float gv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int x = tid + 256 * i, rl = x >> 7, k = x & 127;
+      gv[i] = G[(long)min(r0 + rl, rows - 1) * wd + min(k, wd - 1)];
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int x = tid + 256 * i, rl = x >> 7, k = x & 127;
+      if (k < wd) PG[rl * RF_PS + k] = ((float)cb[rl * RF_CS + k] - zrow[rl]) * gv[i];
+    }
+  }
+  __syncthreads();
+  // num = sum_k u_k g_k, den = sum_k u_k hu_k, sequential in k (src/engine.rs:562-566); then the
+  // closed-form f16 scale and its acceptance test (:567-587)
+  if (wv == 0) {
+    const int r = r0 + lane;
+    const bool live = r < rows && active[r / rc];
+    int moved = 0;
+    float s_new = 0.0f;
+    if (live) {
+      const float* pg = PG + lane * RF_PS;
+      const float* ph = PH + lane * RF_PS;
+      float num = 0.0f, den = 0.0f;
+      int k = 0;
+      for (; k + 8 <= wd; k += 8) {
+        float a[8], b[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          a[j] = pg[k + j];
+          b[j] = ph[k + j];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          num = num + a[j];
+          den = den + b[j];
+        }
+      }
+      for (; k < wd; ++k) {
+        num = num + pg[k];
+        den = den + ph[k];
+      }
+      const float s_old = scales[(long)r * ng + gi];
+      if (den > 1e-30f) {
+        s_new = rs_maxf(round_f16(s_old + num / den), CDCLQ_F16_MIN_NORMAL);
+        const float d = s_new - s_old;
+        const float dl32 = (-2.0f * d) * num + (d * d) * den;
+        if ((double)dl32 < 0.0) {
+          scales[(long)r * ng + gi] = s_new;
+          dlog[r] = (double)dl32;
+          moved = 1;
+        }
+      }
+      dcnt[r] = moved;
+    }
+    mv[lane] = moved;
+    snew[lane] = s_new;
+  }
+  __syncthreads();
+  // e += W_hat - ndq, W_hat = ndq on the accepted rows, in two halves of 16 elements per thread
+  // with all of a half's loads in flight at once
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    constexpr int PER = RF_ROWS * 128 / 256 / 2;
+    float ev[PER], qv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int x = tid + 256 * (PER * h + i), rl = x >> 7, k = x & 127;
+      if (k < wd && mv[rl]) {
+        const long o = (long)(r0 + rl) * n + c0 + k;
+        ev[i] = e[o];
+        qv[i] = wq[o];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int x = tid + 256 * (PER * h + i), rl = x >> 7, k = x & 127;
+      if (k < wd && mv[rl]) {
+        const long o = (long)(r0 + rl) * n + c0 + k;
+        const float ndq = snew[rl] * ((float)cb[rl * RF_CS + k] - zrow[rl]);
+        e[o] = ev[i] + (qv[i] - ndq);
+        wq[o] = ndq;
+      }
+    }
   }
 }
 
@@ -710,26 +880,18 @@ hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, i
                        const float* h32, const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
                        const uint8_t* active, double* dlog, uint32_t* dcnt) {
   const int wd = std::min(gi * g + g, n) - gi * g;
-  static std::atomic<bool> lds_raised{false};  // 64 KB of dynamic LDS for H_CC at wd = 128
-  if (!lds_raised.load(std::memory_order_acquire)) {
-    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_refit<2, true>),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, 65536);
-    if (err != hipSuccess) return err;
-    lds_raised.store(true, std::memory_order_release);
+  if (wd <= 128) {
+    hipLaunchKernelGGL(k_refit_mfma, dim3((rows + RF_ROWS - 1) / RF_ROWS), dim3(256), 0, st, rows, n, ng, g, gi, rc, G,
+                       h32, codes, scales, zeros, wq, e, active, dlog, dcnt);
+    return hipGetLastError();
   }
-#define REFIT_CASE(N, L)                                                                                               \
-  do {                                                                                                                 \
-    constexpr int rows_per_wg = 4 * refit_rows_per_wave<N>();                                                        \
-    const size_t lds = (L) ? (size_t)(64 * N) * (64 * N) * 4 : 0;                                                      \
-    hipLaunchKernelGGL((k_refit<N, L>), dim3((rows + rows_per_wg - 1) / rows_per_wg), dim3(256), lds, st, rows, n, ng, \
-                       g, gi, rc, G, h32, codes, scales, zeros, wq, e, active, dlog, dcnt);                            \
-  } while (0)
+#define REFIT_CASE(N)                                                                                                  \
+  hipLaunchKernelGGL((k_refit<N>), dim3((rows + 3) / 4), dim3(256), 0, st, rows, n, ng, g, gi, rc, G, h32, codes,      \
+                     scales, zeros, wq, e, active, dlog, dcnt)
   switch (npl_for(wd)) {
-    case 1: REFIT_CASE(1, true); break;
-    case 2: REFIT_CASE(2, true); break;
-    case 4: REFIT_CASE(4, false); break;
-    case 8: REFIT_CASE(8, false); break;
-    case 16: REFIT_CASE(16, false); break;
+    case 4: REFIT_CASE(4); break;
+    case 8: REFIT_CASE(8); break;
+    case 16: REFIT_CASE(16); break;
     default: return hipErrorInvalidValue;
   }
 #undef REFIT_CASE
