@@ -209,10 +209,17 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
   };
   auto unit = [&](int u) {
     Unit t;
-    const int ct = u / (nrt * np), rem = u % (nrt * np);
-    t.r0 = (rtiles ? rtiles[rem / np] : rem / np) * PR;
-    t.p = rem % np;
-    t.cb = ct * PC;
+    if (C) {  // one panel; column tiles fastest, so consecutive units share their E tile
+      const int nct = (wd + PC - 1) / PC;
+      t.r0 = (u / nct) * PR;
+      t.cb = (u % nct) * PC;
+      t.p = 0;
+    } else {
+      const int ct = u / (nrt * np), rem = u % (nrt * np);
+      t.r0 = (rtiles ? rtiles[rem / np] : rem / np) * PR;
+      t.p = rem % np;
+      t.cb = ct * PC;
+    }
     t.k0 = t.p * CDCLQ_KC;
     t.nst = min(CDCLQ_KC, k - t.k0) / DSK;
     return t;
@@ -270,6 +277,7 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
   for (int cu_idx = u0; cu_idx < u1; ++cu_idx) {
     const Unit cu = unit(cu_idx);
     v32f acc = {};
+    float cv[32];  // with C: the unit's C values, loaded while its stages are multiplied
     for (int cs = 0; cs < cu.nst; ++cs) {
       // this wave's part of stage fc has landed once at most the next stage's loads are outstanding
       if (fi - fc >= 2)
@@ -278,6 +286,14 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
         wait_vmcnt<0>();
       __builtin_amdgcn_s_barrier();  // publishes all parts; all reads of stage fc - 1 are done
       if (cs + 1 < cu.nst) issue_next();  // into the slot of stage fc - 1
+      if (C && cs == 0) {
+#pragma unroll
+        for (int r = 0; r < 32; ++r) {  // clamped addresses; values outside m x wd are never used
+          const int row = min(cu.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), m - 1);
+          const int col = min(cu.cb + 32 * (r >> 4) + (lane & 31), wd - 1);
+          cv[r] = beta_one ? C[(long)row * ldc + col] : 0.0f;
+        }
+      }
       const float* buf = &R[fc % DNB][0];
       const float* es = buf + 32 * er;
       const float* hs = buf + DSK * PR + lane;
@@ -298,8 +314,7 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
       const int col = cu.cb + 32 * (r >> 4) + (lane & 31);
       if (row < m && col < wd) {
         if (C) {
-          float* cp = C + (long)row * ldc + col;
-          *cp = __builtin_fmaf(alpha, acc[r], beta_one ? *cp : 0.0f);
+          C[(long)row * ldc + col] = __builtin_fmaf(alpha, acc[r], cv[r]);
         } else {
           P[((long)cu.p * m + row) * wd + col] = acc[r];
         }
