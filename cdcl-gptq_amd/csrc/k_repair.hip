@@ -191,8 +191,10 @@ constexpr int DNB = 3;
 constexpr int DSTAGE = DSK * PR + DSK * PC;  // floats per stage (E 4096 + B 2048)
 constexpr int DPW = DSTAGE / 256 / 4;        // 1 KB loads per wave and stage (6)
 
-// With C != null (k <= 256, one panel) the unit's chain is final and is folded straight into C:
-// C = fma(alpha, chain, beta_one ? C : 0), the single-panel case of the GEMM fold.
+// DIRECT (C != null, k <= 256, one panel: the GPTQ lazy trailing update): the unit's chain is
+// final and is folded straight into C: C = fma(alpha, chain, beta_one ? C : 0), the single-panel
+// case of the GEMM fold. Otherwise (the repair gradient) the chains go to P.
+template <bool DIRECT>
 __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const float* __restrict__ A, long lda,
                                                    const float* __restrict__ B, long ldb, float* __restrict__ P,
                                                    int nunits, const int* __restrict__ rtiles, int nrt,
@@ -209,7 +211,7 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
   };
   auto unit = [&](int u) {
     Unit t;
-    if (C) {  // one panel; column tiles fastest, so consecutive units share their E tile
+    if (DIRECT) {  // one panel; column tiles fastest, so consecutive units share their E tile
       const int nct = (wd + PC - 1) / PC;
       t.r0 = (u / nct) * PR;
       t.cb = (u % nct) * PC;
@@ -286,7 +288,7 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
         wait_vmcnt<0>();
       __builtin_amdgcn_s_barrier();  // publishes all parts; all reads of stage fc - 1 are done
       if (cs + 1 < cu.nst) issue_next();  // into the slot of stage fc - 1
-      if (C && cs == 0) {
+      if (DIRECT && cs == 0) {
 #pragma unroll
         for (int r = 0; r < 32; ++r) {  // clamped addresses; values outside m x wd are never used
           const int row = min(cu.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), m - 1);
@@ -313,7 +315,7 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
       const int row = cu.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
       const int col = cu.cb + 32 * (r >> 4) + (lane & 31);
       if (row < m && col < wd) {
-        if (C) {
+        if (DIRECT) {
           C[(long)row * ldc + col] = __builtin_fmaf(alpha, acc[r], cv[r]);
         } else {
           P[((long)cu.p * m + row) * wd + col] = acc[r];
@@ -813,7 +815,7 @@ static hipError_t dma_slots(int* out) {
     int dev = 0, cus = 0, per = 0;
     hipError_t err = hipGetDevice(&dev);
     if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (err == hipSuccess) err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_panel_dma, 256, 0);
+    if (err == hipSuccess) err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_panel_dma<false>, 256, 0);
     if (err != hipSuccess) return err;
     v = std::max(1, cus * std::max(1, per));
     cached.store(v, std::memory_order_relaxed);
@@ -851,7 +853,7 @@ hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long
     int dslots = 0;
     const hipError_t err = dma_slots(&dslots);
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_panel_dma, dim3((int)std::min<long>(nunits, dslots)), dim3(256), 0, st, m, wd, k, A, lda,
+    hipLaunchKernelGGL(k_panel_dma<false>, dim3((int)std::min<long>(nunits, dslots)), dim3(256), 0, st, m, wd, k, A, lda,
                        B, ldb, P, (int)nunits, rtiles, ntiles, (float*)nullptr, 0L, 0.0f, 0);
     return hipGetLastError();
   }
@@ -877,7 +879,7 @@ hipError_t chain_gemm_mfma(hipStream_t st, int m, int n, int k, float alpha, int
   if (err != hipSuccess) return err;
   const int ntiles = (m + PR - 1) / PR;
   const long nunits = (long)ntiles * ((n + PC - 1) / PC);
-  hipLaunchKernelGGL(k_panel_dma, dim3((int)std::min<long>(nunits, dslots)), dim3(256), 0, st, m, n, k, A, lda, B, ldb,
+  hipLaunchKernelGGL(k_panel_dma<true>, dim3((int)std::min<long>(nunits, dslots)), dim3(256), 0, st, m, n, k, A, lda, B, ldb,
                      (float*)nullptr, (int)nunits, (const int*)nullptr, ntiles, C, ldc, alpha, beta_one);
   return hipGetLastError();
 }
