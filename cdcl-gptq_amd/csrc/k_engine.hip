@@ -65,16 +65,43 @@ __global__ __launch_bounds__(256) void k_inv_diag(int n, const float* __restrict
 }
 
 // ---------------------------------------------------------------- phase 1 (src/engine.rs:397-473)
-// One block [i1, i1+cnt) for all rows; NPL = values per lane (cnt <= 64*NPL).
+// One block [i1, i1+cnt) for all rows; NPL = values per lane (cnt <= 64*NPL), one wave per row,
+// GB_ROWS rows per workgroup. For blocks of at most 128 columns the workgroup stages the block of
+// U (rows and columns i1..i1+cnt) and 1/U_jj in LDS first, so the column steps, each of which
+// needs row j of the block, read it from LDS instead of a round trip to L2.
+constexpr int GB_ROWS = 8;
 template <int NPL>
-__global__ __launch_bounds__(256) void k_gptq_block(int rows, int n, int i1, int cnt, int g, int ng,
+__global__ __launch_bounds__(64 * GB_ROWS) void k_gptq_block(int rows, int n, int i1, int cnt, int g, int ng,
                                                     const float* __restrict__ w, const float* __restrict__ u,
                                                     const float* __restrict__ invd, const uint8_t* __restrict__ gbits,
                                                     int mse, float* __restrict__ scales, float* __restrict__ zeros,
                                                     uint8_t* __restrict__ codes, float* __restrict__ wq,
                                                     float* __restrict__ err) {
+  constexpr bool STAGE = NPL <= 2;
+  constexpr int UB = STAGE ? 64 * NPL : 1;  // staged block width
+  __shared__ float ub[UB * UB];
+  __shared__ float idv[UB];
   const int lane = threadIdx.x & 63;
-  const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if constexpr (STAGE) {  // clamped addresses: every load is unconditional, a batch in flight at once
+    constexpr int PER = UB * UB / (64 * GB_ROWS), BATCH = PER < 16 ? PER : 16;
+#pragma unroll
+    for (int b = 0; b < PER; b += BATCH) {
+      float v[BATCH];
+#pragma unroll
+      for (int q = 0; q < BATCH; ++q) {
+        const int x = threadIdx.x + 64 * GB_ROWS * (b + q), i = x / UB, c = x % UB;
+        v[q] = u[(long)(i1 + min(i, cnt - 1)) * n + i1 + min(c, cnt - 1)];
+      }
+#pragma unroll
+      for (int q = 0; q < BATCH; ++q) {
+        const int x = threadIdx.x + 64 * GB_ROWS * (b + q), i = x / UB, c = x % UB;
+        ub[x] = (i < cnt && c < cnt) ? v[q] : 0.0f;
+      }
+    }
+    if (threadIdx.x < UB) idv[threadIdx.x] = invd[i1 + min((int)threadIdx.x, cnt - 1)];
+    __syncthreads();
+  }
+  const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * GB_ROWS + (threadIdx.x >> 6));
   if (r >= rows) return;
   const int i2 = i1 + cnt;
   const float* wr = w + (long)r * n;
@@ -179,13 +206,13 @@ __global__ __launch_bounds__(256) void k_gptq_block(int rows, int n, int i1, int
       const float xv = readlane(x[s], ii);
       float q;
       const float dq = quant_dq(xv, sc, zr, maxq, &q);
-      const float e = (xv - dq) * invd[j];
+      const float e = (xv - dq) * (STAGE ? idv[i] : invd[j]);
       if (lane == ii) {
         mq[s] = q;
         mwq[s] = dq;
         me[s] = e;
       }
-      const float* urow = u + (long)j * n + i1;
+      const float* urow = STAGE ? ub + i * UB : u + (long)j * n + i1;
 #pragma unroll
       for (int s2 = s; s2 < NPL; ++s2) {
         const int c = s2 * 64 + lane;
@@ -380,7 +407,7 @@ static int npl_for(int cnt) {
 hipError_t gptq_block(hipStream_t st, int rows, int n, int i1, int cnt, int g, int ng, float* w, const float* u,
                       const float* invd, const uint8_t* gbits, int mse, float* scales, float* zeros, uint8_t* codes,
                       float* wq, float* err) {
-  const dim3 grid((rows + 3) / 4), blk(256);
+  const dim3 grid((rows + GB_ROWS - 1) / GB_ROWS), blk(64 * GB_ROWS);
 #define GPTQ_CASE(N)                                                                                                   \
   case N:                                                                                                              \
     hipLaunchKernelGGL(k_gptq_block<N>, grid, blk, 0, st, rows, n, i1, cnt, g, ng, w, u, invd, gbits, mse, scales,    \
