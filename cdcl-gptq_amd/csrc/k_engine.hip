@@ -255,77 +255,107 @@ __global__ __launch_bounds__(256) void k_sub(long count, const float* __restrict
 
 // Per-chunk loss bookkeeping of one pass, in the reference's order (src/engine.rs:583, :640):
 // steps in execution order (refit groups, then CD sub-blocks), within a step rows ascending,
-// within a row its accepted deltas in the order they were made. One workgroup per chunk. For each
-// step and batch of up to 256 rows the workgroup scans the rows' delta counts, gathers the deltas
-// into LDS in fold order (every output position finds its row by binary search over the scanned
-// offsets, so all loads are independent), and wave 0 folds them sequentially in f64.
+// within a row its accepted deltas in the order they were made. One workgroup per chunk. The
+// (step, row) entries of the chunk are taken ACC_ENT at a time in that order: each thread loads
+// the counts of ACC_ENT / 256 consecutive entries, one workgroup scan gives every entry its first
+// position in the fold order, and the deltas are gathered into LDS ACC_LDS positions at a time
+// (every position finds its entry by binary search over the offsets, so all loads are
+// independent). Waves 1-3 gather the next ACC_LDS positions while wave 0 folds the current ones
+// sequentially in f64, so the fold's add chain sets the time.
 constexpr int ACC_LDS = 4096;
+constexpr int ACC_ENT = 4096;
+constexpr int ACC_PER = ACC_ENT / 256;
 __global__ __launch_bounds__(256) void k_pass_accum(int rows, int rc, int nref, const double* __restrict__ rlog,
                                                     const uint32_t* __restrict__ rcnt, int ncd, int cap,
                                                     const double* __restrict__ clog,
                                                     const uint32_t* __restrict__ ccnt,
                                                     const uint8_t* __restrict__ active, double* __restrict__ ld,
                                                     uint64_t* __restrict__ upd) {
-  __shared__ double vals[ACC_LDS];
-  __shared__ uint32_t offs[257];  // exclusive offsets of the batch's rows; offs[nr] = total
+  __shared__ double vals[2][ACC_LDS];
+  __shared__ uint32_t offs[ACC_ENT + 1];  // exclusive offsets of the batch's entries; offs[ne] = total
   __shared__ uint32_t wsum[4];
   const int c = blockIdx.x;
   if (!active[c]) return;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int r0 = c * rc, r1 = min(rows, r0 + rc);
-  double acc = ld[c];  // meaningful in wave 0
+  const int r0 = c * rc, nr = min(rows, r0 + rc) - r0;
+  const long nent = (long)(nref + ncd) * nr;  // entries (step, row) of this chunk, fold order
+  double acc = ld[c];                          // meaningful in wave 0
   uint64_t u = upd[c];
-  for (int step = 0; step < nref + ncd; ++step) {
-    const bool refit = step < nref;
-    const long sbase = refit ? (long)step * rows : (long)(step - nref) * rows;
-    const uint32_t* cnt = refit ? rcnt : ccnt;
-    for (int base = r0; base < r1; base += 256) {
-      const int nr = min(256, r1 - base);
-      const int r = base + tid;
-      const uint32_t k = (tid < nr) ? cnt[sbase + r] : 0u;
-      // workgroup exclusive scan of k
-      uint32_t incl = k;
+  // entry e -> (step e / nr, row r0 + e % nr)
+  auto entry_cnt = [&](long e) -> uint32_t {
+    const int step = (int)(e / nr), row = r0 + (int)(e % nr);
+    return step < nref ? rcnt[(long)step * rows + row] : ccnt[(long)(step - nref) * rows + row];
+  };
+  auto value_at = [&](long e, uint32_t k) -> double {
+    const int step = (int)(e / nr), row = r0 + (int)(e % nr);
+    return step < nref ? rlog[(long)step * rows + row] : clog[((long)(step - nref) * rows + row) * cap + k];
+  };
+  for (long eb = 0; eb < nent; eb += ACC_ENT) {
+    const int ne = (int)min((long)ACC_ENT, nent - eb);
+    // counts of this thread's ACC_PER consecutive entries, all loads in flight at once
+    uint32_t k[ACC_PER];
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t v = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += v;
-      }
-      if (lane == 63) wsum[wv] = incl;
-      __syncthreads();
-      uint32_t before = 0;
-      for (int w = 0; w < wv; ++w) before += wsum[w];
-      const uint32_t total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
-      offs[tid] = before + incl - k;
-      if (tid == 0) offs[nr] = total;  // nr <= 256; entries past nr are never searched
-      __syncthreads();
-      if (total == 0) continue;  // uniform
-      u += total;
-      for (uint32_t done = 0; done < total; done += ACC_LDS) {
-        const uint32_t m = min((uint32_t)ACC_LDS, total - done);
-        for (uint32_t i = tid; i < m; i += 256) {
-          const uint32_t pos = done + i;
-          int lo = 0, hi = nr;  // largest j in [0, nr) with offs[j] <= pos
-          while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (offs[mid] <= pos) lo = mid; else hi = mid;
-          }
-          const long rr = sbase + base + lo;
-          vals[i] = refit ? rlog[rr] : clog[rr * cap + (pos - offs[lo])];
+    for (int q = 0; q < ACC_PER; ++q) {
+      const int e = tid * ACC_PER + q;
+      k[q] = e < ne ? entry_cnt(eb + e) : 0u;
+    }
+    uint32_t tsum = 0;
+#pragma unroll
+    for (int q = 0; q < ACC_PER; ++q) tsum += k[q];
+    uint32_t incl = tsum;  // workgroup exclusive scan of the thread sums
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t v = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += v;
+    }
+    if (lane == 63) wsum[wv] = incl;
+    __syncthreads();
+    uint32_t run = incl - tsum;
+    for (int w = 0; w < wv; ++w) run += wsum[w];
+    const uint32_t total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+#pragma unroll
+    for (int q = 0; q < ACC_PER; ++q) {
+      const int e = tid * ACC_PER + q;
+      if (e < ne) offs[e] = run;
+      run += k[q];
+    }
+    if (tid == 0) offs[ne] = total;
+    __syncthreads();
+    if (total == 0) continue;  // uniform
+    u += total;
+    // gather positions [done, done + m) into vals[buf]; threads [t0, t0 + nthr) take part
+    auto gather = [&](uint32_t done, int buf, int t0, int nthr) {
+      const uint32_t m = min((uint32_t)ACC_LDS, total - done);
+      for (uint32_t i = tid - t0; i < m; i += nthr) {
+        const uint32_t pos = done + i;
+        int lo = 0, hi = ne;  // largest e in [0, ne) with offs[e] <= pos
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if (offs[mid] <= pos) lo = mid; else hi = mid;
         }
-        __syncthreads();
-        if (wv == 0) {
-          uint32_t i = 0;
-          for (; i + 8 <= m; i += 8) {
-            double v[8];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) v[q] = vals[i + q];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) acc = acc + v[q];
-          }
-          for (; i < m; ++i) acc = acc + vals[i];
-        }
-        __syncthreads();
+        vals[buf][i] = value_at(eb + lo, pos - offs[lo]);
       }
+    };
+    gather(0, 0, 0, 256);
+    __syncthreads();
+    int buf = 0;
+    for (uint32_t done = 0; done < total; done += ACC_LDS) {
+      const uint32_t m = min((uint32_t)ACC_LDS, total - done);
+      if (wv == 0) {
+        uint32_t i = 0;
+        for (; i + 8 <= m; i += 8) {
+          double v[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) v[q] = vals[buf][i + q];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc = acc + v[q];
+        }
+        for (; i < m; ++i) acc = acc + vals[buf][i];
+      } else if (done + ACC_LDS < total) {
+        gather(done + ACC_LDS, buf ^ 1, 64, 192);
+      }
+      __syncthreads();
+      buf ^= 1;
     }
   }
   if (tid == 0) {
