@@ -71,7 +71,7 @@ def cpu_baseline(spec: dict, cores: int) -> dict:
 
     O.set_threads(cores)
     n0 = 4096 if "attn_in" in spec["inputs"] else 2048
-    ts = 2048
+    ts = 16384  # eight 2048-token chunks
     cs = O.synth_outlier_scales(101, n0, spec["outlier_frac"], spec["outlier_factor"])
     x = O.synth_tokens(102, ts, n0, cs)
     t0 = time.perf_counter()
@@ -86,7 +86,7 @@ def cpu_baseline(spec: dict, cores: int) -> dict:
     t_fac = time.perf_counter() - t0
     fac_full = t_fac * sum((n / n0) ** 3 for n in spec["inputs"].values())
     rc = 171 if n0 == 4096 else 64
-    rows = min(rc * cores, 4096)
+    rows = min(2 * rc * cores, 8192)  # two row chunks per thread
     w = O.synth_normal(103, rows * n0, spec["wsigma"]).reshape(rows, n0)
     cfg = O.config(**{**spec["cfg"], "row_chunk": rc})
     q = O.quantize_layer(w, h, cfg, nthreads=cores)
