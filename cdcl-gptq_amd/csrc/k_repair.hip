@@ -326,6 +326,113 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
   }
 }
 
+// The lazy trailing update C = fma(alpha, A B, C) (k <= 256, one panel) on 128 x 128 tiles: 8
+// waves, wave w rows 32 (w & 3) .. +31 and columns 64 (w >> 2) .. +63, one E tile read per 128
+// columns; the stage ring, load plan and per-element chain are those of k_panel_dma<true> (B
+// stage [32 k][128 cols], 2 k rows per load). Used when there are enough 128 x 128 tiles to give
+// every CU one.
+constexpr int LPC = 128;
+constexpr int LSTAGE = DSK * PR + DSK * LPC;   // 8192 floats = 32 KB
+constexpr int LDPW = LSTAGE / 512 / 4;         // 4 loads per wave and stage
+__global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const float* __restrict__ A, long lda,
+                                                   const float* __restrict__ B, long ldb, float* __restrict__ C,
+                                                   long ldc, float alpha, int nunits) {
+  __shared__ float R[DNB][LSTAGE];
+  const int nct = (wd + LPC - 1) / LPC;
+  const int u0 = (int)((long)blockIdx.x * nunits / gridDim.x);
+  const int u1 = (int)((long)(blockIdx.x + 1) * nunits / gridDim.x);
+  if (u0 >= u1) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wv & 3, wc = wv >> 2;
+  const int nst = k / DSK;
+  const uint32_t lds0 = lds_offset(&R[0][0]);
+  int iu_idx = u0, is = 0, fi = 0;
+  int ir0 = (u0 / nct) * PR, icb = (u0 % nct) * LPC;
+  bool ivalid = true;
+  int off[LDPW];
+  auto unit_offsets = [&]() {
+#pragma unroll
+    for (int q = 0; q < LDPW; ++q) {
+      const int ins = wv + 8 * q;
+      if (q < 2) {
+        const int rl = 8 * ins + (lane >> 3);
+        off[q] = (min(ir0 + rl, m - 1) - ir0) * (int)lda + 4 * ((lane & 7) ^ (rl & 7));
+      } else {
+        off[q] = (2 * (ins - 16) + (lane >> 5)) * (int)ldb + min(icb + 4 * (lane & 31), wd - 4);
+      }
+    }
+  };
+  unit_offsets();
+  auto issue_next = [&]() {
+    if (!ivalid) return;
+    const uint32_t buf = lds0 + (uint32_t)((fi % DNB) * LSTAGE * 4);
+    const int ks = is * DSK;
+    const float* ea = A + (long)ir0 * lda + ks;
+    const float* hb = B + (long)ks * ldb;
+#pragma unroll
+    for (int q = 0; q < LDPW; ++q) {
+      const int ins = wv + 8 * q;
+      dma16_untracked((q < 2 ? ea : hb) + off[q], buf + 1024u * (uint32_t)ins);
+    }
+    ++fi;
+    if (++is >= nst) {
+      if (++iu_idx < u1) {
+        ir0 = (iu_idx / nct) * PR;
+        icb = (iu_idx % nct) * LPC;
+        is = 0;
+        unit_offsets();
+      } else {
+        ivalid = false;
+      }
+    }
+  };
+  issue_next();
+  issue_next();
+  const int er = 32 * wr + (lane & 31);
+  int fc = 0;
+  for (int cu_idx = u0; cu_idx < u1; ++cu_idx) {
+    const int r0 = (cu_idx / nct) * PR, cb = (cu_idx % nct) * LPC;
+    v32f acc = {};
+    float cv[32];
+    for (int cs = 0; cs < nst; ++cs) {
+      if (fi - fc >= 2)
+        wait_vmcnt<LDPW>();
+      else
+        wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      if (cs + 1 < nst) issue_next();
+      if (cs == 0) {
+#pragma unroll
+        for (int r = 0; r < 32; ++r) {
+          const int row = min(r0 + 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), m - 1);
+          const int col = min(cb + 64 * wc + 32 * (r >> 4) + (lane & 31), wd - 1);
+          cv[r] = C[(long)row * ldc + col];
+        }
+      }
+      const float* buf = &R[fc % DNB][0];
+      const float* es = buf + 32 * er;
+      const float* hs = buf + DSK * PR + 64 * wc + lane;
+#pragma unroll
+      for (int q = 0; q < DSK / 4; ++q) {
+        const float4 a = *reinterpret_cast<const float4*>(es + 4 * (q ^ (er & 7)));
+        acc = mfma32(a.x, hs[(4 * q + 0) * LPC], acc);
+        acc = mfma32(a.y, hs[(4 * q + 1) * LPC], acc);
+        acc = mfma32(a.z, hs[(4 * q + 2) * LPC], acc);
+        acc = mfma32(a.w, hs[(4 * q + 3) * LPC], acc);
+      }
+      ++fc;
+    }
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+      const int row = r0 + 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
+      const int col = cb + 64 * wc + 32 * (r >> 4) + (lane & 31);
+      if (row < m && col < wd) C[(long)row * ldc + col] = __builtin_fmaf(alpha, acc[r], cv[r]);
+    }
+    issue_next();
+  }
+}
+
 // G[r][c] = ordered fold of the panel chains (alpha 1, beta 0): C = fma(1, P_p, C) for p = 0, 1, ...
 // One thread per element of the listed 128-row tiles, panel loads unrolled so many are in flight.
 __global__ __launch_bounds__(256) void k_fold(int m, int wd, int np, const int* __restrict__ rtiles, long count,
@@ -874,6 +981,22 @@ bool chain_gemm_mfma_ok(int m, int n, int k, const float* A, long lda, const flo
 hipError_t chain_gemm_mfma(hipStream_t st, int m, int n, int k, float alpha, int beta_one, const float* A, long lda,
                            const float* B, long ldb, float* C, long ldc) {
   if (!chain_gemm_mfma_ok(m, n, k, A, lda, B, ldb)) return hipErrorInvalidValue;
+  static std::atomic<int> wide_slots{0};  // resident k_lazy_wide workgroups (cached per process)
+  int ws = wide_slots.load(std::memory_order_relaxed);
+  if (ws == 0) {
+    int dev = 0, cus = 0, per = 0;
+    hipError_t e2 = hipGetDevice(&dev);
+    if (e2 == hipSuccess) e2 = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e2 == hipSuccess) e2 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_lazy_wide, 512, 0);
+    if (e2 != hipSuccess) return e2;
+    ws = std::max(1, cus * std::max(1, per));
+    wide_slots.store(ws, std::memory_order_relaxed);
+  }
+  const long wunits = (long)((m + PR - 1) / PR) * ((n + LPC - 1) / LPC);
+  if (beta_one && wunits >= ws && wunits <= INT32_MAX) {
+    hipLaunchKernelGGL(k_lazy_wide, dim3(ws), dim3(512), 0, st, m, n, k, A, lda, B, ldb, C, ldc, alpha, (int)wunits);
+    return hipGetLastError();
+  }
   int dslots = 0;
   const hipError_t err = dma_slots(&dslots);
   if (err != hipSuccess) return err;
