@@ -55,26 +55,29 @@ __global__ __launch_bounds__(256) void k_build_flipped_f64(int n, const double* 
 // is final (right-looking) performs exactly the same operations on every element in the same
 // order, with the trailing triangle updated in parallel.
 //
-// Element (i, j) lives in a register of thread (i % 16, j % 16) of a 16 x 16 thread grid for the
-// whole factorisation (2-D cyclic, so every step's trailing triangle is spread over all threads).
+// Element (i, j) lives in a register of thread (i % DGR, j % DGR) of a DGR x DGR thread grid for
+// the whole factorisation (2-D cyclic, so every step's trailing triangle is spread over all
+// threads; 32 x 32 threads hold 3 x 3 slots each).
 // Per step t: the pivot and the divisions of column t run one per thread from the LDS copy of the
 // column (pre), then every thread applies column t to its elements (slot rows and columns that lie
 // wholly before t are skipped by the wave); the owners of column t + 1 copy it to LDS for the next
 // step.
-constexpr int DS = NBC / 16;  // row / column slots per thread
-__global__ __launch_bounds__(256) void k_chol_diag(int n, double* __restrict__ a, int k, int kb, int* status,
+constexpr int DGR = 32;         // thread grid side
+constexpr int DS = NBC / DGR;   // row / column slots per thread
+constexpr int DGT = DGR * DGR;  // threads
+__global__ __launch_bounds__(DGT) void k_chol_diag(int n, double* __restrict__ a, int k, int kb, int* status,
                                                    double* pivot) {
   __shared__ double pre[NBC];  // column t with all earlier columns applied, before the division
   __shared__ double col[NBC];  // column t of L
   if (*status) return;
-  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
-  const int wrow_max = 4 * ((tid >> 6) + 1) - 1;  // the wave's largest tr
+  const int tid = threadIdx.x, tr = tid / DGR, tc = tid % DGR;
+  const int wrow_max = (64 / DGR) * ((tid >> 6) + 1) - 1;  // the wave's largest tr
   double v[DS][DS];
 #pragma unroll
   for (int r = 0; r < DS; ++r)
 #pragma unroll
     for (int c = 0; c < DS; ++c) {
-      const int i = 16 * r + tr, j = 16 * c + tc;
+      const int i = DGR * r + tr, j = DGR * c + tc;
       v[r][c] = a[(long)(k + min(i, kb - 1)) * n + k + min(j, kb - 1)];
     }
   __builtin_amdgcn_sched_barrier(0);
@@ -82,7 +85,7 @@ __global__ __launch_bounds__(256) void k_chol_diag(int n, double* __restrict__ a
   for (int r = 0; r < DS; ++r)
 #pragma unroll
     for (int c = 0; c < DS; ++c) {
-      const int i = 16 * r + tr, j = 16 * c + tc;
+      const int i = DGR * r + tr, j = DGR * c + tc;
       if (!(i < kb && j <= i)) v[r][c] = 0.0;
       if (j == 0 && i < kb) pre[i] = v[r][c];
     }
@@ -103,16 +106,16 @@ __global__ __launch_bounds__(256) void k_chol_diag(int n, double* __restrict__ a
     double ci[DS], cj[DS];
 #pragma unroll
     for (int q = 0; q < DS; ++q) {
-      ci[q] = col[16 * q + tr];
-      cj[q] = col[16 * q + tc];
+      ci[q] = col[DGR * q + tr];
+      cj[q] = col[DGR * q + tc];
     }
 #pragma unroll
     for (int r = 0; r < DS; ++r) {
-      if (16 * r + wrow_max < t) continue;  // the wave's rows in this slot are all finished
+      if (DGR * r + wrow_max < t) continue;  // the wave's rows in this slot are all finished
 #pragma unroll
       for (int c = 0; c < DS; ++c) {
-        if (16 * c + 15 < t) continue;  // all columns of this slot are finished
-        const int i = 16 * r + tr, j = 16 * c + tc;
+        if (DGR * c + DGR - 1 < t) continue;  // all columns of this slot are finished
+        const int i = DGR * r + tr, j = DGR * c + tc;
         if (i < kb && i >= t) {
           if (j == t)
             v[r][c] = ci[r];
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(256) void k_chol_diag(int n, double* __restrict__ a
   for (int r = 0; r < DS; ++r)
 #pragma unroll
     for (int c = 0; c < DS; ++c) {
-      const int i = 16 * r + tr, j = 16 * c + tc;
+      const int i = DGR * r + tr, j = DGR * c + tc;
       if (i < kb && j <= i) a[(long)(k + i) * n + k + j] = v[r][c];
     }
 }
@@ -245,7 +248,7 @@ hipError_t build_flipped_f64(hipStream_t st, int n, const double* h, double* a) 
 }
 
 hipError_t chol_diag(hipStream_t st, int n, double* a, int k, int kb, int* status, double* pivot) {
-  hipLaunchKernelGGL(k_chol_diag, dim3(1), dim3(256), 0, st, n, a, k, kb, status, pivot);
+  hipLaunchKernelGGL(k_chol_diag, dim3(1), dim3(DGT), 0, st, n, a, k, kb, status, pivot);
   return hipGetLastError();
 }
 
