@@ -147,7 +147,7 @@ __device__ __forceinline__ void dma16(const float* g, float* lds) {
 // orders the data with wait_vmcnt and a barrier. The memory clobber keeps the compiler from moving
 // LDS accesses across it; s_nop 0 covers the M0-write to LDS-DMA wait state. M0 is clobbered:
 // only for kernels whose compiled code does not otherwise keep a value in M0 (checked for
-// k_panel_dma, where these blocks are M0's only writers and nothing else reads it).
+// k_panel_dma and k_lazy_wide, where these blocks are M0's only writers and nothing else reads it).
 __device__ __forceinline__ void dma16_untracked(const float* g, uint32_t lds_byte_offset) {
   const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_byte_offset);
   uint32_t m0out;  // M0 is written by the block: declared as an output so the compiler knows
