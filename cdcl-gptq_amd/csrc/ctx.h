@@ -34,7 +34,7 @@ struct cdclq_ctx {
   using DevBuf = cdclq::DevBuf;
   DevBuf w_in, h_in, m_in, x_in, y_in, h64_in, u_out, codes_o, scales_o, zeros_o;
   DevBuf wp, wwork, wq, ebuf, gbits_d, perm_d, deadp_d, dead_d, diag_d, colsq_d, invd, colloss_d;
-  DevBuf G, part, rlog, rcnt, clog, ccnt, active_d, sel_d, ld_d, upd_d, mp, t1, t2, a64, y64, tbuf, tpart, status_d, rtiles_d,
+  DevBuf G, part, rlog, rcnt, clog, ccnt, sel_d, ld_d, mp, t1, t2, a64, y64, tbuf, tpart, status_d, rtiles_d,
       tiles_d, proxy_p, cs_d;
   // one-entry PrepCache (src/engine.rs:207-223): key, perm, damping and the device factors
   bool cache_valid = false;
@@ -50,6 +50,9 @@ struct cdclq_ctx {
   std::vector<uint8_t> pk_layout_wid;
   // timing
   bool timing = false;
+  // pinned host staging of the repair loop's per-pass transfers (grows; freed with the context)
+  void* pin = nullptr;
+  size_t pin_size = 0;
   std::vector<cdclq::TimedRegion> pending;
   std::vector<hipEvent_t> event_pool;  // recycled timing events (creating one per region is slow)
   uint32_t pk_epoch = 0;               // tags this call's device flags (no per-call clearing)

@@ -157,6 +157,21 @@ int factor(cdclq_ctx* ctx, int n, double* a, double* y, float* u) {
   return CDCLQ_OK;
 }
 
+// Pinned host staging of at least `bytes` (kept by the context; a larger request replaces it
+// after the stream has drained, since earlier copies may still read it).
+int ensure_pinned(cdclq_ctx* ctx, size_t bytes) {
+  if (ctx->pin_size >= bytes) return CDCLQ_OK;
+  if (ctx->pin) {
+    HIPCK(hipStreamSynchronize(ctx->st));
+    HIPCK(hipHostFree(ctx->pin));
+    ctx->pin = nullptr;
+    ctx->pin_size = 0;
+  }
+  HIPCK(hipHostMalloc(&ctx->pin, bytes, hipHostMallocDefault));
+  ctx->pin_size = bytes;
+  return CDCLQ_OK;
+}
+
 // The G = E H[:, c0:c0+wd] GEMM of phase 2 (src/engine.rs:548, :608): per-panel chains into
 // ctx->part, then folded in panel order into ctx->G.
 int grad_gemm(cdclq_ctx* ctx, int rows, int n, int c0, int wd, const float* e, const float* h32, const int* rtiles,
@@ -398,12 +413,14 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
     uint32_t* rcnt = P<uint32_t>(ctx->rcnt);
     double* clog = do_cd ? P<double>(ctx->clog) : nullptr;
     uint32_t* ccnt = do_cd ? P<uint32_t>(ctx->ccnt) : nullptr;
-    CK(ensure(ctx, ctx->active_d, (size_t)nchunks));
-    CK(ensure(ctx, ctx->ld_d, (size_t)nchunks * 8));
-    CK(ensure(ctx, ctx->upd_d, (size_t)nchunks * 8));
-    HIPCK(hipMemsetAsync(ctx->ld_d.p, 0, (size_t)nchunks * 8, st));
+    // Per-pass transfers, each one copy through pinned memory: down, the chunk losses and update
+    // counts (ld_d = [ld f64 | upd u64]); up, the active flags and the tile lists (rtiles_d =
+    // [active u8, padded to 16 bytes | tile lists i32]).
+    CK(ensure(ctx, ctx->ld_d, (size_t)nchunks * 16));
+    double* ldd = P<double>(ctx->ld_d);
+    uint64_t* updd = reinterpret_cast<uint64_t*>(ldd + nchunks);
+    HIPCK(hipMemsetAsync(ldd, 0, (size_t)nchunks * 8, st));
     std::vector<uint8_t> act(nchunks, 1);
-    HIPCK(hipMemcpyAsync(ctx->active_d.p, act.data(), nchunks, hipMemcpyHostToDevice, st));
     std::vector<double> prev(nchunks, 0.0);
     std::vector<uint64_t> upd(nchunks);
     // The gradient GEMM runs only over the 128-row tiles that hold rows of a chunk still being
@@ -411,8 +428,26 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
     // chunks that selected it). A null list means every tile (the final refit).
     const int rt = panel_row_tile(), ntile = (d_out + rt - 1) / rt;
     std::vector<int> tl((size_t)(1 + n_sb) * ntile), tcnt(1 + n_sb);
-    CK(ensure(ctx, ctx->rtiles_d, tl.size() * sizeof(int)));
-    int* rtiles = P<int>(ctx->rtiles_d);
+    const size_t apad = ((size_t)nchunks + 15) / 16 * 16, up_bytes = apad + tl.size() * sizeof(int);
+    CK(ensure(ctx, ctx->rtiles_d, up_bytes));
+    uint8_t* active = P<uint8_t>(ctx->rtiles_d);
+    int* rtiles = reinterpret_cast<int*>(P<char>(ctx->rtiles_d) + apad);
+    CK(ensure_pinned(ctx, up_bytes + (size_t)nchunks * 16));
+    char* pin_up = static_cast<char*>(ctx->pin);
+    char* pin_down = pin_up + up_bytes;
+    auto upload_pass = [&]() -> int {  // the previous upload has finished: every pass ends in a sync
+      std::memcpy(pin_up, act.data(), nchunks);
+      std::memcpy(pin_up + apad, tl.data(), tl.size() * sizeof(int));
+      HIPCK(hipMemcpyAsync(ctx->rtiles_d.p, pin_up, up_bytes, hipMemcpyHostToDevice, st));
+      return CDCLQ_OK;
+    };
+    auto download_pass = [&]() -> int {
+      HIPCK(hipMemcpyAsync(pin_down, ldd, (size_t)nchunks * 16, hipMemcpyDeviceToHost, st));
+      HIPCK(hipStreamSynchronize(st));
+      std::memcpy(ld.data(), pin_down, (size_t)nchunks * 8);
+      std::memcpy(upd.data(), pin_down + (size_t)nchunks * 8, (size_t)nchunks * 8);
+      return CDCLQ_OK;
+    };
     auto build_tiles = [&]() -> int {
       for (int l = 0; l <= n_sb; ++l) {
         int cnt = 0;
@@ -425,8 +460,7 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
         }
         tcnt[l] = cnt;
       }
-      HIPCK(hipMemcpyAsync(rtiles, tl.data(), tl.size() * sizeof(int), hipMemcpyHostToDevice, st));
-      return CDCLQ_OK;
+      return upload_pass();
     };
     CK(build_tiles());
     bool all_tiles = false;
@@ -436,13 +470,13 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
         const int c0 = gi * g, wd = std::min(c0 + g, n) - c0;
         CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32, all_tiles ? nullptr : rtiles, all_tiles ? ntile : tcnt[0]));
         HIPCK(refit_group(st, d_out, n, ng, g, gi, rc, P<float>(ctx->G), H32, codes, scales, zeros, wq, eb,
-                          P<uint8_t>(ctx->active_d), rlog + (size_t)gi * d_out, rcnt + (size_t)gi * d_out));
+                          active, rlog + (size_t)gi * d_out, rcnt + (size_t)gi * d_out));
       }
       return CDCLQ_OK;
     };
     const uint64_t npass = cfg->passes > 0 ? cfg->passes : 1;
     for (uint64_t pass = 0; pass < npass; ++pass) {
-      HIPCK(hipMemsetAsync(ctx->upd_d.p, 0, (size_t)nchunks * 8, st));
+      HIPCK(hipMemsetAsync(updd, 0, (size_t)nchunks * 8, st));
       if (do_refit) CK(refit_all());
       if (do_cd) {
         HIPCK(hipMemsetAsync(ccnt, 0, (size_t)n_sb * d_out * 4, st));
@@ -453,15 +487,13 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
           const int c0 = s * sbw, wd = std::min(c0 + sbw, n) - c0;
           CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32, rtiles + (size_t)(1 + s) * ntile, tcnt[1 + s]));
           HIPCK(cd_subblock(st, d_out, n, ng, g, c0, wd, s, n_sb, rc, (int)cfg->cd_sweeps, P<float>(ctx->G), H32,
-                            P<uint8_t>(ctx->gbits_d), scales, zeros, codes, wq, eb, P<uint8_t>(ctx->active_d),
+                            P<uint8_t>(ctx->gbits_d), scales, zeros, codes, wq, eb, active,
                             P<uint8_t>(ctx->sel_d), clog + (size_t)s * d_out * cap, ccnt + (size_t)s * d_out, cap));
         }
       }
       HIPCK(pass_accum(st, d_out, rc, nchunks, do_refit ? ng : 0, rlog, rcnt, do_cd ? n_sb : 0, cap, clog, ccnt,
-                       P<uint8_t>(ctx->active_d), P<double>(ctx->ld_d), P<uint64_t>(ctx->upd_d)));
-      HIPCK(hipMemcpyAsync(ld.data(), ctx->ld_d.p, (size_t)nchunks * 8, hipMemcpyDeviceToHost, st));
-      HIPCK(hipMemcpyAsync(upd.data(), ctx->upd_d.p, (size_t)nchunks * 8, hipMemcpyDeviceToHost, st));
-      HIPCK(hipStreamSynchronize(st));
+                       active, ldd, updd));
+      CK(download_pass());
       bool any_active = false;
       for (int c = 0; c < nchunks; ++c) {
         if (!act[c]) continue;
@@ -474,20 +506,16 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
           any_active = true;
       }
       if (!any_active) break;
-      HIPCK(hipMemcpyAsync(ctx->active_d.p, act.data(), nchunks, hipMemcpyHostToDevice, st));
       CK(build_tiles());
     }
     if (do_refit) {  // final refit (src/engine.rs:668-670)
       std::fill(act.begin(), act.end(), 1);
       all_tiles = true;
-      HIPCK(hipMemcpyAsync(ctx->active_d.p, act.data(), nchunks, hipMemcpyHostToDevice, st));
-      HIPCK(hipMemsetAsync(ctx->upd_d.p, 0, (size_t)nchunks * 8, st));
+      CK(upload_pass());
+      HIPCK(hipMemsetAsync(updd, 0, (size_t)nchunks * 8, st));
       CK(refit_all());
-      HIPCK(pass_accum(st, d_out, rc, nchunks, ng, rlog, rcnt, 0, cap, clog, ccnt, P<uint8_t>(ctx->active_d),
-                       P<double>(ctx->ld_d), P<uint64_t>(ctx->upd_d)));
-      HIPCK(hipMemcpyAsync(ld.data(), ctx->ld_d.p, (size_t)nchunks * 8, hipMemcpyDeviceToHost, st));
-      HIPCK(hipMemcpyAsync(upd.data(), ctx->upd_d.p, (size_t)nchunks * 8, hipMemcpyDeviceToHost, st));
-      HIPCK(hipStreamSynchronize(st));
+      HIPCK(pass_accum(st, d_out, rc, nchunks, ng, rlog, rcnt, 0, cap, clog, ccnt, active, ldd, updd));
+      CK(download_pass());
       for (int c = 0; c < nchunks; ++c) updates[c] += upd[c];
     }
   }
@@ -671,8 +699,8 @@ void cdclq_ctx_destroy(cdclq_ctx* ctx) {
   DevBuf* bufs[] = {&ctx->w_in, &ctx->h_in, &ctx->m_in, &ctx->x_in, &ctx->y_in, &ctx->h64_in, &ctx->u_out,
                     &ctx->codes_o, &ctx->scales_o, &ctx->zeros_o, &ctx->wp, &ctx->wwork, &ctx->wq, &ctx->ebuf,
                     &ctx->gbits_d, &ctx->perm_d, &ctx->deadp_d, &ctx->dead_d, &ctx->diag_d, &ctx->colsq_d,
-                    &ctx->invd, &ctx->colloss_d, &ctx->G, &ctx->part, &ctx->rlog, &ctx->rcnt, &ctx->clog, &ctx->ccnt, &ctx->active_d, &ctx->rtiles_d,
-                    &ctx->sel_d, &ctx->ld_d, &ctx->upd_d, &ctx->mp, &ctx->t1, &ctx->t2, &ctx->a64, &ctx->y64,
+                    &ctx->invd, &ctx->colloss_d, &ctx->G, &ctx->part, &ctx->rlog, &ctx->rcnt, &ctx->clog, &ctx->ccnt, &ctx->rtiles_d,
+                    &ctx->sel_d, &ctx->ld_d, &ctx->mp, &ctx->t1, &ctx->t2, &ctx->a64, &ctx->y64,
                     &ctx->tbuf, &ctx->tpart, &ctx->status_d, &ctx->tiles_d, &ctx->proxy_p, &ctx->cs_d,
                     &ctx->cache_u, &ctx->cache_h32, &ctx->pk_flag};
   for (DevBuf* b : bufs) free_buf(*b);
@@ -680,6 +708,7 @@ void cdclq_ctx_destroy(cdclq_ctx* ctx) {
   for (DevBuf& b : ctx->pk_out) free_buf(b);
   for (DevBuf& b : ctx->pk_tab) free_buf(b);
   for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
+  if (ctx->pin) (void)hipHostFree(ctx->pin);
   (void)hipStreamSynchronize(ctx->st2);
   (void)hipEventDestroy(ctx->ev_col);
   (void)hipEventDestroy(ctx->ev_panel);
