@@ -318,7 +318,7 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
         if (DIRECT) {
           C[(long)row * ldc + col] = __builtin_fmaf(alpha, acc[r], cv[r]);
         } else {
-          P[((long)cu.p * m + row) * wd + col] = acc[r];
+          __builtin_nontemporal_store(acc[r], &P[((long)cu.p * m + row) * wd + col]);
         }
       }
     }
@@ -451,11 +451,11 @@ __global__ __launch_bounds__(256) void k_fold(int m, int wd, int np, const int* 
   for (; p + 8 <= np; p += 8) {
     float v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = src[(long)(p + u) * pstride];
+    for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(src + (long)(p + u) * pstride);
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(1.0f, v[u], acc);
   }
-  for (; p < np; ++p) acc = __builtin_fmaf(1.0f, src[(long)p * pstride], acc);
+  for (; p < np; ++p) acc = __builtin_fmaf(1.0f, __builtin_nontemporal_load(src + (long)p * pstride), acc);
   G[g] = acc;
 }
 
