@@ -272,13 +272,25 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
   issue_next();
   const int er = 32 * wv + (lane & 31);
   // Vector memory operations complete in issue order, so "at most the newest DPW outstanding"
-  // means everything older -- stage fc and any P stores issued before stage fc + 1 -- is done. At
-  // a unit's last stage the next load is issued after the unit's P stores, so the wait that
-  // follows does not also hold back the stage after.
+  // means everything older -- stage fc and any stores issued before stage fc + 1's loads -- is
+  // done. With C, at a unit's last stage the next load is issued after the unit's C stores, so the
+  // wait that follows does not also hold back the stage after. Without C, a unit's chains stay in
+  // acc until the next unit's first stage has landed and are stored there, before that stage's
+  // load is issued: the stores then have the whole stage to complete before the next wait.
   int fc = 0;
+  v32f acc = {};
+  Unit pu = iu;  // without C: the unit whose chains acc holds
+  auto store_p = [&](const Unit& t) {
+    // block b = r >> 4 (cols 32b..), row i = (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), col j = lane & 31
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+      const int row = t.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
+      const int col = t.cb + 32 * (r >> 4) + (lane & 31);
+      if (row < m && col < wd) __builtin_nontemporal_store(acc[r], &P[((long)t.p * m + row) * wd + col]);
+    }
+  };
   for (int cu_idx = u0; cu_idx < u1; ++cu_idx) {
     const Unit cu = unit(cu_idx);
-    v32f acc = {};
     float cv[32];  // with C: the unit's C values, loaded while its stages are multiplied
     for (int cs = 0; cs < cu.nst; ++cs) {
       // this wave's part of stage fc has landed once at most the next stage's loads are outstanding
@@ -287,7 +299,11 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
       else
         wait_vmcnt<0>();
       __builtin_amdgcn_s_barrier();  // publishes all parts; all reads of stage fc - 1 are done
-      if (cs + 1 < cu.nst) issue_next();  // into the slot of stage fc - 1
+      if (!DIRECT && cs == 0 && cu_idx > u0) {
+        store_p(pu);
+        acc = v32f{};
+      }
+      if (!DIRECT || cs + 1 < cu.nst) issue_next();  // into the slot of stage fc - 1
       if (DIRECT && cs == 0) {
 #pragma unroll
         for (int r = 0; r < 32; ++r) {  // clamped addresses; values outside m x wd are never used
@@ -309,21 +325,20 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
       }
       ++fc;
     }
-    // block b = r >> 4 (cols 32b..), row i = (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), col j = lane & 31
+    if (DIRECT) {
 #pragma unroll
-    for (int r = 0; r < 32; ++r) {
-      const int row = cu.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
-      const int col = cu.cb + 32 * (r >> 4) + (lane & 31);
-      if (row < m && col < wd) {
-        if (DIRECT) {
-          C[(long)row * ldc + col] = __builtin_fmaf(alpha, acc[r], cv[r]);
-        } else {
-          __builtin_nontemporal_store(acc[r], &P[((long)cu.p * m + row) * wd + col]);
-        }
+      for (int r = 0; r < 32; ++r) {
+        const int row = cu.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
+        const int col = cu.cb + 32 * (r >> 4) + (lane & 31);
+        if (row < m && col < wd) C[(long)row * ldc + col] = __builtin_fmaf(alpha, acc[r], cv[r]);
       }
+      acc = v32f{};
+      issue_next();  // the load deferred at the unit's last stage
+    } else {
+      pu = cu;
     }
-    issue_next();  // the load deferred at the unit's last stage
   }
+  if (!DIRECT) store_p(pu);
 }
 
 // The lazy trailing update C = fma(alpha, A B, C) (k <= 256, one panel) on 128 x 128 tiles: 8
