@@ -201,8 +201,14 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
                                                    float* __restrict__ C, long ldc, float alpha, int beta_one) {
   __shared__ float R[DNB][DSTAGE];
   const int np = k / CDCLQ_KC + (k % CDCLQ_KC != 0);
-  const int u0 = (int)((long)blockIdx.x * nunits / gridDim.x);
-  const int u1 = (int)((long)(blockIdx.x + 1) * nunits / gridDim.x);
+  // With a full grid (two workgroups per CU), workgroups j and j + G/2 end up on the same CU: the
+  // first half fills every CU once and the second half pairs up with it in dispatch order. They
+  // take adjacent unit ranges 2j and 2j + 1, whose sizes (floor and ceiling of units / G) add up
+  // to the CU's fair share when units / G is not whole.
+  const int G = gridDim.x, j = blockIdx.x;
+  const int v = (G & 1) ? j : (j < G / 2 ? 2 * j : 2 * (j - G / 2) + 1);
+  const int u0 = (int)((long)v * nunits / G);
+  const int u1 = (int)((long)(v + 1) * nunits / G);
   if (u0 >= u1) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
