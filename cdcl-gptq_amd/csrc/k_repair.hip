@@ -15,6 +15,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdint>
+#include <type_traits>
 
 #include "cdclq_dev.h"
 #include "kernels.h"
@@ -620,17 +621,25 @@ __global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, i
   }
 }
 
-// Matrix-core refit for groups of at most 128 columns, 64 rows per workgroup, same results as
+// Matrix-core refit for groups of at most 128 columns, RF_ROWS rows per workgroup, same results as
 // k_refit. hu = U H_CC (U = codes - zero, one row per row of the group) is a K = 1 chain per
-// element in k order (one KC panel), so v_mfma_f32_32x32x1_2b_f32 computes it as the sgemm does:
-// wave w takes rows 32 (w >> 1) .. +31 and columns 64 (w & 1) .. +63, A = u (read from the codes
-// staged in LDS), B = H_CC staged in LDS. The products u_k hu_k and u_k g_k are then formed in
+// element in k order (one KC panel), so a K = 1 MFMA computes it as the sgemm does. 64 rows:
+// v_mfma_f32_32x32x1_2b_f32, wave w takes rows 32 (w >> 1) .. +31 and columns 64 (w & 1) .. +63.
+// 16 rows (for matrices with too few rows to give every CU a 64-row workgroup): waves 0 and 1
+// take columns 64 w .. +63 with v_mfma_f32_16x16x1_4b_f32, its four 16 x 16 blocks side by side
+// (lane l supplies A = u of row l % 16 and B = H_CC column 64 w + l; D register r of lane l is
+// row 4 (l >> 4) + (r & 3), column 64 w + 16 (r >> 2) + (l & 15)). A = u is read from the codes
+// staged in LDS, B = H_CC staged in LDS. The products u_k hu_k and u_k g_k are then formed in
 // parallel into LDS, the sequential sums num = sum u_k g_k and den = sum u_k hu_k run one lane per
 // row, and the accepted rows' e and W_hat are updated by the whole workgroup along the columns.
-constexpr int RF_ROWS = 64;
 constexpr int RF_CS = 132;  // byte stride of a staged code row (33 dwords: conflict-free by row)
 constexpr int RF_PS = 129;  // float stride of a staged product row (odd: conflict-free by row)
 
+__device__ __forceinline__ v16f mfma16(float a, float b, v16f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0);
+}
+
+template <int RF_ROWS>
 __global__ __launch_bounds__(256) void k_refit_mfma(int rows, int n, int ng, int g, int gi, int rc,
                                                     const float* __restrict__ G, const float* __restrict__ h32,
                                                     const uint8_t* __restrict__ codes, float* __restrict__ scales,
@@ -698,38 +707,52 @@ __global__ __launch_bounds__(256) void k_refit_mfma(int rows, int n, int ng, int
   }
   __syncthreads();
   // hu chains on the matrix cores
-  const int wr = wv >> 1, wc = wv & 1;
-  const int arow = 32 * wr + (lane & 31);
+  constexpr bool R64 = RF_ROWS == 64;
+  static_assert(RF_ROWS == 64 || RF_ROWS == 16, "64- or 16-row workgroups");
+  const int wr = R64 ? wv >> 1 : 0, wc = R64 ? wv & 1 : wv;
+  const bool mwave = R64 || wv < 2;
+  const int arow = R64 ? 32 * wr + (lane & 31) : (lane & 15);
   const float za = zrow[arow];
   const uint32_t* crow = CB + arow * (RF_CS / 4);
-  const float* hcol = S + 64 * wc + lane;
-  v32f acc = {};
-  int k0 = 0;
-  for (; k0 + 8 <= wd; k0 += 8) {
-    const uint32_t w0 = crow[k0 >> 2], w1 = crow[(k0 >> 2) + 1];
-    float hb[8];
+  const float* hcol = S + 64 * (wc & 1) + lane;
+  typedef typename std::conditional<R64, v32f, v16f>::type acc_t;
+  acc_t acc = {};
+  auto step = [&](float a, float b) {
+    if constexpr (R64)
+      acc = mfma32(a, b, acc);
+    else
+      acc = mfma16(a, b, acc);
+  };
+  if (mwave) {
+    int k0 = 0;
+    for (; k0 + 8 <= wd; k0 += 8) {
+      const uint32_t w0 = crow[k0 >> 2], w1 = crow[(k0 >> 2) + 1];
+      float hb[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) hb[j] = hcol[(k0 + j) * 128];
+      for (int j = 0; j < 8; ++j) hb[j] = hcol[(k0 + j) * 128];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t w = j < 4 ? w0 : w1;
-      acc = mfma32((float)((w >> (8 * (j & 3))) & 0xffu) - za, hb[j], acc);
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t w = j < 4 ? w0 : w1;
+        step((float)((w >> (8 * (j & 3))) & 0xffu) - za, hb[j]);
+      }
     }
-  }
-  for (; k0 < wd; ++k0) {
-    const uint32_t w = crow[k0 >> 2];
-    acc = mfma32((float)((w >> (8 * (k0 & 3))) & 0xffu) - za, hcol[k0 * 128], acc);
+    for (; k0 < wd; ++k0) {
+      const uint32_t w = crow[k0 >> 2];
+      step((float)((w >> (8 * (k0 & 3))) & 0xffu) - za, hcol[k0 * 128]);
+    }
   }
   __syncthreads();  // every wave is done with H_CC
   const uint8_t* cb = reinterpret_cast<const uint8_t*>(CB);
   float* PH = S;
   float* PG = S + RF_ROWS * RF_PS;
+  if (mwave) {
 #pragma unroll
-  for (int r = 0; r < 32; ++r) {  // panel end C = fma(1, chain, 0), then u_k * hu_k
-    const int row = 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
-    const int col = 64 * wc + 32 * (r >> 4) + (lane & 31);
-    const float u = (float)cb[row * RF_CS + col] - zrow[row];
-    PH[row * RF_PS + col] = u * __builtin_fmaf(1.0f, acc[r], 0.0f);
+    for (int r = 0; r < (R64 ? 32 : 16); ++r) {  // panel end C = fma(1, chain, 0), then u_k * hu_k
+      const int row = R64 ? 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5) : 4 * (lane >> 4) + (r & 3);
+      const int col = R64 ? 64 * wc + 32 * (r >> 4) + (lane & 31) : 64 * wc + 16 * (r >> 2) + (lane & 15);
+      const float u = (float)cb[row * RF_CS + col] - zrow[row];
+      PH[row * RF_PS + col] = u * __builtin_fmaf(1.0f, acc[r], 0.0f);
+    }
   }
   {  // u_k * g_k: all of a thread's G loads in flight at once (clamped addresses)
     constexpr int PER = RF_ROWS * 128 / 256;
@@ -748,7 +771,7 @@ __global__ __launch_bounds__(256) void k_refit_mfma(int rows, int n, int ng, int
   __syncthreads();
   // num = sum_k u_k g_k, den = sum_k u_k hu_k, sequential in k (src/engine.rs:562-566); then the
   // closed-form f16 scale and its acceptance test (:567-587)
-  if (wv == 0) {
+  if (wv == 0 && lane < RF_ROWS) {
     const int r = r0 + lane;
     const bool live = r < rows && active[r / rc];
     int moved = 0;
@@ -935,6 +958,22 @@ size_t panel_partials_elems(int m, int wd, int k) {
 
 int panel_row_tile() { return PR; }
 
+// compute units of the current device (cached per process)
+static hipError_t cu_count(int* out) {
+  static std::atomic<int> cached{0};
+  int v = cached.load(std::memory_order_relaxed);
+  if (v == 0) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err == hipSuccess) err = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess) return err;
+    v = std::max(1, v);
+    cached.store(v, std::memory_order_relaxed);
+  }
+  *out = v;
+  return hipSuccess;
+}
+
 // resident workgroups of k_panel_dma on the whole device (cached per process)
 static hipError_t dma_slots(int* out) {
   static std::atomic<int> cached{0};
@@ -1042,8 +1081,16 @@ hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, i
                        const uint8_t* active, double* dlog, uint32_t* dcnt) {
   const int wd = std::min(gi * g + g, n) - gi * g;
   if (wd <= 128) {
-    hipLaunchKernelGGL(k_refit_mfma, dim3((rows + RF_ROWS - 1) / RF_ROWS), dim3(256), 0, st, rows, n, ng, g, gi, rc, G,
-                       h32, codes, scales, zeros, wq, e, active, dlog, dcnt);
+    // 64-row workgroups while they give at least half of the CUs one; 16-row ones below that
+    int cus = 0;
+    const hipError_t err = cu_count(&cus);
+    if (err != hipSuccess) return err;
+    if ((rows + 63) / 64 >= cus / 2)
+      hipLaunchKernelGGL(k_refit_mfma<64>, dim3((rows + 63) / 64), dim3(256), 0, st, rows, n, ng, g, gi, rc, G, h32,
+                         codes, scales, zeros, wq, e, active, dlog, dcnt);
+    else
+      hipLaunchKernelGGL(k_refit_mfma<16>, dim3((rows + 15) / 16), dim3(256), 0, st, rows, n, ng, g, gi, rc, G, h32,
+                         codes, scales, zeros, wq, e, active, dlog, dcnt);
     return hipGetLastError();
   }
 #define REFIT_CASE(N)                                                                                                  \

@@ -190,6 +190,16 @@ def test_quantize_repair_knobs(ctx):
                     label=str(kw))
 
 
+@pytest.mark.parametrize("d_out", [1000, 8256])
+def test_quantize_refit_row_tilings(ctx, d_out):
+    """The group refit runs 16-row workgroups when 64-row ones would leave more than half of the
+    CUs idle (fewer than 64 x CUs / 2 rows, 8128 on a 256-CU part) and 64-row ones above: 1000 rows
+    take the 16-row form (ragged last workgroup), 8256 the 64-row form (ragged last workgroup)."""
+    w, x, h, _ = synth_layer(40 + d_out % 7, d_out, 256, 1024)
+    assert_same(*run_both(ctx, w, h, bits=4, group=128, block=128, act_order=True, passes=3, row_chunk=64),
+                label=f"refit rows {d_out}")
+
+
 def test_quantize_skeleton_and_dead_columns(ctx):
     w, x, h, _ = synth_layer(33, 64, 256, 800)
     h = h.copy()
