@@ -5,6 +5,9 @@ Flags that the engine's bit-exactness depends on:
   -ffp-contract=off   no implicit a*b+c fusion anywhere (fused ops are explicit fma calls)
   -Xclang -target-feature -Xclang -packed-fp32-ops   keep packed-FP32 VALU forms out of the code
 hipcc's default correctly-rounded f32 division/sqrt and IEEE denormal handling are kept.
+For speed: -mllvm -amdgpu-mfma-vgpr-form keeps MFMA accumulators in ordinary VGPRs (the same
+instructions in their VGPR form), so loop-carried accumulators are not copied between AGPRs and
+VGPRs around every LDS stage.
 """
 from __future__ import annotations
 
@@ -28,6 +31,7 @@ SOURCES = ["k_gemm.hip", "k_gram.hip", "k_factor.hip", "k_engine.hip", "k_repair
 COMMON = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-function", "-Wno-unknown-pragmas",
     "-I", INCLUDE, "-I", CSRC,
 ]
