@@ -139,33 +139,40 @@ __global__ __launch_bounds__(256) void k_gemm(int m, int n, int k, T alpha, int 
 // order differs in a third of the cases) matched that sequence bit for bit. Operand layout: lane l
 // supplies A[l % 16][l / 16] and B[l / 16][l % 16]; D[i][j] is register r of lane j + 16 (i % 4)
 // with i = l / 16 + 4 r. Slots past the end of k hold A = -0, B = +0, whose step c + (-0) = c is
-// exact. Workgroup tile 64 x 64, wave (wi, wj) owns rows 32 wi.., cols 32 wj.. as 2 x 2 blocks;
-// k is staged 16 at a time through double-buffered LDS. Operand loads are 16-byte pairs along the
-// contiguous dimension when the host found it aligned (mode 1: along k, mode 2: along i / j).
+// exact. Workgroup tile BM x 64 (BM = 64, or 96 for the triangular inverse's 96-row block rows,
+// which a 64-row tile would cover with a quarter of its rows idle); wave (wi, wj) owns rows
+// (BM / 2) wi.., cols 32 wj.. as (BM / 32) x 2 blocks; k is staged 16 at a time through
+// double-buffered LDS. Operand loads are 16-byte pairs along the contiguous dimension when the
+// host found it aligned (mode 1: along k, mode 2: along i / j).
 typedef double v4d __attribute__((ext_vector_type(4)));
 typedef double v2d __attribute__((ext_vector_type(2)));
 constexpr int DBM = 64, DBN = 64, DKT = 16, DPAD = 16;
 
-template <bool SPLIT, bool LOWER>
+template <bool SPLIT, bool LOWER, int BM = DBM>
 __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double alpha, int beta_one,
                                                     const double* __restrict__ A, long rsa, long csa, int amode,
                                                     const double* __restrict__ B, long rsb, long csb, int bmode,
                                                     double* __restrict__ C, long rsc, long csc, double* __restrict__ P,
                                                     int b_tri) {
-  __shared__ double As[2][DKT][DBM + DPAD];  // As[.][k][i]
+  static_assert(BM == 64 || BM == 96, "64- or 96-row tiles");
+  constexpr int WR = BM / 2;        // rows per wave
+  constexpr int NBI = WR / 16;      // 16-row blocks per wave
+  constexpr int QA = BM * DKT / 512;  // A pairs per thread and stage
+  constexpr int PA = BM / 2;        // A pairs per k row (mode 2)
+  __shared__ double As[2][DKT][BM + DPAD];   // As[.][k][i]
   __shared__ double Bs[2][DKT][DBN + DPAD];  // Bs[.][k][j]
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wi = wv >> 1, wj = wv & 1;
-  const int i0 = blockIdx.y * DBM, j0 = blockIdx.x * DBN;
-  if (LOWER && j0 > i0 + DBM - 1) return;  // tile strictly above the diagonal
+  const int i0 = blockIdx.y * BM, j0 = blockIdx.x * DBN;
+  if (LOWER && j0 > i0 + BM - 1) return;  // tile strictly above the diagonal
   int kbeg = 0, kend = k;
   if (SPLIT) {
     kbeg = blockIdx.z * CDCLQ_KC;
     kend = min(k, kbeg + CDCLQ_KC);
   }
   const int kfirst = b_tri ? max(kbeg, (j0 / DKT) * DKT) : kbeg;
-  v2d ra[2], rb[2];
-  // pair p = tid + 256 q of the A tile (64 x 16) / B tile (16 x 64); 2 doubles each
+  v2d ra[QA], rb[2];
+  // pair p = tid + 256 q of the A tile (BM x 16) / B tile (16 x 64); 2 doubles each
   auto a_at = [&](int i, int kk) -> double {
     return (i < m && kk < kend) ? A[(long)i * rsa + (long)kk * csa] : -0.0;
   };
@@ -174,10 +181,10 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
   };
   auto gload = [&](int k0) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < QA; ++q) {
       const int pr = tid + 256 * q;
       if (amode == 2) {  // along i
-        const int kk = pr >> 5, i = (pr & 31) * 2, gi = i0 + i, gk = k0 + kk;
+        const int kk = pr / PA, i = (pr % PA) * 2, gi = i0 + i, gk = k0 + kk;
         if (gi + 1 < m && gk < kend)
           ra[q] = *reinterpret_cast<const v2d*>(A + (long)gi * rsa + (long)gk * csa);
         else
@@ -189,6 +196,10 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
         else
           ra[q] = v2d{a_at(gi, gk), a_at(gi, gk + 1)};
       }
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int pr = tid + 256 * q;
       if (bmode == 2) {  // along j
         const int kk = pr >> 5, j = (pr & 31) * 2, gj = j0 + j, gk = k0 + kk;
         if (gj + 1 < n && gk < kend)
@@ -206,10 +217,10 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
   };
   auto lstore = [&](int buf) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < QA; ++q) {
       const int pr = tid + 256 * q;
       if (amode == 2) {
-        const int kk = pr >> 5, i = (pr & 31) * 2;
+        const int kk = pr / PA, i = (pr % PA) * 2;
         As[buf][kk][i] = ra[q].x;
         As[buf][kk][i + 1] = ra[q].y;
       } else {
@@ -217,6 +228,10 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
         As[buf][kk][i] = ra[q].x;
         As[buf][kk + 1][i] = ra[q].y;
       }
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int pr = tid + 256 * q;
       if (bmode == 2) {
         const int kk = pr >> 5, j = (pr & 31) * 2;
         Bs[buf][kk][j] = rb[q].x;
@@ -228,9 +243,9 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
       }
     }
   };
-  v4d acc[2][2], cv[2][2];
+  v4d acc[NBI][2], cv[NBI][2];
 #pragma unroll
-  for (int bi = 0; bi < 2; ++bi)
+  for (int bi = 0; bi < NBI; ++bi)
 #pragma unroll
     for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
@@ -238,7 +253,7 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
         acc[bi][bj][r] = 0.0;
         cv[bi][bj][r] = 0.0;
         if (!SPLIT && beta_one) {
-          const int gi = i0 + 32 * wi + 16 * bi + (lane >> 4) + 4 * r, gj = j0 + 32 * wj + 16 * bj + (lane & 15);
+          const int gi = i0 + WR * wi + 16 * bi + (lane >> 4) + 4 * r, gj = j0 + 32 * wj + 16 * bj + (lane & 15);
           if (gi < m && gj < n) cv[bi][bj][r] = C[(long)gi * rsc + (long)gj * csc];
         }
       }
@@ -253,14 +268,13 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
     if (s + 1 < nst) gload(k0 + DKT);
 #pragma unroll
     for (int k4 = 0; k4 < DKT; k4 += 4) {
-      double a[2], b[2];
+      double a[NBI], b[2];
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        a[x] = As[buf][k4 + (lane >> 4)][32 * wi + 16 * x + (lane & 15)];
-        b[x] = Bs[buf][k4 + (lane >> 4)][32 * wj + 16 * x + (lane & 15)];
-      }
+      for (int x = 0; x < NBI; ++x) a[x] = As[buf][k4 + (lane >> 4)][WR * wi + 16 * x + (lane & 15)];
 #pragma unroll
-      for (int bi = 0; bi < 2; ++bi)
+      for (int x = 0; x < 2; ++x) b[x] = Bs[buf][k4 + (lane >> 4)][32 * wj + 16 * x + (lane & 15)];
+#pragma unroll
+      for (int bi = 0; bi < NBI; ++bi)
 #pragma unroll
         for (int bj = 0; bj < 2; ++bj)
           acc[bi][bj] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[bi], b[bj], acc[bi][bj], 0, 0, 0);
@@ -271,7 +285,7 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
       const int kn = k0 + DKT;
       if ((kn % CDCLQ_KC) == 0 || kn >= kend) {
 #pragma unroll
-        for (int bi = 0; bi < 2; ++bi)
+        for (int bi = 0; bi < NBI; ++bi)
 #pragma unroll
           for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
@@ -283,12 +297,12 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
     }
   }
 #pragma unroll
-  for (int bi = 0; bi < 2; ++bi)
+  for (int bi = 0; bi < NBI; ++bi)
 #pragma unroll
     for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int gi = i0 + 32 * wi + 16 * bi + (lane >> 4) + 4 * r, gj = j0 + 32 * wj + 16 * bj + (lane & 15);
+        const int gi = i0 + WR * wi + 16 * bi + (lane >> 4) + 4 * r, gj = j0 + 32 * wj + 16 * bj + (lane & 15);
         if (gi < m && gj < n) {
           if (SPLIT)
             P[((long)blockIdx.z * m + gi) * n + gj] = acc[bi][bj][r];
@@ -350,8 +364,14 @@ hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, int beta_one
     if (np > 1 && partials != nullptr && !lower) {
       dim3 g3 = grid;
       g3.z = np;
-      hipLaunchKernelGGL((k_dgemm_mfma<true, false>), g3, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa, am,
-                         B, rsb, csb, bm, C, rsc, csc, partials, bt);
+      if (m == 96) {  // the triangular inverse's block rows: one 96-row tile
+        g3.y = 1;
+        hipLaunchKernelGGL((k_dgemm_mfma<true, false, 96>), g3, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa,
+                           csa, am, B, rsb, csb, bm, C, rsc, csc, partials, bt);
+      } else {
+        hipLaunchKernelGGL((k_dgemm_mfma<true, false>), g3, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa,
+                           am, B, rsb, csb, bm, C, rsc, csc, partials, bt);
+      }
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL((k_combine<T>), dim3((unsigned)(((long)m * n + 255) / 256)), dim3(256), 0, st, m, n, np,
