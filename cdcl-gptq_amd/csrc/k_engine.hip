@@ -203,20 +203,29 @@ __global__ __launch_bounds__(64 * GB_ROWS) void k_gptq_block(int rows, int n, in
           zeros[(long)r * ng + gi] = zr;
         }
       }
+      // With the block staged, row i of U and 1/U_ii are read before the column's quantization,
+      // so the LDS latency overlaps the division instead of following it (unconditional reads
+      // inside the staged block; lanes outside the update discard them).
+      float uv[NPL], di = 0.0f;
+      if constexpr (STAGE) {
+        di = idv[i];
+#pragma unroll
+        for (int s2 = 0; s2 < NPL; ++s2) uv[s2] = ub[i * UB + s2 * 64 + lane];
+      }
       const float xv = readlane(x[s], ii);
       float q;
       const float dq = quant_dq(xv, sc, zr, maxq, &q);
-      const float e = (xv - dq) * (STAGE ? idv[i] : invd[j]);
+      const float e = (xv - dq) * (STAGE ? di : invd[j]);
       if (lane == ii) {
         mq[s] = q;
         mwq[s] = dq;
         me[s] = e;
       }
-      const float* urow = STAGE ? ub + i * UB : u + (long)j * n + i1;
+      const float* urow = u + (long)j * n + i1;
 #pragma unroll
       for (int s2 = s; s2 < NPL; ++s2) {
         const int c = s2 * 64 + lane;
-        if (c > i && c < cnt) x[s2] = x[s2] - e * urow[c];
+        if (c > i && c < cnt) x[s2] = x[s2] - e * (STAGE ? uv[s2] : urow[c]);
       }
     }
   }
