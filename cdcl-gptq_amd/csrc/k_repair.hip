@@ -186,7 +186,9 @@ __global__ __launch_bounds__(256) void k_panel_gemm(int m, int wd, int k, const 
 // reads eight whole 128-byte row segments, and the XOR keeps the b128 reads of 32 rows free of bank
 // conflicts), then B as [32 k][64 cols] (load j: lane l -> k row 4 j + (l >> 4), columns
 // 4 (l & 15) .. +3). Rows past m and columns past wd are read from clamped addresses and only
-// reach outputs that are never stored.
+// reach outputs that are never stored. The per-panel chains are written with nontemporal stores
+// (and k_fold reads them with nontemporal loads): they are used once, and cached they would evict
+// E, which the next step streams again and which fits the last-level cache on its own.
 constexpr int DSK = 32;
 constexpr int DNB = 3;
 constexpr int DSTAGE = DSK * PR + DSK * PC;  // floats per stage (E 4096 + B 2048)
