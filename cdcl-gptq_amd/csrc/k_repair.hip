@@ -354,25 +354,47 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
 // waves, wave w rows 32 (w & 3) .. +31 and columns 64 (w >> 2) .. +63, one E tile read per 128
 // columns; the stage ring, load plan and per-element chain are those of k_panel_dma<true> (B
 // stage [32 k][128 cols], 2 k rows per load). Used when there are enough 128 x 128 tiles to give
-// every CU one.
+// every CU one. Without C (DIRECT false) the same tile computes the repair gradient's 128-column
+// per-panel chains (units (row tile, panel)), stored to P as k_panel_dma<false> stores them, when
+// there are at least four units per workgroup.
 constexpr int LPC = 128;
 constexpr int LSTAGE = DSK * PR + DSK * LPC;   // 8192 floats = 32 KB
 constexpr int LDPW = LSTAGE / 512 / 4;         // 4 loads per wave and stage
+template <bool DIRECT>
 __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const float* __restrict__ A, long lda,
                                                    const float* __restrict__ B, long ldb, float* __restrict__ C,
-                                                   long ldc, float alpha, int nunits) {
+                                                   long ldc, float alpha, int nunits, float* __restrict__ P,
+                                                   const int* __restrict__ rtiles) {
   __shared__ float R[DNB][LSTAGE];
   const int nct = (wd + LPC - 1) / LPC;
+  const int np = k / CDCLQ_KC + (k % CDCLQ_KC != 0);
   const int u0 = (int)((long)blockIdx.x * nunits / gridDim.x);
   const int u1 = (int)((long)(blockIdx.x + 1) * nunits / gridDim.x);
   if (u0 >= u1) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wv & 3, wc = wv >> 2;
-  const int nst = k / DSK;
+  struct Unit {
+    int r0, cb, p, k0, nst;
+  };
+  auto unit = [&](int u) {
+    Unit t;
+    if (DIRECT) {  // one panel, column tiles fastest
+      t.r0 = (u / nct) * PR;
+      t.cb = (u % nct) * LPC;
+      t.p = 0;
+    } else {  // the repair gradient, wd == 128: (row tile, panel), panels fastest
+      t.r0 = (rtiles ? rtiles[u / np] : u / np) * PR;
+      t.cb = 0;
+      t.p = u % np;
+    }
+    t.k0 = t.p * CDCLQ_KC;
+    t.nst = min(CDCLQ_KC, k - t.k0) / DSK;
+    return t;
+  };
   const uint32_t lds0 = lds_offset(&R[0][0]);
   int iu_idx = u0, is = 0, fi = 0;
-  int ir0 = (u0 / nct) * PR, icb = (u0 % nct) * LPC;
+  Unit iu = unit(u0);
   bool ivalid = true;
   int off[LDPW];
   auto unit_offsets = [&]() {
@@ -381,9 +403,9 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
       const int ins = wv + 8 * q;
       if (q < 2) {
         const int rl = 8 * ins + (lane >> 3);
-        off[q] = (min(ir0 + rl, m - 1) - ir0) * (int)lda + 4 * ((lane & 7) ^ (rl & 7));
+        off[q] = (min(iu.r0 + rl, m - 1) - iu.r0) * (int)lda + 4 * ((lane & 7) ^ (rl & 7));
       } else {
-        off[q] = (2 * (ins - 16) + (lane >> 5)) * (int)ldb + min(icb + 4 * (lane & 31), wd - 4);
+        off[q] = (2 * (ins - 16) + (lane >> 5)) * (int)ldb + min(iu.cb + 4 * (lane & 31), wd - 4);
       }
     }
   };
@@ -391,8 +413,8 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
   auto issue_next = [&]() {
     if (!ivalid) return;
     const uint32_t buf = lds0 + (uint32_t)((fi % DNB) * LSTAGE * 4);
-    const int ks = is * DSK;
-    const float* ea = A + (long)ir0 * lda + ks;
+    const int ks = iu.k0 + is * DSK;
+    const float* ea = A + (long)iu.r0 * lda + ks;
     const float* hb = B + (long)ks * ldb;
 #pragma unroll
     for (int q = 0; q < LDPW; ++q) {
@@ -400,10 +422,9 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
       dma16_untracked((q < 2 ? ea : hb) + off[q], buf + 1024u * (uint32_t)ins);
     }
     ++fi;
-    if (++is >= nst) {
+    if (++is >= iu.nst) {
       if (++iu_idx < u1) {
-        ir0 = (iu_idx / nct) * PR;
-        icb = (iu_idx % nct) * LPC;
+        iu = unit(iu_idx);
         is = 0;
         unit_offsets();
       } else {
@@ -414,23 +435,38 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
   issue_next();
   issue_next();
   const int er = 32 * wr + (lane & 31);
+  // Ordering as in k_panel_dma: with C the unit's stores precede the deferred load of its last
+  // stage; without C the chains are stored (nontemporal) at the next unit's first stage.
   int fc = 0;
+  v32f acc = {};
+  Unit pu = iu;
+  auto store_p = [&](const Unit& t) {
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+      const int row = t.r0 + 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
+      const int col = 64 * wc + 32 * (r >> 4) + (lane & 31);
+      if (row < m && col < wd) __builtin_nontemporal_store(acc[r], &P[((long)t.p * m + row) * wd + col]);
+    }
+  };
   for (int cu_idx = u0; cu_idx < u1; ++cu_idx) {
-    const int r0 = (cu_idx / nct) * PR, cb = (cu_idx % nct) * LPC;
-    v32f acc = {};
+    const Unit cu = unit(cu_idx);
     float cv[32];
-    for (int cs = 0; cs < nst; ++cs) {
+    for (int cs = 0; cs < cu.nst; ++cs) {
       if (fi - fc >= 2)
         wait_vmcnt<LDPW>();
       else
         wait_vmcnt<0>();
       __builtin_amdgcn_s_barrier();
-      if (cs + 1 < nst) issue_next();
-      if (cs == 0) {
+      if (!DIRECT && cs == 0 && cu_idx > u0) {
+        store_p(pu);
+        acc = v32f{};
+      }
+      if (!DIRECT || cs + 1 < cu.nst) issue_next();
+      if (DIRECT && cs == 0) {
 #pragma unroll
         for (int r = 0; r < 32; ++r) {
-          const int row = min(r0 + 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), m - 1);
-          const int col = min(cb + 64 * wc + 32 * (r >> 4) + (lane & 31), wd - 1);
+          const int row = min(cu.r0 + 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), m - 1);
+          const int col = min(cu.cb + 64 * wc + 32 * (r >> 4) + (lane & 31), wd - 1);
           cv[r] = C[(long)row * ldc + col];
         }
       }
@@ -447,14 +483,20 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
       }
       ++fc;
     }
+    if (DIRECT) {
 #pragma unroll
-    for (int r = 0; r < 32; ++r) {
-      const int row = r0 + 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
-      const int col = cb + 64 * wc + 32 * (r >> 4) + (lane & 31);
-      if (row < m && col < wd) C[(long)row * ldc + col] = __builtin_fmaf(alpha, acc[r], cv[r]);
+      for (int r = 0; r < 32; ++r) {
+        const int row = cu.r0 + 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
+        const int col = cu.cb + 64 * wc + 32 * (r >> 4) + (lane & 31);
+        if (row < m && col < wd) C[(long)row * ldc + col] = __builtin_fmaf(alpha, acc[r], cv[r]);
+      }
+      acc = v32f{};
+      issue_next();
+    } else {
+      pu = cu;
     }
-    issue_next();
   }
+  if (!DIRECT) store_p(pu);
 }
 
 // G[r][c] = ordered fold of the panel chains (alpha 1, beta 0): C = fma(1, P_p, C) for p = 0, 1, ...
@@ -993,6 +1035,24 @@ static hipError_t dma_slots(int* out) {
   return hipSuccess;
 }
 
+// resident k_lazy_wide workgroups on the whole device (both forms use the same resources; cached
+// per process)
+static hipError_t wide_slots(int* out) {
+  static std::atomic<int> cached{0};
+  int v = cached.load(std::memory_order_relaxed);
+  if (v == 0) {
+    int dev = 0, cus = 0, per = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err == hipSuccess) err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_lazy_wide<true>, 512, 0);
+    if (err != hipSuccess) return err;
+    v = std::max(1, cus * std::max(1, per));
+    cached.store(v, std::memory_order_relaxed);
+  }
+  *out = v;
+  return hipSuccess;
+}
+
 hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long lda, const float* B, long ldb,
                       float* P, const int* rtiles, int ntiles) {
   if (m <= 0 || wd <= 0 || k <= 0) return hipSuccess;
@@ -1019,6 +1079,17 @@ hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long
   const int grid = (int)std::min<long>(nunits, sl.load(std::memory_order_relaxed));
   const bool dma = vec4 && k % DSK == 0 && wd % 4 == 0 && wd >= 4 && ldb % 4 == 0 && (uintptr_t)B % 16 == 0;
   if (dma) {
+    if (wd == LPC) {  // 128-column gradients of tall enough matrices: one E tile read per unit
+      int ws = 0;
+      const hipError_t e2 = wide_slots(&ws);
+      if (e2 != hipSuccess) return e2;
+      const long wunits = (long)ntiles * ((k + CDCLQ_KC - 1) / CDCLQ_KC);
+      if (wunits >= 4L * ws) {
+        hipLaunchKernelGGL(k_lazy_wide<false>, dim3(ws), dim3(512), 0, st, m, wd, k, A, lda, B, ldb, (float*)nullptr,
+                           0L, 0.0f, (int)wunits, P, rtiles);
+        return hipGetLastError();
+      }
+    }
     int dslots = 0;
     const hipError_t err = dma_slots(&dslots);
     if (err != hipSuccess) return err;
@@ -1043,20 +1114,13 @@ bool chain_gemm_mfma_ok(int m, int n, int k, const float* A, long lda, const flo
 hipError_t chain_gemm_mfma(hipStream_t st, int m, int n, int k, float alpha, int beta_one, const float* A, long lda,
                            const float* B, long ldb, float* C, long ldc) {
   if (!chain_gemm_mfma_ok(m, n, k, A, lda, B, ldb)) return hipErrorInvalidValue;
-  static std::atomic<int> wide_slots{0};  // resident k_lazy_wide workgroups (cached per process)
-  int ws = wide_slots.load(std::memory_order_relaxed);
-  if (ws == 0) {
-    int dev = 0, cus = 0, per = 0;
-    hipError_t e2 = hipGetDevice(&dev);
-    if (e2 == hipSuccess) e2 = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e2 == hipSuccess) e2 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_lazy_wide, 512, 0);
-    if (e2 != hipSuccess) return e2;
-    ws = std::max(1, cus * std::max(1, per));
-    wide_slots.store(ws, std::memory_order_relaxed);
-  }
+  int ws = 0;
+  const hipError_t e2 = wide_slots(&ws);
+  if (e2 != hipSuccess) return e2;
   const long wunits = (long)((m + PR - 1) / PR) * ((n + LPC - 1) / LPC);
   if (beta_one && wunits >= ws && wunits <= INT32_MAX) {
-    hipLaunchKernelGGL(k_lazy_wide, dim3(ws), dim3(512), 0, st, m, n, k, A, lda, B, ldb, C, ldc, alpha, (int)wunits);
+    hipLaunchKernelGGL(k_lazy_wide<true>, dim3(ws), dim3(512), 0, st, m, n, k, A, lda, B, ldb, C, ldc, alpha,
+                       (int)wunits, (float*)nullptr, (const int*)nullptr);
     return hipGetLastError();
   }
   int dslots = 0;
