@@ -202,10 +202,10 @@ def test_quantize_refit_row_tilings(ctx, d_out):
 
 def test_quantize_wide_gradient_tiles(ctx):
     """128-column repair gradients with at least four (row tile, panel) units per CU take the
-    128 x 128 / 8-wave tile (one E tile read per unit): 131150 rows x 256 columns is 1025 row
-    tiles (ragged last) of one panel; later passes, with fewer active tiles, fall back to the
-    128 x 64 tiles within the same run."""
-    w, x, h, _ = synth_layer(47, 131150, 256, 1024)
+    128 x 128 / 8-wave tile (one E tile read per unit): 131150 rows x 768 columns is 1025 row
+    tiles (ragged last) x 3 panels, and the passes after the first run it over the active
+    tiles' list (or fall back to the 128 x 64 tiles when too few remain)."""
+    w, x, h, _ = synth_layer(47, 131150, 768, 2048)
     assert_same(*run_both(ctx, w, h, bits=4, group=128, block=128, act_order=True, passes=3, row_chunk=64),
                 label="wide gradient tiles")
 
