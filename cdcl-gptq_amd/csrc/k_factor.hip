@@ -138,11 +138,16 @@ __global__ __launch_bounds__(DGT) void k_chol_diag(int n, double* __restrict__ a
 
 // Panel solve X L_kk^T = A_panel for all rows below the block (src/linalg.rs:233-241). One wave
 // advances PANEL_RPW rows together (columns over lanes), so the LDS reads of L and the long
-// divisions of the rows overlap.
+// divisions of the rows overlap. The strict lower part of L is staged transposed with zeros on
+// and above the diagonal (the diagonal separately), so step t applies x_t to every lane without
+// predication: lanes at or before t, already final, take -x_t * 0 into a copy that is no longer
+// read; each final value is kept in f0 / f1 when its step comes. Columns 0..63 (held in s0) and
+// 64.. (s1) run as two loops, so the lane holding column t is known without a select.
 constexpr int PANEL_RPW = 4;  // rows per wave
 __global__ __launch_bounds__(256) void k_chol_panel(int n, double* __restrict__ a, int k, int kb,
                                                     const int* status) {
-  __shared__ double LT[NBC][NBC + 1];  // LT[t][j] = L[j][t]
+  __shared__ double LT[NBC][NBC + 1];  // LT[t][j] = L[j][t] for t < j < kb, else 0
+  __shared__ double dg[NBC];           // L[t][t]
   if (*status) return;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   {  // stage the block with all of a thread's loads in flight at once
@@ -157,31 +162,43 @@ __global__ __launch_bounds__(256) void k_chol_panel(int n, double* __restrict__ 
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       const int e = tid + 256 * q, j = e / NBC, t = e % NBC;
-      LT[t][j] = (t <= j && j < kb) ? v[q] : 0.0;
+      LT[t][j] = (t < j && j < kb) ? v[q] : 0.0;
+      if (t == j) dg[t] = v[q];
     }
   }
   __syncthreads();
   const int kend = k + kb;
   const int i0 = kend + (blockIdx.x * 4 + wv) * PANEL_RPW;
-  double s0[PANEL_RPW], s1[PANEL_RPW];
+  double s0[PANEL_RPW], s1[PANEL_RPW], f0[PANEL_RPW], f1[PANEL_RPW];
 #pragma unroll
   for (int q = 0; q < PANEL_RPW; ++q) {
     const int i = min(i0 + q, n - 1);  // rows past the end are computed but never stored
     const double* row = a + (long)i * n + k;
     s0[q] = (lane < kb) ? row[lane] : 0.0;
     s1[q] = (lane + 64 < kb) ? row[lane + 64] : 0.0;
+    f0[q] = 0.0;
+    f1[q] = 0.0;
   }
-  for (int t = 0; t < kb; ++t) {
-    const double ltt = LT[t][t];
+  const int kb0 = min(kb, 64);
+  for (int t = 0; t < kb0; ++t) {  // column t in s0 (lane t)
+    const double ltt = dg[t];
     const double l0 = LT[t][lane], l1 = (lane + 64 < NBC) ? LT[t][lane + 64] : 0.0;
 #pragma unroll
     for (int q = 0; q < PANEL_RPW; ++q) {
-      const double st = (t < 64) ? readlane_f64(s0[q], t) : readlane_f64(s1[q], t - 64);
-      const double xt = st / ltt;
-      if (lane == t) s0[q] = xt;
-      if (lane + 64 == t) s1[q] = xt;
-      if (lane > t && lane < kb) s0[q] = s0[q] - xt * l0;
-      if (lane + 64 > t && lane + 64 < kb) s1[q] = s1[q] - xt * l1;
+      const double xt = readlane_f64(s0[q], t) / ltt;
+      f0[q] = (lane == t) ? xt : f0[q];
+      s0[q] = s0[q] - xt * l0;
+      s1[q] = s1[q] - xt * l1;
+    }
+  }
+  for (int t = 64; t < kb; ++t) {  // column t in s1 (lane t - 64); columns 0..63 are final
+    const double ltt = dg[t];
+    const double l1 = (lane + 64 < NBC) ? LT[t][lane + 64] : 0.0;
+#pragma unroll
+    for (int q = 0; q < PANEL_RPW; ++q) {
+      const double xt = readlane_f64(s1[q], t - 64) / ltt;
+      f1[q] = (lane + 64 == t) ? xt : f1[q];
+      s1[q] = s1[q] - xt * l1;
     }
   }
 #pragma unroll
@@ -189,8 +206,8 @@ __global__ __launch_bounds__(256) void k_chol_panel(int n, double* __restrict__ 
     const int i = i0 + q;
     if (i >= n) break;
     double* row = a + (long)i * n + k;
-    if (lane < kb) row[lane] = s0[q];
-    if (lane + 64 < kb) row[lane + 64] = s1[q];
+    if (lane < kb) row[lane] = f0[q];
+    if (lane + 64 < kb) row[lane + 64] = f1[q];
   }
 }
 
