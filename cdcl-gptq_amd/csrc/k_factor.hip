@@ -68,7 +68,7 @@ constexpr int DGT = DGR * DGR;  // threads
 __global__ __launch_bounds__(DGT) void k_chol_diag(int n, double* __restrict__ a, int k, int kb, int* status,
                                                    double* pivot) {
   __shared__ double pre[NBC];  // column t with all earlier columns applied, before the division
-  __shared__ double col[NBC];  // column t of L
+  __shared__ double col[NBC];  // column t of L (zero above row t)
   if (*status) return;
   const int tid = threadIdx.x, tr = tid / DGR, tc = tid % DGR;
   const int wrow_max = (64 / DGR) * ((tid >> 6) + 1) - 1;  // the wave's largest tr
@@ -86,10 +86,14 @@ __global__ __launch_bounds__(DGT) void k_chol_diag(int n, double* __restrict__ a
 #pragma unroll
     for (int c = 0; c < DS; ++c) {
       const int i = DGR * r + tr, j = DGR * c + tc;
-      if (!(i < kb && j <= i)) v[r][c] = 0.0;
       if (j == 0 && i < kb) pre[i] = v[r][c];
     }
+  if (tid < NBC) col[tid] = 0.0;
   __syncthreads();
+  // Column t is final once divided: it goes to a from the LDS copy, and the registers of columns
+  // <= t (and of the upper triangle) are not read again. So every slot still in the trailing
+  // square takes v - l_it l_jt without a predicate; only slots of the lower triangle with
+  // j > t are ever read later, and those see exactly the reference's subtraction sequence.
   for (int t = 0; t < kb; ++t) {
     const double d = pre[t];  // every thread reads the same pivot: the branch below is uniform
     if (!(d > 0.0) || !isfinite(d)) {
@@ -102,7 +106,9 @@ __global__ __launch_bounds__(DGT) void k_chol_diag(int n, double* __restrict__ a
     const double ltt = sqrt(d);
     if (tid == t) col[t] = ltt;
     if (tid > t && tid < kb) col[tid] = pre[tid] / ltt;
+    if (tid == t - 1) col[t - 1] = 0.0;  // rows above t: zero (col held column t - 1 there)
     __syncthreads();
+    if (tid >= t && tid < kb) a[(long)(k + tid) * n + k + t] = col[tid];
     double ci[DS], cj[DS];
 #pragma unroll
     for (int q = 0; q < DS; ++q) {
@@ -115,25 +121,21 @@ __global__ __launch_bounds__(DGT) void k_chol_diag(int n, double* __restrict__ a
 #pragma unroll
       for (int c = 0; c < DS; ++c) {
         if (DGR * c + DGR - 1 < t) continue;  // all columns of this slot are finished
-        const int i = DGR * r + tr, j = DGR * c + tc;
-        if (i < kb && i >= t) {
-          if (j == t)
-            v[r][c] = ci[r];
-          else if (j > t && j <= i)
-            v[r][c] = v[r][c] - ci[r] * cj[c];
-          if (j == t + 1 && j <= i) pre[i] = v[r][c];
-        }
+        v[r][c] = v[r][c] - ci[r] * cj[c];
+      }
+    }
+    // the owners of column t + 1 publish it for the next step's pivot and divisions
+    const int jn = t + 1;
+    if (jn < kb && tc == jn % DGR) {
+      const int cn = jn / DGR;  // uniform: selects the slot without indexing registers
+#pragma unroll
+      for (int r = 0; r < DS; ++r) {
+        const int i = DGR * r + tr;
+        if (i >= jn && i < kb) pre[i] = cn == 0 ? v[r][0] : (cn == 1 ? v[r][1] : v[r][2]);
       }
     }
     __syncthreads();
   }
-#pragma unroll
-  for (int r = 0; r < DS; ++r)
-#pragma unroll
-    for (int c = 0; c < DS; ++c) {
-      const int i = DGR * r + tr, j = DGR * c + tc;
-      if (i < kb && j <= i) a[(long)(k + i) * n + k + j] = v[r][c];
-    }
 }
 
 // Panel solve X L_kk^T = A_panel for all rows below the block (src/linalg.rs:233-241). One wave
