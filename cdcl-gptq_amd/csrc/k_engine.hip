@@ -225,7 +225,10 @@ __global__ __launch_bounds__(64 * GB_ROWS) void k_gptq_block(int rows, int n, in
 #pragma unroll
       for (int s2 = s; s2 < NPL; ++s2) {
         const int c = s2 * 64 + lane;
-        if (c > i && c < cnt) x[s2] = x[s2] - e * (STAGE ? uv[s2] : urow[c]);
+        if constexpr (STAGE)  // lanes at or before column i (already quantized) and past cnt take
+          x[s2] = x[s2] - e * uv[s2];  // garbage that is never read: no predicate
+        else if (c > i && c < cnt)
+          x[s2] = x[s2] - e * urow[c];
       }
     }
   }
