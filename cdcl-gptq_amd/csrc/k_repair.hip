@@ -957,9 +957,9 @@ __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int 
         ++moves;
         const float* hrow = h32 + (long)(c0 + s * 64 + jl) * n + c0;
 #pragma unroll
-        for (int s2 = 0; s2 < NPL; ++s2) {
-          const int k = s2 * 64 + lane;
-          if (k < wd) gg[s2] = gg[s2] + de * hrow[k];
+        for (int s2 = 0; s2 < NPL; ++s2) {  // lanes past wd (never selected, never stored) take
+          const int k = s2 * 64 + lane;       // garbage: no predicate, clamped address
+          gg[s2] = gg[s2] + de * hrow[min(k, wd - 1)];
         }
         if (lane == jl) {
           mwq[s] = nd;
