@@ -330,7 +330,17 @@ __global__ __launch_bounds__(256) void k_combine(int m, int n, int np, T alpha, 
   const int i = (int)(idx / n), j = (int)(idx % n);
   T* c = C + (long)i * rsc + (long)j * csc;
   T cv = beta_one ? *c : T(0);
-  for (int p = 0; p < np; ++p) cv = fma_t(alpha, P[((long)p * m + i) * n + j], cv);
+  const T* src = P + (long)i * n + j;
+  const long ps = (long)m * n;
+  int p = 0;
+  for (; p + 8 <= np; p += 8) {  // 8 panel loads in flight, folded in order
+    T v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[(long)(p + u) * ps];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) cv = fma_t(alpha, v[u], cv);
+  }
+  for (; p < np; ++p) cv = fma_t(alpha, src[(long)p * ps], cv);
   *c = cv;
 }
 
