@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import ctypes as C
 import enum
+import itertools
 import os
 from dataclasses import dataclass, field
 
@@ -282,6 +283,7 @@ class Context:
             raise CdclqError(rc, f"cdclq_ctx_create(device={device}) failed (no usable GPU?)")
         self.ptr = p
         self.device = device
+        self.cache_owner = None  # token of the PrepCache whose entry the context's factor cache holds
 
     def close(self):
         if getattr(self, "ptr", None) and _lib is not None:
@@ -296,6 +298,7 @@ class Context:
 
     def clear_cache(self):
         self.check(lib().cdclq_ctx_clear_cache(self.ptr))
+        self.cache_owner = None
 
     # ---- timing
     def set_timing(self, on: bool):
@@ -315,10 +318,23 @@ class Context:
 
 class PrepCache:
     """engine::PrepCache handle: callers create it empty and pass it to every quantize_layer call
-    (src/engine.rs:220-223). It owns the GPU context holding the cached factorisation."""
+    (src/engine.rs:220-223). The factorisation itself lives in the context's one-entry cache; a
+    context shared by several PrepCache objects serves each of them as its own cache: the entry
+    belongs to the cache that filled it, and a call through another cache drops it first. So a new
+    PrepCache is always empty, like `None` in the reference, even when it reuses a context."""
+
+    _tokens = itertools.count(1)
 
     def __init__(self, device: int = 0, ctx: Context | None = None):
         self.ctx = ctx or Context(device)
+        self.token = next(PrepCache._tokens)
+
+    def claim(self) -> Context:
+        """The context, with its cache entry dropped unless this cache filled it."""
+        if self.ctx.cache_owner != self.token:
+            self.ctx.clear_cache()
+            self.ctx.cache_owner = self.token
+        return self.ctx
 
 
 class DeviceArray:
@@ -382,7 +398,7 @@ def quantize_layer(w, d_out: int, d_in: int, h, m, hkey: str, cfg: Config, cache
     h = _f32(h).reshape(d_in, d_in)
     if m is not None:
         m = _f32(m).reshape(d_in, d_in)
-    ctx = cache.ctx
+    ctx = cache.claim()
     n = d_in
     g = effective_group(cfg, n)
     ng = (n + g - 1) // g

@@ -515,7 +515,15 @@ bool st_open(const std::string& path, StFile& f, std::string& err) {
         return false;
       }
       st.shape.push_back((size_t)x);
-      numel *= (size_t)x;
+      if (__builtin_mul_overflow(numel, (size_t)x, &numel)) {  // the crate's checked_mul fold
+        err = path + ": ValidationOverflow";
+        return false;
+      }
+    }
+    size_t nbytes;
+    if (__builtin_mul_overflow(numel, (size_t)di->size, &nbytes)) {
+      err = path + ": ValidationOverflow";
+      return false;
     }
     uint64_t a, bb;
     if (!json_uint(off->arr[0], &a) || !json_uint(off->arr[1], &bb) || a > bb || bb > dlen) {
@@ -524,7 +532,7 @@ bool st_open(const std::string& path, StFile& f, std::string& err) {
     }
     st.begin = (size_t)a;
     st.end = (size_t)bb;
-    if (st.end - st.begin != numel * di->size) {
+    if (st.end - st.begin != nbytes) {
       err = path + ": TensorInvalidInfo";
       return false;
     }

@@ -205,8 +205,10 @@ void orc_find_params(const float* vals, size_t len, uint32_t bits, int mse, floa
     for (size_t i = 0; i < mb; ++i)                                                                                   \
       for (size_t j = 0; j < nb; ++j)                                                                                 \
         cv[i * NBF + j] = (beta == (T)0) ? (T)0 : beta * c[(ptrdiff_t)(i0 + i) * rsc + (ptrdiff_t)(j0 + j) * csc];    \
-    for (size_t k0 = 0; k0 < k; k0 += KC) {                                                                           \
-      size_t kc = (k - k0 < KC) ? (k - k0) : KC;                                                                      \
+    /* planted mutation 12: the f64 panel width halved */                                                             \
+    const size_t kcw = (sizeof(T) == 8 && g_mut == 12) ? KC / 2 : KC;                                                \
+    for (size_t k0 = 0; k0 < k; k0 += kcw) {                                                                          \
+      size_t kc = (k - k0 < kcw) ? (k - k0) : kcw;                                                                    \
       for (size_t kk = 0; kk < kc; ++kk) {                                                                            \
         const T* brow = b + (ptrdiff_t)(k0 + kk) * rsb + (ptrdiff_t)j0 * csb;                                         \
         T* dst = bp + kk * NBF;                                                                                       \
@@ -218,10 +220,21 @@ void orc_find_params(const float* vals, size_t len, uint32_t bits, int mse, floa
       for (size_t i = 0; i < mb; ++i) {                                                                               \
         const T* arow = a + (ptrdiff_t)(i0 + i) * rsa + (ptrdiff_t)k0 * csa;                                          \
         for (size_t j = 0; j < nb; ++j) acc[j] = (T)0;                                                                \
-        for (size_t kk = 0; kk < kc; ++kk) {                                                                          \
-          const T av = arow[(ptrdiff_t)kk * csa];                                                                     \
-          const T* bk = bp + kk * NBF;                                                                                \
-          for (size_t j = 0; j < nb; ++j) acc[j] = FMA(av, bk[j], acc[j]);                                           \
+        if (g_mut == 11) { /* planted mutation 11: every product rounded before it is added */                       \
+          for (size_t kk = 0; kk < kc; ++kk) {                                                                        \
+            const T av = arow[(ptrdiff_t)kk * csa];                                                                   \
+            const T* bk = bp + kk * NBF;                                                                              \
+            for (size_t j = 0; j < nb; ++j) {                                                                         \
+              const T p = av * bk[j];                                                                                 \
+              acc[j] = acc[j] + p;                                                                                    \
+            }                                                                                                         \
+          }                                                                                                           \
+        } else {                                                                                                      \
+          for (size_t kk = 0; kk < kc; ++kk) {                                                                        \
+            const T av = arow[(ptrdiff_t)kk * csa];                                                                   \
+            const T* bk = bp + kk * NBF;                                                                              \
+            for (size_t j = 0; j < nb; ++j) acc[j] = FMA(av, bk[j], acc[j]);                                         \
+          }                                                                                                           \
         }                                                                                                             \
         T* cr = cv + i * NBF;                                                                                         \
         for (size_t j = 0; j < nb; ++j) cr[j] = FMA(alpha, acc[j], cr[j]);                                           \

@@ -80,3 +80,66 @@ def rand_spd(n: int, seed: int) -> np.ndarray:
     h = m @ m.T
     h[np.arange(n), np.arange(n)] += 1.0
     return h
+
+
+def gemm_order_failures() -> list:
+    """Closed forms that fix matrixmultiply 0.3.8's per-element order (src/linalg.rs:3-6, :93,
+    :98-99): each KC = 256 panel is a chain of fused multiply-adds started from 0, folded into C in
+    panel order. Each case has an exact answer under that order and a different one under a
+    plausible alternative (products rounded before the add, the panel chain started from C, another
+    panel width). Returns the names of the cases that fail (empty when the order holds)."""
+    bad = []
+    # f32: (1 + 2^-12)^2 - 1 = 2^-11 + 2^-24 exactly; a rounded product loses the 2^-24 (a tie
+    # between 1 + 2^-11 and its upper neighbour, resolved to the even 1 + 2^-11).
+    e = 2.0 ** -12
+    a = np.array([[1.0, 1.0 + e]], np.float32)
+    b = np.array([[-1.0], [1.0 + e]], np.float32)
+    want = 2.0 ** -11 + 2.0 ** -24
+    if O.sgemm(a, b)[0, 0] != np.float32(want):
+        bad.append("sgemm fused chain")
+    if O.sgemm(a, b, alpha=-1.0)[0, 0] != np.float32(-want):
+        bad.append("sgemm fused chain, alpha -1")
+    c = np.full((1, 1), 2.0 ** -10, np.float32)
+    if O.sgemm(a, b, c, alpha=1.0, beta=1.0)[0, 0] != np.float32(2.0 ** -10 + want):
+        bad.append("sgemm fused chain, beta 1")
+    if O.sgemm(a, b, c, alpha=-1.0, beta=1.0)[0, 0] != np.float32(2.0 ** -10 - want):
+        bad.append("sgemm fused chain, alpha -1 beta 1")
+    # f32: the panel chain starts at 0 and is added to C once: 1 + (2^-24 + 2^-24) = 1 + 2^-23,
+    # whereas a chain started from C = 1 stays at 1 (each 1 + 2^-24 ties to the even 1).
+    a2 = np.full((1, 2), 2.0 ** -24, np.float32)
+    b2 = np.ones((2, 1), np.float32)
+    if O.sgemm(a2, b2, np.ones((1, 1), np.float32), beta=1.0)[0, 0] != np.float32(1.0 + 2.0 ** -23):
+        bad.append("sgemm chain from zero, beta 1")
+    # f64 analogue of the fused chain: (1 + 2^-27)^2 - 1 = 2^-26 + 2^-54; the rounded product is
+    # 1 + 2^-26 (2^-54 is a quarter of an ulp of 1).
+    e = 2.0 ** -27
+    a = np.array([[1.0, 1.0 + e]])
+    b = np.array([[-1.0], [1.0 + e]])
+    want = 2.0 ** -26 + 2.0 ** -54
+    if O.dgemm(a, b)[0, 0] != want:
+        bad.append("dgemm fused chain")
+    if O.dgemm(a, b, alpha=-1.0)[0, 0] != -want:
+        bad.append("dgemm fused chain, alpha -1")
+    c = np.full((1, 1), 2.0 ** -25)
+    if O.dgemm(a, b, c, alpha=1.0, beta=1.0)[0, 0] != 2.0 ** -25 + want:
+        bad.append("dgemm fused chain, beta 1")
+    if O.dgemm(a, b, c, alpha=-1.0, beta=1.0)[0, 0] != 2.0 ** -25 - want:
+        bad.append("dgemm fused chain, alpha -1 beta 1")
+    # f64 panel width: a[0] b[0] = 2^27 * 2^26 = 2^53, after which every +1 inside the panel ties
+    # back to 2^53, while each later panel adds its exact count of ones.
+    for k in (256, 258, 600, 1024):
+        a = np.ones((1, k))
+        b = np.ones((k, 1))
+        a[0, 0] = 2.0 ** 27
+        b[0, 0] = 2.0 ** 26
+        full, rem = divmod(k, 256)
+        if O.dgemm(a, b)[0, 0] != 2.0 ** 53 + 256.0 * (full - 1) + rem:
+            bad.append(f"dgemm KC panels, k {k}")
+    # f32 panel width (2^12 * 2^12 = 2^24; same argument with f32 ties)
+    for k in (256, 258, 600, 1024):
+        a = np.ones((1, k), np.float32)
+        a[0, 0] = 4096.0
+        full, rem = divmod(k, 256)
+        if O.sgemm(a, a.T.copy())[0, 0] != np.float32(2.0 ** 24 + 256.0 * (full - 1) + rem):
+            bad.append(f"sgemm KC panels, k {k}")
+    return bad

@@ -116,9 +116,11 @@ def test_gram_batch_matches_single_calls(ctx):
 
 
 # ---------------------------------------------------------------- U
-@pytest.mark.parametrize("n", [1, 5, 96, 150, 200, 400, 700])
+@pytest.mark.parametrize("n", [1, 5, 96, 150, 200, 400, 700, 2700])
 def test_upper_chol_bitexact(ctx, n):
-    h = rand_spd(n, n + 2)
+    """n = 2700 puts 9 to 11 KC = 256 panels into the inverse's chain GEMMs (k up to n), so the
+    ordered panel fold runs both its 8-panel loop and its remainder."""
+    h = rand_spd(n, n + 2) if n <= 700 else _spd_fast(n, n + 2)
     ug = cdclq.upper_chol_of_inverse(h, n, ctx)
     uo = O.upper_chol_of_inverse(h)
     assert np.array_equal(np.tril(ug, -1), np.zeros_like(ug))
@@ -126,6 +128,15 @@ def test_upper_chol_bitexact(ctx, n):
     rel = np.abs(ug.astype(np.float64) - uo) / np.maximum(np.abs(uo), 1e-30)
     assert rel.max() <= REL
     assert np.array_equal(ug.view(np.uint32), uo.view(np.uint32)), f"{(ug != uo).sum()} U entries differ"
+
+
+def _spd_fast(n, seed):
+    """M M^T / n + I with M n x (n + 8) from numpy's generator (rand_spd's per-draw loop is slow at
+    this size); any SPD input serves for bit parity."""
+    m = np.random.default_rng(seed).standard_normal((n, n + 8))
+    h = m @ m.T / n
+    h[np.arange(n), np.arange(n)] += 1.0
+    return h
 
 
 def test_upper_chol_fixtures_bitexact(ctx):
@@ -271,6 +282,22 @@ def test_prepcache_reuse(ctx):
     oc = O.Cache()
     assert_same(q1, s1, O.quantize_layer(w1, h, ocfg, hkey="attn", cache=oc), "first")
     assert_same(q2, s2, O.quantize_layer(w2, h, ocfg, hkey="attn", cache=oc), "reused")
+
+
+def test_fresh_prepcache_is_empty_on_a_shared_context(ctx):
+    """A new PrepCache is empty (`None` in the reference) even when it shares a context whose cache
+    holds an entry with the same key: same hkey, same n, natural order (identity perm), different H.
+    Alternating between two caches never lets one see the other's factorisation."""
+    w, _, h1, _ = synth_layer(57, 32, 128, 600)
+    _, _, h2, _ = synth_layer(58, 32, 128, 700)
+    gcfg, ocfg = cfgs(bits=4, group=32, block=64, act_order=False, row_chunk=16, passes=2)
+    want1 = O.quantize_layer(w, h1, ocfg, hkey="same")
+    want2 = O.quantize_layer(w, h2, ocfg, hkey="same")
+    c1 = cdclq.PrepCache(ctx=ctx)
+    assert_same(*cdclq.quantize_layer(w, 32, 128, h1, None, "same", gcfg, c1), want1, "first cache")
+    c2 = cdclq.PrepCache(ctx=ctx)
+    assert_same(*cdclq.quantize_layer(w, 32, 128, h2, None, "same", gcfg, c2), want2, "fresh cache, other H")
+    assert_same(*cdclq.quantize_layer(w, 32, 128, h1, None, "same", gcfg, c1), want1, "first cache again")
 
 
 def test_validation_errors_match_reference(ctx):

@@ -245,3 +245,19 @@ def test_error_texts(ctx, tmp_path):
     orig, _ = T.read_st(ck)
     deq, _ = T.read_st(tmp_path / "o4" / "dequant" / "model.safetensors")
     assert_same_tensors(deq, orig, "pass-through")
+
+
+@pytest.mark.parametrize("shape", [[2 ** 62, 4], [2 ** 62, 1], [2 ** 32, 2 ** 32, 3]])
+def test_header_shape_overflow_is_rejected(ctx, tmp_path, shape):
+    """A header whose element count (or byte count) wraps around 2^64 is refused with the
+    safetensors crate's ValidationOverflow (checked multiplies) instead of passing the size check
+    with a wrapped product of 0."""
+    hdr = json.dumps({"x.weight": {"dtype": "F32", "shape": shape, "data_offsets": [0, 0]}}).encode()
+    hdr += b" " * (-len(hdr) % 8)
+    p = tmp_path / "overflow.safetensors"
+    p.write_bytes(len(hdr).to_bytes(8, "little") + hdr)
+    m = T.MODELS[0]
+    hess = os.path.join(T.GOLDEN, m["fixture"])
+    with pytest.raises(cdclq.CdclqError) as e:
+        cdclq.quantize_model(ctx, [str(p)], [hess], tmp_path / "o", gcfg(T.cfg_kw(m)))
+    assert str(e.value).endswith(": ValidationOverflow"), str(e.value)

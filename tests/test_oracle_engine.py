@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from problems import damped, ref_problem, synth_layer
+from problems import damped, gemm_order_failures, ref_problem, synth_layer
 
 
 def cfg_small(**kw):
@@ -243,6 +243,8 @@ def _caught(mid):
         s, _ = O.find_params(v, 3, False)
         if np.float32(s) != np.float32(np.float16(s)):
             return True
+        if gemm_order_failures():
+            return True
     return False
 
 
@@ -250,6 +252,7 @@ def _caught(mid):
     (1, "sign of the in-block compensation"), (2, "U transposed in the lazy GEMM"), (3, "scale not f16-rounded"),
     (4, "sign of the CD loss delta"), (5, "one term dropped from the Cholesky update"),
     (6, "undamped phase-2 metric"), (7, "ragged last token chunk dropped"), (8, "off-by-one in the inverse"),
+    (11, "GEMM products rounded before the add (unfused chain)"), (12, "dgemm panel width 128 instead of 256"),
 ])
 def test_planted_mistakes_are_caught(mid, what):
     assert _caught(mid), what

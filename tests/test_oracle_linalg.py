@@ -3,7 +3,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from problems import rand_spd
+from problems import gemm_order_failures, rand_spd
 
 
 def test_cholesky_matches_definition():
@@ -91,6 +91,20 @@ def test_gemm_panel_structure_closed_form():
         full, rem = divmod(k, 256)
         expect = 2.0 ** 24 + 256.0 * (full - 1) + rem
         assert O.sgemm(a, b)[0, 0] == np.float32(expect), k
+
+
+def test_gemm_order_closed_forms():
+    """Fused chains from 0 per KC = 256 panel, folded in order, for sgemm and dgemm (alpha = +-1,
+    beta 0 and 1): the matrixmultiply 0.3.8 order that every GEMM call site of the reference relies
+    on (src/engine.rs:454,548,560,608; src/linalg.rs:254,310,326,398)."""
+    assert gemm_order_failures() == []
+
+
+@pytest.mark.parametrize("mid,case", [(11, "sgemm fused chain"), (11, "dgemm fused chain"),
+                                      (12, "dgemm KC panels, k 256")])
+def test_gemm_order_mutations_fail_the_closed_forms(mid, case):
+    with O.mutation(mid):
+        assert case in gemm_order_failures()
 
 
 def test_gram_chunks_closed_form():
