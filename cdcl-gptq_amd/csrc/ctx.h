@@ -48,6 +48,10 @@ struct cdclq_ctx {
   bool pk_layout_valid = false;  // pk_tab[0] holds the tables of this layout
   size_t pk_layout_n = 0, pk_layout_g = 0;
   std::vector<uint8_t> pk_layout_wid;
+  // device address of this GPU's fixed scratch (allocation-free Gram entry point), or null with
+  // the lookup's error
+  void* gram_scratch = nullptr;
+  hipError_t gram_scratch_err = hipSuccess;
   // timing
   bool timing = false;
   // pinned host staging of the repair loop's per-pass transfers (grows; freed with the context)

@@ -546,8 +546,11 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
 }
 
 // One launch of the matrix-core Gram kernel over several (X, Y, H) jobs (src/linalg.rs:388-418).
+// The status words and the job / tile lists live in the context's grow-only workspace, or, when
+// `fixed` is set (the allocation-free entry point), in that GPU's fixed scratch memory
+// (kGramScratchBytes: 256 B of status, 256 B for the job record, then the tiles).
 int gram_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const float* const* ys, const size_t* ts,
-                      const size_t* ns, double* const* hs) {
+                      const size_t* ns, double* const* hs, char* fixed = nullptr) {
   if (count <= 0) return CDCLQ_OK;
   if (!xs || !ys || !ts || !ns || !hs) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
   HIPCK(hipSetDevice(ctx->device));
@@ -564,13 +567,21 @@ int gram_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const f
     vec4 = vec4 && (ns[i] % 4 == 0) && ((uintptr_t)xs[i] % 16 == 0) && ((uintptr_t)ys[i] % 16 == 0);
   }
   if (jobs.empty()) return CDCLQ_OK;
+  if (fixed && (jobs.size() != 1 || 16 * (jobs.size() + 1) > 256 || sizeof(GramJob) > 256))
+    return fail(ctx, CDCLQ_INVALID_ARG, "gram_accumulate: the allocation-free path takes one accumulation");
   // Mirrored (upper-triangle-only) tiles need Y == X and a bitwise-symmetric incoming H.
-  CK(ensure(ctx, ctx->status_d, 16 * (jobs.size() + 1)));
-  HIPCK(hipMemsetAsync(ctx->status_d.p, 0, 16 * (jobs.size() + 1), st));
+  int* status;
+  if (fixed) {
+    status = reinterpret_cast<int*>(fixed);
+  } else {
+    CK(ensure(ctx, ctx->status_d, 16 * (jobs.size() + 1)));
+    status = P<int>(ctx->status_d);
+  }
+  HIPCK(zero_words(st, status, (int)(4 * (jobs.size() + 1))));
   for (size_t i = 0; i < jobs.size(); ++i)
-    if (jobs[i].x == jobs[i].y) HIPCK(sym_check(st, jobs[i].n, jobs[i].h, P<int>(ctx->status_d) + 4 * i));
+    if (jobs[i].x == jobs[i].y) HIPCK(sym_check(st, jobs[i].n, jobs[i].h, status + 4 * i));
   std::vector<int> flags(4 * jobs.size());
-  HIPCK(hipMemcpyAsync(flags.data(), ctx->status_d.p, flags.size() * 4, hipMemcpyDeviceToHost, st));
+  HIPCK(hipMemcpyAsync(flags.data(), status, flags.size() * 4, hipMemcpyDeviceToHost, st));
   HIPCK(hipStreamSynchronize(st));
   // Jobs whose tiles are all interior go to the direct-to-LDS kernel, the rest to k_gram_mfma.
   std::vector<int4> tiles[2];
@@ -593,10 +604,19 @@ int gram_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const f
     tl.swap(ord);
   }
   const size_t ntile = tiles[0].size() + tiles[1].size();
-  CK(ensure(ctx, ctx->tiles_d, ntile * sizeof(int4) + jobs.size() * sizeof(GramJob) + 64));
-  char* base = P<char>(ctx->tiles_d);
-  GramJob* djobs = reinterpret_cast<GramJob*>(base);
-  int4* dtiles = reinterpret_cast<int4*>(base + ((jobs.size() * sizeof(GramJob) + 63) / 64) * 64);
+  GramJob* djobs;
+  int4* dtiles;
+  if (fixed) {
+    if (ntile > kGramScratchTiles)
+      return fail(ctx, CDCLQ_INVALID_ARG, "gram_accumulate: tile list exceeds the allocation-free scratch");
+    djobs = reinterpret_cast<GramJob*>(fixed + 256);
+    dtiles = reinterpret_cast<int4*>(fixed + 512);
+  } else {
+    CK(ensure(ctx, ctx->tiles_d, ntile * sizeof(int4) + jobs.size() * sizeof(GramJob) + 64));
+    char* base = P<char>(ctx->tiles_d);
+    djobs = reinterpret_cast<GramJob*>(base);
+    dtiles = reinterpret_cast<int4*>(base + ((jobs.size() * sizeof(GramJob) + 63) / 64) * 64);
+  }
   HIPCK(hipMemcpyAsync(djobs, jobs.data(), jobs.size() * sizeof(GramJob), hipMemcpyHostToDevice, st));
   HIPCK(hipMemcpyAsync(dtiles, tiles[0].data(), tiles[0].size() * sizeof(int4), hipMemcpyHostToDevice, st));
   HIPCK(hipMemcpyAsync(dtiles + tiles[0].size(), tiles[1].data(), tiles[1].size() * sizeof(int4),
@@ -687,6 +707,8 @@ int cdclq_ctx_create(int device, cdclq_ctx** out) {
     delete ctx;
     return CDCLQ_DEVICE;
   }
+  // this GPU's fixed scratch of the allocation-free Gram entry point (looked up once per device)
+  ctx->gram_scratch_err = gram_scratch(device, &ctx->gram_scratch);
   *out = ctx;
   return CDCLQ_OK;
 }
@@ -774,6 +796,22 @@ int cdclq_gram_accumulate_device(cdclq_ctx* ctx, const float* x, const float* y,
   if (!ctx) return CDCLQ_INVALID_ARG;
   ctx->err.clear();
   return gram_device(ctx, x, y, t, n, h);
+}
+
+int cdclq_gram_accumulate_device_noalloc(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n,
+                                        double* h) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  if (!x || !y || !h) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+  if (n == 0 || t == 0) return CDCLQ_OK;
+  if (n > (size_t)kGramNoAllocMaxN)
+    return fail(ctx, CDCLQ_INVALID_ARG, "gram_accumulate_device_noalloc: n = " + std::to_string(n) +
+                                            " exceeds the allocation-free limit of " +
+                                            std::to_string(kGramNoAllocMaxN) + " columns");
+  if (!ctx->gram_scratch)
+    return fail(ctx, CDCLQ_DEVICE, std::string("allocation-free scratch unavailable on this device (") +
+                                       hipGetErrorString(ctx->gram_scratch_err) + ")");
+  return gram_batch_device(ctx, 1, &x, &y, &t, &n, &h, static_cast<char*>(ctx->gram_scratch));
 }
 
 int cdclq_gram_accumulate_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const float* const* ys,

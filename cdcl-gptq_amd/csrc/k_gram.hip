@@ -19,11 +19,23 @@
 // 128x128 super-tile triangle are listed and off-diagonal results are also written transposed
 // (exact: fma(a, b, c) == fma(b, a, c)); this requires the incoming H to be symmetric, which the
 // host checks.
+#include <mutex>
+
 #include "cdclq_dev.h"
 #include "kernels.h"
 
 namespace cdclq {
 namespace {
+
+// Device memory of the allocation-free entry point (cdclq_gram_accumulate_device_noalloc): the
+// symmetry status words, the job record and the tile list of one accumulation with n <= 32768.
+// Each GPU holds its own copy for the life of the process. Host code never uses this name as an
+// address (it is a host-side stand-in there): gram_scratch() looks up the device address.
+static __device__ __align__(256) unsigned char scratch[kGramScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
 
 typedef float v32f __attribute__((ext_vector_type(32)));
 typedef __attribute__((address_space(1))) const float gfloat;
@@ -290,6 +302,13 @@ __global__ __launch_bounds__(256) void k_sym_check(int n, const double* __restri
   if (a != b) atomicOr(flag, 1);
 }
 
+// A fill kernel rather than hipMemsetAsync, so the clear stays an ordinary kernel node when a
+// caller records the stream into a HIP graph.
+__global__ __launch_bounds__(256) void k_zero_words(int* __restrict__ p, int count) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < count) p[i] = 0;
+}
+
 }  // namespace
 
 void gram_mfma_tiles(int job, int n, bool sym, std::vector<int4>& out) {
@@ -327,6 +346,30 @@ hipError_t gram_dma(hipStream_t st, const GramJob* jobs, const int4* tiles, int 
 
 bool gram_dma_eligible(int n, int t, const void* x, const void* y) {
   return n % 128 == 0 && t % KT == 0 && t > 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0;
+}
+
+hipError_t gram_scratch(int device, void** ptr) {
+  *ptr = nullptr;
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (cur != device) return hipErrorInvalidDevice;  // the caller makes `device` current
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[device] = p;
+  }
+  *ptr = g_scratch_ptr[device];
+  return hipSuccess;
+}
+
+hipError_t zero_words(hipStream_t st, int* p, int count) {
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_zero_words, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st, p, count);
+  return hipGetLastError();
 }
 
 hipError_t sym_check(hipStream_t st, int n, const double* h, int* flag) {

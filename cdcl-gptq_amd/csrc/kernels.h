@@ -36,6 +36,17 @@ hipError_t gram_dma(hipStream_t st, const GramJob* jobs, const int4* tiles, int 
 bool gram_dma_eligible(int n, int t, const void* x, const void* y);
 hipError_t gram_mfma(hipStream_t st, const GramJob* jobs, const int4* tiles, int ntiles, bool vec4);
 hipError_t sym_check(hipStream_t st, int n, const double* h, int* flag);
+// p[0..count) = 0 (a kernel, not a memset node)
+hipError_t zero_words(hipStream_t st, int* p, int count);
+// Fixed device memory of the allocation-free Gram entry point: status words (256 B), the job
+// record (256 B), then the tile list of one job with n <= kGramNoAllocMaxN (non-symmetric worst
+// case: ceil(n/128) * ceil(n/64) tiles of 16 bytes).
+constexpr int kGramNoAllocMaxN = 32768;
+constexpr size_t kGramScratchTiles = (size_t)(kGramNoAllocMaxN / 128) * (kGramNoAllocMaxN / 64);
+constexpr size_t kGramScratchBytes = 512 + kGramScratchTiles * 16;
+// Device address of this GPU's copy of that memory; `device` must be the current device. Looked
+// up once per device (hipGetSymbolAddress) and kept for the life of the process.
+hipError_t gram_scratch(int device, void** ptr);
 
 // ---- k_factor.hip: damping, Cholesky, triangular inverse, U
 hipError_t build_flipped(hipStream_t st, int n, const float* h, const uint32_t* perm, double damp_val, double* a,

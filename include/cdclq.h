@@ -120,6 +120,15 @@ int cdclq_quantize_layer_device(cdclq_ctx* ctx, const float* w, size_t d_out, si
  * t x n f32. y == x selects the symmetric Hessian path. */
 int cdclq_gram_accumulate(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h);
 int cdclq_gram_accumulate_device(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h);
+/* Allocation-free variant of cdclq_gram_accumulate_device, with no counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph capture, calibration hooks
+ * in a tight forward loop, harnesses that forbid hipMalloc). Same arguments, same result bit for
+ * bit. It calls no hipMalloc / hipFree: its status words and tile list live in a fixed array of
+ * about 2 MiB per GPU, held until the process ends. Limit: n <= 32768 (larger n returns
+ * CDCLQ_INVALID_ARG before any device work). Every call on a GPU shares that GPU's array, so calls
+ * that overlap on one GPU (several contexts or threads at once) race; calls in sequence do not. */
+int cdclq_gram_accumulate_device_noalloc(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n,
+                                        double* h);
 /* `count` independent accumulations in one launch (device pointers): hs[i] += xs[i]^T ys[i] with
  * ts[i] tokens of width ns[i]. Each result equals a separate gram_accumulate call; batching only
  * lets the inputs of one decoder layer (q/k/v, o, gate/up, down) share the GPU. The reference's
