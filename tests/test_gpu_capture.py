@@ -156,11 +156,11 @@ def test_capture_matches_a_float64_restatement(ctx, tmp_path):
 
 def test_split_passes_equal_one_pass(ctx, tmp_path):
     """scripts/capture_hessians.py:40-45: a split Hessian is bit-identical to a single-pass one."""
-    from cdclq.capture import capture_hessians, accumulator_bytes
+    from cdclq.capture import capture_hessians, plan_entry_bytes
     model = tiny_llama(1)
     samples = torch.randint(0, 128, (4, 40), generator=torch.Generator().manual_seed(2))
     one = capture_hessians(model, samples, str(tmp_path / "one.safetensors"), ctx=ctx, batch=2)
-    budget = (accumulator_bytes(96) + accumulator_bytes(64)) / (1 << 30)
+    budget = (plan_entry_bytes(96) + plan_entry_bytes(64)) / (1 << 30)
     many = capture_hessians(model, samples, str(tmp_path / "split.safetensors"), ctx=ctx, batch=2,
                             max_hessian_mem=budget)
     assert len(many) > 1 and all(".of" not in p and "of" in os.path.basename(p) for p in many)
