@@ -113,6 +113,10 @@ def lib() -> C.CDLL:
         "cdclq_gram_accumulate": ([vp, vp, vp, sz, sz, vp], i32),
         "cdclq_gram_accumulate_device": ([vp, vp, vp, sz, sz, vp], i32),
         "cdclq_gram_accumulate_device_noalloc": ([vp, vp, vp, sz, sz, vp], i32),
+        "cdclq_sgemm_device": ([vp, sz, sz, sz, C.c_float, vp, C.c_ssize_t, C.c_ssize_t, vp, C.c_ssize_t,
+                                C.c_ssize_t, C.c_float, vp, C.c_ssize_t, C.c_ssize_t], i32),
+        "cdclq_dgemm_device": ([vp, sz, sz, sz, C.c_double, vp, C.c_ssize_t, C.c_ssize_t, vp, C.c_ssize_t,
+                                C.c_ssize_t, C.c_double, vp, C.c_ssize_t, C.c_ssize_t], i32),
         "cdclq_gram_accumulate_batch_device": ([vp, i32, C.POINTER(vp), C.POINTER(vp), C.POINTER(sz), C.POINTER(sz),
                                                 C.POINTER(vp)], i32),
         "cdclq_upper_chol_of_inverse": ([vp, vp, sz, vp], i32),
@@ -166,7 +170,8 @@ def exported_symbols() -> list[str]:
         "cdclq_abi_version", "cdclq_sizeof_config", "cdclq_sizeof_stats", "cdclq_default_config",
         "cdclq_num_groups", "cdclq_ctx_create", "cdclq_ctx_destroy", "cdclq_last_error", "cdclq_ctx_clear_cache",
         "cdclq_quantize_layer", "cdclq_quantize_layer_device", "cdclq_gram_accumulate",
-        "cdclq_gram_accumulate_device", "cdclq_gram_accumulate_device_noalloc", "cdclq_gram_accumulate_batch_device", "cdclq_upper_chol_of_inverse", "cdclq_upper_chol_of_inverse_device",
+        "cdclq_gram_accumulate_device", "cdclq_gram_accumulate_device_noalloc", "cdclq_gram_accumulate_batch_device",
+        "cdclq_sgemm_device", "cdclq_dgemm_device", "cdclq_upper_chol_of_inverse", "cdclq_upper_chol_of_inverse_device",
         "cdclq_proxy_loss", "cdclq_device_alloc", "cdclq_device_free", "cdclq_memcpy_h2d", "cdclq_memcpy_d2h",
         "cdclq_memset_device", "cdclq_synth_normal_device", "cdclq_synth_outlier_scales", "cdclq_synth_tokens_device", "cdclq_f64_to_f32_device",
         "cdclq_ctx_set_timing", "cdclq_ctx_reset_timing", "cdclq_ctx_get_timing",

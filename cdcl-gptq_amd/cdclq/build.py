@@ -26,7 +26,7 @@ OBJDIR = os.path.join(ROOT, "_build")
 LIB = os.path.join(PKG, "libcdclq_hip.so")
 ARCH = os.environ.get("CDCLQ_ARCH", "gfx950")
 
-SOURCES = ["k_gemm.hip", "k_gram.hip", "k_factor.hip", "k_engine.hip", "k_repair.hip", "k_pack.hip", "k_eval.hip",
+SOURCES = ["k_gemm.hip", "k_gemm_wide.hip", "k_gram.hip", "k_factor.hip", "k_engine.hip", "k_repair.hip", "k_pack.hip", "k_eval.hip",
            "engine.cpp", "container.cpp", "harness.cpp", "pipeline.cpp"]
 COMMON = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",

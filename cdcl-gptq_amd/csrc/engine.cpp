@@ -11,8 +11,10 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <cstdint>
 #include <cstring>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "cdclq.h"
@@ -304,10 +306,22 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
     CK(ensure(ctx, ctx->t2, wn * 4));
     float* mp = P<float>(ctx->mp);
     HIPCK(permute_m(st, n, m, P<uint32_t>(ctx->perm_d), (float)ctx->cache_damp, mp));
-    HIPCK(gemm_chain<float>(st, d_out, n, n, 1.0f, 0, wp, n, 1, mp, n, 1, P<float>(ctx->t1), n, 1, false, nullptr));
-    HIPCK(gemm_chain<float>(st, d_out, n, n, 1.0f, 0, P<float>(ctx->t1), n, 1, U, 1, n, P<float>(ctx->t2), n, 1, false,
-                            nullptr));
-    HIPCK(gemm_chain<float>(st, d_out, n, n, 1.0f, 0, P<float>(ctx->t2), n, 1, U, n, 1, wp, n, 1, false, nullptr));
+    float* t1 = P<float>(ctx->t1);
+    float* t2 = P<float>(ctx->t2);
+    if (chain_gemm_tiles_ok(d_out, n, n, wp, n, mp, n, t1, n)) {
+      // matrix cores, panels folded in registers; U^T staged row-major in the factorisation's f64
+      // work buffer (free once U is built), so the second GEMM reads B row by row
+      CK(ensure(ctx, ctx->a64, (size_t)n * n * 8));
+      float* ut = P<float>(ctx->a64);
+      HIPCK(transpose_f32(st, n, U, ut));
+      HIPCK(chain_gemm_tiles(st, d_out, n, n, wp, n, mp, n, t1, n, 0));
+      HIPCK(chain_gemm_tiles(st, d_out, n, n, t1, n, ut, n, t2, n, 2));  // B = U^T, zero above its diagonal
+      HIPCK(chain_gemm_tiles(st, d_out, n, n, t2, n, U, n, wp, n, 1));   // B = U, zero below its diagonal
+    } else {
+      HIPCK(gemm_chain<float>(st, d_out, n, n, 1.0f, 0, wp, n, 1, mp, n, 1, t1, n, 1, false, nullptr));
+      HIPCK(gemm_chain<float>(st, d_out, n, n, 1.0f, 0, t1, n, 1, U, 1, n, t2, n, 1, false, nullptr));
+      HIPCK(gemm_chain<float>(st, d_out, n, n, 1.0f, 0, t2, n, 1, U, n, 1, wp, n, 1, false, nullptr));
+    }
   }
   HIPCK(hipStreamSynchronize(st));
   const double secs_prepare = now_secs() - t0;
@@ -630,6 +644,38 @@ int gram_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const f
   return CDCLQ_OK;
 }
 
+// linalg::sgemm / dgemm and pgemm_f32 / pgemm_f64 (src/linalg.rs:56-184) on device memory: C = alpha A B
+// + beta C with arbitrary strides, in matrixmultiply's per-element order. Row-major f32 products
+// with alpha 1 and beta 0 (the shape of the asymmetric target) run on the matrix cores, panels
+// folded in registers; the rest on the chain GEMMs (panels split over workgroups when k spans
+// several, then folded in order).
+template <typename T>
+int gemm_device(cdclq_ctx* ctx, size_t m, size_t k, size_t n, T alpha, const T* a, ptrdiff_t rsa, ptrdiff_t csa,
+                const T* b, ptrdiff_t rsb, ptrdiff_t csb, T beta, T* c, ptrdiff_t rsc, ptrdiff_t csc) {
+  if (m == 0 || n == 0) return CDCLQ_OK;
+  if (!c || (k > 0 && (!a || !b))) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+  if (m > (size_t)INT32_MAX / 2 || n > (size_t)INT32_MAX / 2 || k > (size_t)INT32_MAX / 2)
+    return fail(ctx, CDCLQ_INVALID_ARG, "gemm: m, k and n must be below 2^30 in this build");
+  HIPCK(hipSetDevice(ctx->device));
+  const int mi = (int)m, ki = (int)k, ni = (int)n;
+  if constexpr (std::is_same<T, float>::value) {
+    if (alpha == 1.0f && beta == 0.0f && csa == 1 && csb == 1 && csc == 1 &&
+        chain_gemm_tiles_ok(mi, ni, ki, a, rsa, b, rsb, c, rsc)) {
+      HIPCK(chain_gemm_tiles(ctx->st, mi, ni, ki, a, rsa, b, rsb, c, rsc, 0));
+      HIPCK(hipStreamSynchronize(ctx->st));
+      return CDCLQ_OK;
+    }
+  }
+  T* part = nullptr;
+  if (k > (size_t)CDCLQ_KC) {
+    CK(ensure(ctx, ctx->gemm_part, gemm_partials_elems(mi, ni, ki) * sizeof(T)));
+    part = P<T>(ctx->gemm_part);
+  }
+  HIPCK(gemm_chain<T>(ctx->st, mi, ni, ki, alpha, beta, a, rsa, csa, b, rsb, csb, c, rsc, csc, false, part));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
 int gram_device(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h) {
   if (!x || !y || !h) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
   return gram_batch_device(ctx, 1, &x, &y, &t, &n, &h);
@@ -723,7 +769,7 @@ void cdclq_ctx_destroy(cdclq_ctx* ctx) {
                     &ctx->gbits_d, &ctx->perm_d, &ctx->deadp_d, &ctx->dead_d, &ctx->diag_d, &ctx->colsq_d,
                     &ctx->invd, &ctx->colloss_d, &ctx->G, &ctx->part, &ctx->rlog, &ctx->rcnt, &ctx->clog, &ctx->ccnt, &ctx->rtiles_d,
                     &ctx->sel_d, &ctx->ld_d, &ctx->mp, &ctx->t1, &ctx->t2, &ctx->a64, &ctx->y64,
-                    &ctx->tbuf, &ctx->tpart, &ctx->status_d, &ctx->tiles_d, &ctx->proxy_p, &ctx->cs_d,
+                    &ctx->tbuf, &ctx->tpart, &ctx->status_d, &ctx->tiles_d, &ctx->proxy_p, &ctx->cs_d, &ctx->gemm_part,
                     &ctx->cache_u, &ctx->cache_h32, &ctx->pk_flag};
   for (DevBuf* b : bufs) free_buf(*b);
   for (DevBuf& b : ctx->pk_in) free_buf(b);
@@ -812,6 +858,22 @@ int cdclq_gram_accumulate_device_noalloc(cdclq_ctx* ctx, const float* x, const f
     return fail(ctx, CDCLQ_DEVICE, std::string("allocation-free scratch unavailable on this device (") +
                                        hipGetErrorString(ctx->gram_scratch_err) + ")");
   return gram_batch_device(ctx, 1, &x, &y, &t, &n, &h, static_cast<char*>(ctx->gram_scratch));
+}
+
+int cdclq_sgemm_device(cdclq_ctx* ctx, size_t m, size_t k, size_t n, float alpha, const float* a, ptrdiff_t rsa,
+                       ptrdiff_t csa, const float* b, ptrdiff_t rsb, ptrdiff_t csb, float beta, float* c, ptrdiff_t rsc,
+                       ptrdiff_t csc) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  return gemm_device<float>(ctx, m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc);
+}
+
+int cdclq_dgemm_device(cdclq_ctx* ctx, size_t m, size_t k, size_t n, double alpha, const double* a, ptrdiff_t rsa,
+                       ptrdiff_t csa, const double* b, ptrdiff_t rsb, ptrdiff_t csb, double beta, double* c,
+                       ptrdiff_t rsc, ptrdiff_t csc) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  return gemm_device<double>(ctx, m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc);
 }
 
 int cdclq_gram_accumulate_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const float* const* ys,

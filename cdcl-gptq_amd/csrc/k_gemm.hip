@@ -29,7 +29,7 @@ __device__ __forceinline__ double fma_t(double a, double b, double c) { return _
 // only of such products folds to +0, so the tile starts its k loop at its first column (rounded
 // down to a stage, which keeps the panel ends on stage ends) with identical results.
 template <typename T, bool SPLIT, bool LOWER>
-__global__ __launch_bounds__(256) void k_gemm(int m, int n, int k, T alpha, int beta_one, const T* __restrict__ A,
+__global__ __launch_bounds__(256) void k_gemm(int m, int n, int k, T alpha, T beta, const T* __restrict__ A,
                                               long rsa, long csa, const T* __restrict__ B, long rsb, long csb,
                                               T* __restrict__ C, long rsc, long csc, T* __restrict__ P, int b_tri) {
   __shared__ T As[KT][BM + 4];
@@ -52,13 +52,13 @@ __global__ __launch_bounds__(256) void k_gemm(int m, int n, int k, T alpha, int 
       acc[a][b] = T(0);
       cv[a][b] = T(0);
     }
-  if (!SPLIT && beta_one) {
+  if (!SPLIT && beta != T(0)) {  // C' = beta * C (C is not read when beta == 0)
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const int gi = i0 + ty * 4 + a, gj = j0 + tx * 4 + b;
-        if (gi < m && gj < n) cv[a][b] = C[(long)gi * rsc + (long)gj * csc];
+        if (gi < m && gj < n) cv[a][b] = beta * C[(long)gi * rsc + (long)gj * csc];
       }
   }
   for (int k0 = kfirst; k0 < kend; k0 += KT) {
@@ -149,7 +149,7 @@ typedef double v2d __attribute__((ext_vector_type(2)));
 constexpr int DBM = 64, DBN = 64, DKT = 16, DPAD = 16;
 
 template <bool SPLIT, bool LOWER, int BM = DBM>
-__global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double alpha, int beta_one,
+__global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double alpha, double beta,
                                                     const double* __restrict__ A, long rsa, long csa, int amode,
                                                     const double* __restrict__ B, long rsb, long csb, int bmode,
                                                     double* __restrict__ C, long rsc, long csc, double* __restrict__ P,
@@ -252,9 +252,9 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
       for (int r = 0; r < 4; ++r) {
         acc[bi][bj][r] = 0.0;
         cv[bi][bj][r] = 0.0;
-        if (!SPLIT && beta_one) {
+        if (!SPLIT && beta != 0.0) {
           const int gi = i0 + WR * wi + 16 * bi + (lane >> 4) + 4 * r, gj = j0 + 32 * wj + 16 * bj + (lane & 15);
-          if (gi < m && gj < n) cv[bi][bj][r] = C[(long)gi * rsc + (long)gj * csc];
+          if (gi < m && gj < n) cv[bi][bj][r] = beta * C[(long)gi * rsc + (long)gj * csc];
         }
       }
   const int nst = kend > kfirst ? (kend - kfirst + DKT - 1) / DKT : 0;
@@ -323,13 +323,13 @@ inline int dmode(const double* p, long k_stride, long other_stride) {
 
 // Ordered fold of per-panel chains: C = fma(alpha, P_p, C') for p = 0, 1, ... (see file header).
 template <typename T>
-__global__ __launch_bounds__(256) void k_combine(int m, int n, int np, T alpha, int beta_one, const T* __restrict__ P,
+__global__ __launch_bounds__(256) void k_combine(int m, int n, int np, T alpha, T beta, const T* __restrict__ P,
                                                  T* __restrict__ C, long rsc, long csc) {
   const long idx = (long)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (long)m * n) return;
   const int i = (int)(idx / n), j = (int)(idx % n);
   T* c = C + (long)i * rsc + (long)j * csc;
-  T cv = beta_one ? *c : T(0);
+  T cv = beta != T(0) ? beta * *c : T(0);
   const T* src = P + (long)i * n + j;
   const long ps = (long)m * n;
   int p = 0;
@@ -352,17 +352,17 @@ size_t gemm_partials_elems(int m, int n, int k) {
 }
 
 template <typename T>
-hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, int beta_one, const T* A, long rsa, long csa,
+hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, T beta, const T* A, long rsa, long csa,
                       const T* B, long rsb, long csb, T* C, long rsc, long csc, bool lower, T* partials,
                       bool b_lower_tri) {
   // the zero-prefix skip relies on C starting at +0, i.e. beta == 0
-  const int bt = (b_lower_tri && !beta_one) ? 1 : 0;
+  const int bt = (b_lower_tri && beta == T(0)) ? 1 : 0;
   if (m <= 0 || n <= 0) return hipSuccess;
   if (k <= 0) {
-    // k == 0: C = beta * C (src/linalg.rs:82-91); beta in {0, 1}
-    if (!beta_one) {
+    // k == 0: C = beta * C, or 0 when beta == 0, untouched when beta == 1 (src/linalg.rs:79-92)
+    if (beta != T(1)) {
       hipLaunchKernelGGL((k_combine<T>), dim3((unsigned)(((long)m * n + 255) / 256)), dim3(256), 0, st, m, n, 0, alpha,
-                         0, (const T*)nullptr, C, rsc, csc);
+                         beta, (const T*)nullptr, C, rsc, csc);
     }
     return hipGetLastError();
   }
@@ -376,49 +376,49 @@ hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, int beta_one
       g3.z = np;
       if (m == 96) {  // the triangular inverse's block rows: one 96-row tile
         g3.y = 1;
-        hipLaunchKernelGGL((k_dgemm_mfma<true, false, 96>), g3, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa,
+        hipLaunchKernelGGL((k_dgemm_mfma<true, false, 96>), g3, dim3(256), 0, st, m, n, k, alpha, beta, A, rsa,
                            csa, am, B, rsb, csb, bm, C, rsc, csc, partials, bt);
       } else {
-        hipLaunchKernelGGL((k_dgemm_mfma<true, false>), g3, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa,
+        hipLaunchKernelGGL((k_dgemm_mfma<true, false>), g3, dim3(256), 0, st, m, n, k, alpha, beta, A, rsa, csa,
                            am, B, rsb, csb, bm, C, rsc, csc, partials, bt);
       }
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL((k_combine<T>), dim3((unsigned)(((long)m * n + 255) / 256)), dim3(256), 0, st, m, n, np,
-                         alpha, beta_one, (const T*)partials, C, rsc, csc);
+                         alpha, beta, (const T*)partials, C, rsc, csc);
       return hipGetLastError();
     }
     if (lower)
-      hipLaunchKernelGGL((k_dgemm_mfma<false, true>), grid, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa,
+      hipLaunchKernelGGL((k_dgemm_mfma<false, true>), grid, dim3(256), 0, st, m, n, k, alpha, beta, A, rsa, csa,
                          am, B, rsb, csb, bm, C, rsc, csc, (double*)nullptr, bt);
     else
-      hipLaunchKernelGGL((k_dgemm_mfma<false, false>), grid, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa,
+      hipLaunchKernelGGL((k_dgemm_mfma<false, false>), grid, dim3(256), 0, st, m, n, k, alpha, beta, A, rsa, csa,
                          am, B, rsb, csb, bm, C, rsc, csc, (double*)nullptr, bt);
     return hipGetLastError();
   }
   if (np > 1 && partials != nullptr && !lower) {
     dim3 g3 = grid;
     g3.z = np;
-    hipLaunchKernelGGL((k_gemm<T, true, false>), g3, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa, B, rsb,
+    hipLaunchKernelGGL((k_gemm<T, true, false>), g3, dim3(256), 0, st, m, n, k, alpha, beta, A, rsa, csa, B, rsb,
                        csb, C, rsc, csc, partials, bt);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((k_combine<T>), dim3((unsigned)(((long)m * n + 255) / 256)), dim3(256), 0, st, m, n, np, alpha,
-                       beta_one, (const T*)partials, C, rsc, csc);
+                       beta, (const T*)partials, C, rsc, csc);
     return hipGetLastError();
   }
   if (lower)
-    hipLaunchKernelGGL((k_gemm<T, false, true>), grid, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa, B,
+    hipLaunchKernelGGL((k_gemm<T, false, true>), grid, dim3(256), 0, st, m, n, k, alpha, beta, A, rsa, csa, B,
                        rsb, csb, C, rsc, csc, (T*)nullptr, bt);
   else
-    hipLaunchKernelGGL((k_gemm<T, false, false>), grid, dim3(256), 0, st, m, n, k, alpha, beta_one, A, rsa, csa, B,
+    hipLaunchKernelGGL((k_gemm<T, false, false>), grid, dim3(256), 0, st, m, n, k, alpha, beta, A, rsa, csa, B,
                        rsb, csb, C, rsc, csc, (T*)nullptr, bt);
   return hipGetLastError();
 }
 
-template hipError_t gemm_chain<float>(hipStream_t, int, int, int, float, int, const float*, long, long, const float*,
+template hipError_t gemm_chain<float>(hipStream_t, int, int, int, float, float, const float*, long, long, const float*,
                                       long, long, float*, long, long, bool, float*, bool);
-template hipError_t gemm_chain<double>(hipStream_t, int, int, int, double, int, const double*, long, long,
+template hipError_t gemm_chain<double>(hipStream_t, int, int, int, double, double, const double*, long, long,
                                        const double*, long, long, double*, long, long, bool, double*, bool);
 
 }  // namespace cdclq

@@ -11,11 +11,13 @@
 namespace cdclq {
 
 // ---- k_gemm.hip: bit-exact chain GEMMs (matrixmultiply 0.3.8 order, see k_gemm.hip)
-// C = alpha * A * B + beta * C, alpha in {+1,-1}, beta in {0,1}. `lower` computes only tiles that
-// intersect the lower triangle (i >= j) of C. When k spans several KC panels and `partials` is
-// non-null, panels run in parallel into partials[npanel][m][n] and are combined in panel order.
+// C = alpha * A * B + beta * C in the matrixmultiply order: per panel, C = fma(alpha, chain, C')
+// with C' = beta * C before the first panel (0 when beta == 0, C unread). `lower` computes only
+// tiles that intersect the lower triangle (i >= j) of C. When k spans several KC panels and
+// `partials` is non-null, panels run in parallel into partials[npanel][m][n] and are combined in
+// panel order.
 template <typename T>
-hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, int beta_one, const T* A, long rsa, long csa,
+hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, T beta, const T* A, long rsa, long csa,
                       const T* B, long rsb, long csb, T* C, long rsc, long csc, bool lower, T* partials,
                       bool b_lower_tri = false);
 size_t gemm_partials_elems(int m, int n, int k);
@@ -86,6 +88,14 @@ hipError_t fold_panels(hipStream_t st, int m, int wd, int np, const float* P, fl
 bool chain_gemm_mfma_ok(int m, int n, int k, const float* A, long lda, const float* B, long ldb);
 hipError_t chain_gemm_mfma(hipStream_t st, int m, int n, int k, float alpha, int beta_one, const float* A, long lda,
                            const float* B, long ldb, float* C, long ldc);
+// ---- k_gemm_wide.hip: multi-panel f32 chain GEMM C = A B (alpha 1, beta 0) on the matrix cores,
+// panels folded in registers (the asymmetric target's three GEMMs). tri: 0 dense B, 1 B upper
+// triangular (B[k][j] = 0 for k > j), 2 B lower triangular (B[k][j] = 0 for k < j).
+bool chain_gemm_tiles_ok(int m, int n, int k, const float* A, long lda, const float* B, long ldb, const float* C,
+                         long ldc);
+hipError_t chain_gemm_tiles(hipStream_t st, int m, int n, int k, const float* A, long lda, const float* B, long ldb,
+                            float* C, long ldc, int tri);
+hipError_t transpose_f32(hipStream_t st, int n, const float* src, float* dst);
 hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, int rc, const float* G,
                        const float* h32, const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
                        const uint8_t* active, double* dlog, uint32_t* dcnt);

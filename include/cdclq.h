@@ -153,6 +153,19 @@ int cdclq_hessian_finalize_device(cdclq_ctx* ctx, const double* acc, size_t n, u
 int cdclq_upper_chol_of_inverse(cdclq_ctx* ctx, const double* h, size_t n, float* u);
 int cdclq_upper_chol_of_inverse_device(cdclq_ctx* ctx, const double* h, size_t n, float* u);
 
+/* linalg::sgemm / dgemm (src/linalg.rs:56-99) and pgemm_f32 / pgemm_f64 (:101-184), device memory:
+ * C = alpha A B + beta C for A m x k, B k x n, C m x n with arbitrary element strides (rs* = row
+ * stride, cs* = column stride, in elements). The result is matrixmultiply 0.3.8's: per element a
+ * fused multiply-add chain over each 256-wide panel of k, started from 0 and folded in panel order,
+ * C = fma(alpha, chain, C'), with C' = beta C before the first panel (C unread when beta == 0);
+ * k == 0 gives C = beta C (0 when beta == 0). C must not alias A or B. */
+int cdclq_sgemm_device(cdclq_ctx* ctx, size_t m, size_t k, size_t n, float alpha, const float* a, ptrdiff_t rsa,
+                       ptrdiff_t csa, const float* b, ptrdiff_t rsb, ptrdiff_t csb, float beta, float* c, ptrdiff_t rsc,
+                       ptrdiff_t csc);
+int cdclq_dgemm_device(cdclq_ctx* ctx, size_t m, size_t k, size_t n, double alpha, const double* a, ptrdiff_t rsa,
+                       ptrdiff_t csa, const double* b, ptrdiff_t rsb, ptrdiff_t csb, double beta, double* c,
+                       ptrdiff_t rsc, ptrdiff_t csc);
+
 /* engine::proxy_loss (src/engine.rs:808-815): sum_rows e H e^T with e = w_t - w_hat. */
 int cdclq_proxy_loss(cdclq_ctx* ctx, const float* w_t, const float* w_hat, size_t rows, size_t n, const float* h,
                      double* out);

@@ -115,6 +115,47 @@ def test_gram_batch_matches_single_calls(ctx):
         assert np.array_equal(d.download().view(np.uint64), ho.view(np.uint64)), (t, n)
 
 
+# ---------------------------------------------------------------- sgemm / dgemm
+def _gemm_device(ctx, dt, m, k, n, alpha, a, sa, b, sb, beta, c0, sc):
+    """Runs cdclq_{s,d}gemm_device on device copies of a, b, c0 with element strides sa, sb, sc."""
+    fn = cdclq.lib().cdclq_sgemm_device if dt == np.float32 else cdclq.lib().cdclq_dgemm_device
+    da, db, dc = (cdclq.DeviceArray.from_host(ctx, np.ascontiguousarray(x, dt)) for x in (a, b, c0))
+    ctx.check(fn(ctx.ptr, m, k, n, alpha, da.ptr, sa[0], sa[1], db.ptr, sb[0], sb[1], beta, dc.ptr, sc[0], sc[1]))
+    out = dc.download()
+    for d in (da, db, dc):
+        d.free()
+    return out
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+@pytest.mark.parametrize("m,k,n,alpha,beta,ta,tb", [
+    (300, 1024, 516, 1.0, 0.0, False, False),  # f32: matrix-core tiles, 4 panels, ragged rows
+    (1, 32, 4, 1.0, 0.0, False, False),
+    (257, 288, 1028, 1.0, 0.0, False, False),  # ragged last panel (32 of 256)
+    (130, 2560, 260, 1.0, 0.0, False, False),  # 10 panels
+    (97, 700, 111, -1.0, 1.0, False, False),   # chain GEMM, split panels + ordered fold
+    (64, 300, 48, 0.5, -2.0, True, False),     # general alpha / beta, transposed A
+    (50, 513, 70, 1.0, 0.0, False, True),      # transposed B, ragged k
+    (33, 100, 17, -1.0, 0.0, True, True),
+    (20, 0, 30, 1.0, 0.5, False, False),       # k == 0: C = beta C
+])
+def test_gemm_bitexact(ctx, dt, m, k, n, alpha, beta, ta, tb):
+    """linalg::sgemm / dgemm (src/linalg.rs:56-99) through the C ABI against the oracle: the same
+    fused chains per KC = 256 panel folded in order, on every path the device dispatch takes."""
+    rng = np.random.default_rng(m * 7 + k * 3 + n)
+    a = rng.standard_normal((m, k)).astype(dt)
+    b = rng.standard_normal((k, n)).astype(dt)
+    c0 = rng.standard_normal((m, n)).astype(dt)
+    want = (O.sgemm if dt == np.float32 else O.dgemm)(a, b, c0, alpha=alpha, beta=beta)
+    # transposed operands: store the transpose and pass (row, column) strides that read it back
+    a_dev, sa = (a.T.copy(), (1, m)) if ta else (a, (k, 1))
+    b_dev, sb = (b.T.copy(), (1, k)) if tb else (b, (n, 1))
+    print(f"[parity] gemm {np.dtype(dt).name} {m}x{k}x{n} alpha={alpha} beta={beta} ta={ta} tb={tb}", flush=True)
+    got = _gemm_device(ctx, dt, m, k, n, alpha, a_dev, sa, b_dev, sb, beta, c0, (n, 1))
+    ui = np.uint32 if dt == np.float32 else np.uint64
+    assert np.array_equal(got.view(ui), want.view(ui)), f"{(got != want).sum()} of {got.size} differ"
+
+
 # ---------------------------------------------------------------- U
 @pytest.mark.parametrize("n", [1, 5, 96, 150, 200, 400, 700, 2700])
 def test_upper_chol_bitexact(ctx, n):
@@ -247,6 +288,17 @@ def test_quantize_asymmetric_target(ctx):
     m = O.gram_accumulate(x, xt).astype(np.float32)
     assert_same(*run_both(ctx, w, ht, m=m, bits=3, group=32, block=32, act_order=True, row_chunk=32, passes=3),
                 label="asym")
+
+
+def test_quantize_asymmetric_target_multi_panel(ctx):
+    """The target's three GEMMs across several KC panels on the matrix-core tiles (n = 1024: 4
+    panels; the U^T and U products start and stop at panel and tile boundaries), ragged rows."""
+    w, x, h, _ = synth_layer(46, 300, 1024, 2200)
+    xt = (x + O.synth_normal(47, x.size, 0.05).reshape(x.shape)).astype(np.float32)
+    ht = O.gram_accumulate(xt).astype(np.float32)
+    m = O.gram_accumulate(x, xt).astype(np.float32)
+    assert_same(*run_both(ctx, w, ht, m=m, bits=3, group=128, block=128, act_order=True, row_chunk=64, passes=2),
+                label="asym multi-panel")
 
 
 def test_quantize_config1_full(ctx):
