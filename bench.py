@@ -42,6 +42,44 @@ CONFIGS = {
         cfg=dict(bits=4, group=128, block=128, damp=0.01, act_order=True),
         nthreads=24,
     ),
+    # TinyLlama-1.1B-shaped decoder layer, INT3 g128, act-order, repair
+    # (reference defaults: passes 10, tol 1e-3); 0.5% Student-t(3) channels
+    "c2": dict(
+        workload="tinyllama-1.1b decoder layer (BASELINE config 2)",
+        tokens=128 * 2048,
+        inputs={"attn_in": 2048, "attn_out": 2048, "mlp_in": 2048, "mlp_act": 5632},
+        layers=[("q_proj", 2048, "attn_in"), ("k_proj", 256, "attn_in"), ("v_proj", 256, "attn_in"),
+                ("o_proj", 2048, "attn_out"), ("gate_proj", 5632, "mlp_in"), ("up_proj", 5632, "mlp_in"),
+                ("down_proj", 2048, "mlp_act")],
+        wsigma=0.02, xgen=dict(kind="heavy", frac=0.005),
+        cfg=dict(bits=3, group=128, block=128, act_order=True),
+        nthreads=24,
+    ),
+    # the same layer at INT2 g64, MSE grid, passes 8, 5% INT8 skeleton
+    # (the saliency permutation depends on W, so every matrix has its own factorisation)
+    "c3": dict(
+        workload="tinyllama-1.1b decoder layer, INT2 + 5% INT8 skeleton (BASELINE config 3)",
+        tokens=128 * 2048,
+        inputs={"attn_in": 2048, "attn_out": 2048, "mlp_in": 2048, "mlp_act": 5632},
+        layers=[("q_proj", 2048, "attn_in"), ("k_proj", 256, "attn_in"), ("v_proj", 256, "attn_in"),
+                ("o_proj", 2048, "attn_out"), ("gate_proj", 5632, "mlp_in"), ("up_proj", 5632, "mlp_in"),
+                ("down_proj", 2048, "mlp_act")],
+        wsigma=0.02, xgen=dict(kind="heavy", frac=0.005),
+        cfg=dict(bits=2, group=64, block=128, act_order=True, mse_grid=True, passes=8, skeleton_pct=5.0,
+                 skeleton_bits=8),
+        nthreads=24,
+    ),
+    # Llama-3-70B-shaped MLP, INT3 g128, passes 6, asymmetric target
+    # W* = W M H~^-1 with H~ = X~^T X~, M = X^T X~, X~ = X + N(0, 0.05^2); log-normal channel scales
+    "c5": dict(
+        workload="llama3-70b MLP (BASELINE config 5)",
+        tokens=128 * 4096,
+        inputs={"mlp_in": 8192, "mlp_act": 28672},
+        layers=[("gate_proj", 28672, "mlp_in"), ("up_proj", 28672, "mlp_in"), ("down_proj", 8192, "mlp_act")],
+        wsigma=0.01, xgen=dict(kind="lognormal", sigma=0.5), asym_noise=0.05,
+        cfg=dict(bits=3, group=128, block=128, act_order=True, passes=6),
+        nthreads=24,
+    ),
     # single 2048x2048 layer (CPU-runnable reference case)
     "c1": dict(
         workload="single 2048x2048 layer (BASELINE config 1)",
@@ -59,48 +97,185 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def input_seeds(i: int):
+    """(channel pick / scale seed, token seed, perturbation seed) of the config's i-th input."""
+    return 1000 + 7 * i, 2000 + 7 * i, 4000 + 7 * i
+
+
+def weight_seed(li: int) -> int:
+    return 3000 + li
+
+
+def channel_spec(spec: dict, i: int, n: int):
+    """(channel scales or None, Student-t channel mask or None) of input i, host arrays."""
+    import cdclq
+
+    cseed = input_seeds(i)[0]
+    xg = spec.get("xgen")
+    if xg is None:
+        return cdclq.synth_outlier_scales(cseed, n, spec["outlier_frac"], spec["outlier_factor"]), None
+    if xg["kind"] == "heavy":
+        return None, cdclq.synth_heavy_channels(cseed, n, xg["frac"])
+    if xg["kind"] == "lognormal":
+        return cdclq.synth_lognormal_scales(cseed, n, xg["sigma"]), None
+    raise ValueError(xg["kind"])
+
+
+def make_inputs(ctx, spec: dict, only=None):
+    """Token-major calibration inputs in HBM: {key: X} and, for the asymmetric target, {key: X~}.
+    `only`: a subset of the input keys (each keeps its own seeds)."""
+    import cdclq
+
+    T = spec["tokens"]
+    xs, xts = {}, {}
+    for i, (key, n) in enumerate(spec["inputs"].items()):
+        if only is not None and key not in only:
+            continue
+        cs, heavy = channel_spec(spec, i, n)
+        xs[key] = cdclq.DeviceArray(ctx, (T, n), np.float32)
+        cdclq.synth_tokens_device(ctx, input_seeds(i)[1], T, n, xs[key], ch_scale=cs, heavy=heavy)
+        if spec.get("asym_noise"):
+            xts[key] = cdclq.DeviceArray(ctx, (T, n), np.float32)
+            cdclq.synth_perturb_device(ctx, input_seeds(i)[2], xs[key], xts[key], spec["asym_noise"])
+    return xs, xts
+
+
+def gram_jobs(spec: dict, xs: dict, xts: dict, h64s: dict, m64s: dict):
+    """The layer's accumulations as (x, y, h) device triples: H = X^T X per input, or, with the
+    asymmetric target, H~ = X~^T X~ and M = X^T X~."""
+    jobs = []
+    for key in xs:
+        if xts:
+            jobs += [(xts[key], xts[key], h64s[key]), (xs[key], xts[key], m64s[key])]
+        else:
+            jobs.append((xs[key], xs[key], h64s[key]))
+    return jobs
+
+
 def gram_flops(n: int, t: int) -> float:
     """Algorithmic work of one symmetric H accumulation: n(n+1) t flops (one triangle)."""
     return float(n) * (n + 1) * t
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or platform.machine()
+
+
+def factorisations(spec: dict) -> list:
+    """Widths of the distinct factorisations of one step: one per input (the factor cache is keyed
+    by input and permutation, src/engine.rs:718), or one per matrix when the skeleton makes the
+    permutation depend on W."""
+    if spec["cfg"].get("skeleton_pct", 0.0) > 0.0:
+        return [spec["inputs"][key] for _, _, key in spec["layers"]]
+    return list(spec["inputs"].values())
+
+
+def cpu_sample(spec: dict, cores: int, n0: int, rows: int, rc: int, with_factor: bool = True):
+    """Times the oracle's quantize_layer on `rows` x n0 (chunks of rc) with a synthetic H; returns
+    (seconds of phase 1+2, seconds of the factorisation or 0, seconds of the target GEMMs or 0)."""
+    import oracle as O
+
+    cs = O.synth_outlier_scales(101, n0, 0.01, 20.0)
+    x = O.synth_tokens(102, 2048, n0, cs)
+    h = O.gram_accumulate(x).astype(np.float32)
+    w = O.synth_normal(103, rows * n0, spec["wsigma"]).reshape(rows, n0)
+    t_fac = 0.0
+    if with_factor:
+        hd = h.astype(np.float64)
+        hd[np.arange(n0), np.arange(n0)] += 0.01 * np.mean(np.diag(hd))
+        t0 = time.perf_counter()
+        O.upper_chol_of_inverse(hd)
+        t_fac = time.perf_counter() - t0
+    cfg = O.config(**{**spec["cfg"], "row_chunk": rc})
+    m = h if spec.get("asym_noise") else None
+    q = O.quantize_layer(w, h, cfg, m=m, nthreads=cores)
+    # secs_prepare holds the factorisation and (with M) the target GEMMs; the factor is timed above
+    t_target = max(0.0, q.stats["secs_prepare"] - t_fac) if m is not None else 0.0
+    return q.stats["secs_quant"], t_fac, t_target
+
+
 def cpu_baseline(spec: dict, cores: int) -> dict:
     """Time the oracle (C restatement of the reference's rayon path) on a bounded sample of the
-    workload and extrapolate to one full layer with the work scaling of each phase."""
+    workload and extrapolate to one full step with the work scaling of each phase: the Gram by
+    n^2 T per accumulation (the reference computes every entry, also of a symmetric H), the
+    factorisation by n^3, phase 1 + 2 (and the asymmetric target) by rows x n^2."""
     import oracle as O
 
     O.set_threads(cores)
-    n0 = 4096 if "attn_in" in spec["inputs"] else 2048
+    n0 = min(4096, min(spec["inputs"].values()))
     ts = 16384  # eight 2048-token chunks
-    cs = O.synth_outlier_scales(101, n0, spec["outlier_frac"], spec["outlier_factor"])
-    x = O.synth_tokens(102, ts, n0, cs)
+    x = O.synth_tokens(102, ts, n0, None)
     t0 = time.perf_counter()
-    h64 = O.gram_accumulate(x)  # reference gram computes all n^2 entries
+    O.gram_accumulate(x)
     t_gram = time.perf_counter() - t0
-    gram_full = t_gram * sum(n * n * spec["tokens"] for n in spec["inputs"].values()) / (n0 * n0 * ts)
-    h = h64.astype(np.float32)
-    hd = h.astype(np.float64)
-    hd[np.arange(n0), np.arange(n0)] += 0.01 * np.mean(np.diag(hd))
-    t0 = time.perf_counter()
-    O.upper_chol_of_inverse(hd)
-    t_fac = time.perf_counter() - t0
-    fac_full = t_fac * sum((n / n0) ** 3 for n in spec["inputs"].values())
+    T = spec["tokens"]
+    njobs = 2 if spec.get("asym_noise") else 1  # H~ and M per input with the asymmetric target
+    gram_full = t_gram * njobs * sum(n * n * T for n in spec["inputs"].values()) / (n0 * n0 * ts)
     rc = 171 if n0 == 4096 else 64
     rows = min(2 * rc * cores, 8192)  # two row chunks per thread
-    w = O.synth_normal(103, rows * n0, spec["wsigma"]).reshape(rows, n0)
-    cfg = O.config(**{**spec["cfg"], "row_chunk": rc})
-    q = O.quantize_layer(w, h, cfg, nthreads=cores)
-    t_q = q.stats["secs_quant"]
-    quant_full = 0.0
+    t_q, t_fac, t_tgt = cpu_sample(spec, cores, n0, rows, rc)
+    fac_full = t_fac * sum((n / n0) ** 3 for n in factorisations(spec))
+    quant_full = target_full = 0.0
     for (_, d_out, key) in spec["layers"]:
         n = spec["inputs"][key]
         quant_full += t_q * (d_out / rows) * (n / n0) ** 2
-    total = gram_full + fac_full + quant_full
-    sample = (f"oracle on {cores} threads: gram {ts} tokens x n={n0} ({t_gram:.2f}s, scaled by n^2*T), "
-              f"factor n={n0} ({t_fac:.2f}s, scaled by n^3), phase1+2 of {rows} rows x n={n0} in chunks of {rc} "
-              f"({t_q:.2f}s, scaled by rows and n^2); extrapolated to the full layer")
-    return {"value": round(total, 2), "unit": "s/layer", "cores": cores, "kind": "port", "sample": sample,
-            "phases_s": {"gram": round(gram_full, 2), "factor": round(fac_full, 2), "quant": round(quant_full, 2)}}
+        target_full += t_tgt * (d_out / rows) * (n / n0) ** 2
+    total = gram_full + fac_full + quant_full + target_full
+    val = recorded_cpu_validation()
+    sample = (f"oracle on {cores} threads of {cpu_model()}: gram {ts} tokens x n={n0} ({t_gram:.2f}s, scaled by "
+              f"n^2*T per accumulation), factor n={n0} ({t_fac:.2f}s, scaled by n^3), phase1+2 of {rows} rows x "
+              f"n={n0} in chunks of {rc} ({t_q:.2f}s, scaled by rows and n^2; the number of repair passes is "
+              f"data-dependent, so this is a model, not a measurement)")
+    if t_tgt:
+        sample += f", asymmetric target GEMMs ({t_tgt:.2f}s, scaled by rows and n^2)"
+    if val:
+        sample += f"; {val}"
+    return {"value": round(total, 2), "unit": "s/layer", "cores": cores, "kind": "port", "cpu": cpu_model(),
+            "sample": sample, "phases_s": {"gram": round(gram_full, 2), "factor": round(fac_full, 2),
+                                           "quant": round(quant_full, 2), "target": round(target_full, 2)}}
+
+
+def recorded_cpu_validation():
+    """The check of the rows x n^2 model against a timed down_proj-width sample, as recorded in
+    profiles/cpu_baseline_c4.md by `bench.py --cpu-validate` (None if not recorded)."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "cpu_baseline_c4.md")) as f:
+            for line in f:
+                if line.startswith("validation:"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_validate(spec: dict, cores: int):
+    """Times phase 1 + 2 of the down_proj width (n = 14336, one row chunk of 171 per thread) and
+    compares it with the rows x n^2 extrapolation from the n = 4096 sample cpu_baseline uses."""
+    import oracle as O
+
+    O.set_threads(cores)
+    n0, rc = 4096, 171
+    rows0 = min(2 * rc * cores, 8192)
+    t_q0, _, _ = cpu_sample(spec, cores, n0, rows0, rc, with_factor=False)
+    n1 = max(spec["inputs"].values())
+    rows1 = rc * cores
+    t0 = time.perf_counter()
+    t_q1, _, _ = cpu_sample(spec, cores, n1, rows1, rc, with_factor=False)
+    wall = time.perf_counter() - t0
+    predicted = t_q0 * (rows1 / rows0) * (n1 / n0) ** 2
+    line = (f"measured phase1+2 of {rows1} rows x n={n1} (chunks of {rc}) = {t_q1:.1f}s vs {predicted:.1f}s "
+            f"predicted from {rows0} rows x n={n0} ({t_q0:.1f}s): measured/predicted = {t_q1 / predicted:.2f} "
+            f"({cores} threads of {cpu_model()})")
+    print(json.dumps({"cpu_validate": line, "wall_s": round(wall, 1)}), flush=True)
 
 
 def recorded_traffic(summary: str):
@@ -118,7 +293,7 @@ def recorded_traffic(summary: str):
     return None
 
 
-def profile_gram(ctx, spec, xs, h64s):
+def profile_gram(ctx, spec, jobs):
     """One calibration copy of known size, then one batched gram launch (for rocprofv3 --pmc)."""
     import ctypes
     import cdclq
@@ -131,19 +306,25 @@ def profile_gram(ctx, spec, xs, h64s):
     rc = hip.hipMemcpy(dst.ptr, src.ptr, nbytes, 3)  # hipMemcpyDeviceToDevice: one copy kernel
     if rc != 0 or hip.hipDeviceSynchronize() != 0:
         raise RuntimeError(f"calibration copy failed ({rc})")
-    keys = list(spec["inputs"])
-    for key in keys:
-        h64s[key].zero()
+    for _, _, h in jobs:
+        h.zero()
     T = spec["tokens"]
-    cdclq.gram_accumulate_batch_device(ctx, [xs[k] for k in keys], [xs[k] for k in keys], [T] * len(keys),
-                                       [spec["inputs"][k] for k in keys], [h64s[k] for k in keys])
-    x_bytes = sum(T * n * 4 for n in spec["inputs"].values())
-    h_bytes = sum(n * n * 8 for n in spec["inputs"].values())
+    cdclq.gram_accumulate_batch_device(ctx, [j[0] for j in jobs], [j[1] for j in jobs], [T] * len(jobs),
+                                       [j[0].shape[1] for j in jobs], [j[2] for j in jobs])
+    x_bytes = sum(T * j[0].shape[1] * 4 * (1 if j[0] is j[1] else 2) for j in jobs)
+    h_bytes = sum(j[0].shape[1] ** 2 * 8 for j in jobs)
     print(json.dumps({"profile": "gram", "workload": spec["workload"], "calibration_copy_bytes": nbytes,
                       "algorithmic_read_bytes": x_bytes + h_bytes, "algorithmic_write_bytes": h_bytes}), flush=True)
 
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E (AMD published)
+
+DATA_DESC = {
+    "outlier": "synthetic (counter-based N(0,1) activations with outlier channels, N(0,s^2) weights)",
+    "heavy": "synthetic (counter-based N(0,1) activations with Student-t(3) channels, N(0,s^2) weights)",
+    "lognormal": "synthetic (counter-based N(0,1) activations with log-normal channel scales, X~ = X + N(0,0.05^2), "
+                 "N(0,s^2) weights)",
+}
 
 
 def container_layers(spec):
@@ -304,6 +485,8 @@ def main():
                          "layer's quantized matrices (cdclq-v1)")
     ap.add_argument("--profile", action="store_true",
                     help="with --workload container: counter-collection run (1 GiB copy + one step)")
+    ap.add_argument("--cpu-validate", action="store_true",
+                    help="time the CPU baseline's rows x n^2 model against a down_proj-width sample and exit")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
@@ -314,21 +497,26 @@ def main():
     import cdclq
 
     spec = CONFIGS[args.config]
+    if args.cpu_validate:
+        cpu_validate(spec, min(os.cpu_count() or 1, 16))
+        return
     if args.workload == "container":
         container_bench(args, spec)
         return
     T = spec["tokens"]
     ctx = cdclq.Context(0)
     log(f"[bench] {spec['workload']}: generating inputs in HBM")
-    xs, h64s, h32s = {}, {}, {}
-    for i, (key, n) in enumerate(spec["inputs"].items()):
-        cs = cdclq.synth_outlier_scales(1000 + 7 * i, n, spec["outlier_frac"], spec["outlier_factor"])
-        xs[key] = cdclq.DeviceArray(ctx, (T, n), np.float32)
-        ctx.check(cdclq.lib().cdclq_synth_tokens_device(ctx.ptr, 2000 + 7 * i, 0, T, n, cs.ctypes.data, xs[key].ptr))
+    xs, xts = make_inputs(ctx, spec)
+    h64s, h32s, m64s, m32s = {}, {}, {}, {}
+    for key, n in spec["inputs"].items():
         h64s[key] = cdclq.DeviceArray(ctx, (n, n), np.float64)
         h32s[key] = cdclq.DeviceArray(ctx, (n, n), np.float32)
+        if xts:
+            m64s[key] = cdclq.DeviceArray(ctx, (n, n), np.float64)
+            m32s[key] = cdclq.DeviceArray(ctx, (n, n), np.float32)
+    jobs = gram_jobs(spec, xs, xts, h64s, m64s)
     if args.profile_gram:
-        profile_gram(ctx, spec, xs, h64s)
+        profile_gram(ctx, spec, jobs)
         ctx.close()
         return
     ws, outs = {}, {}
@@ -336,7 +524,7 @@ def main():
     for li, (name, d_out, key) in enumerate(spec["layers"]):
         n = spec["inputs"][key]
         ws[name] = cdclq.DeviceArray(ctx, (d_out, n), np.float32)
-        ctx.check(cdclq.lib().cdclq_synth_normal_device(ctx.ptr, 3000 + li, 0, d_out * n, spec["wsigma"],
+        ctx.check(cdclq.lib().cdclq_synth_normal_device(ctx.ptr, weight_seed(li), 0, d_out * n, spec["wsigma"],
                                                          ws[name].ptr))
         ng = (n + cfg.group - 1) // cfg.group
         outs[name] = (cdclq.DeviceArray(ctx, (d_out, n), np.uint8), cdclq.DeviceArray(ctx, (d_out, ng), np.float32),
@@ -344,19 +532,21 @@ def main():
 
     def step():
         stats = {}
-        keys = list(spec["inputs"])
-        for key in keys:
-            h64s[key].zero()
-        # the layer's Hessians accumulate in one launch (each equals its own gram_accumulate)
-        cdclq.gram_accumulate_batch_device(ctx, [xs[k] for k in keys], [xs[k] for k in keys], [T] * len(keys),
-                                           [spec["inputs"][k] for k in keys], [h64s[k] for k in keys])
+        for _, _, h in jobs:
+            h.zero()
+        # the layer's Hessians (and cross-covariances) accumulate in one launch; each equals its own
+        # gram_accumulate
+        cdclq.gram_accumulate_batch_device(ctx, [j[0] for j in jobs], [j[1] for j in jobs], [T] * len(jobs),
+                                           [j[0].shape[1] for j in jobs], [j[2] for j in jobs])
         for key, n in spec["inputs"].items():
             ctx.check(cdclq.lib().cdclq_f64_to_f32_device(ctx.ptr, h64s[key].ptr, n * n, h32s[key].ptr))
+            if xts:
+                ctx.check(cdclq.lib().cdclq_f64_to_f32_device(ctx.ptr, m64s[key].ptr, n * n, m32s[key].ptr))
         for name, d_out, key in spec["layers"]:
             n = spec["inputs"][key]
             c, s, z = outs[name]
-            _, _, st = cdclq.quantize_layer_device(ctx, ws[name], d_out, n, h32s[key], None, key, cfg, c, s, z,
-                                                   nthreads=spec["nthreads"])
+            _, _, st = cdclq.quantize_layer_device(ctx, ws[name], d_out, n, h32s[key], m32s.get(key), key, cfg, c, s,
+                                                   z, nthreads=spec["nthreads"])
             stats[name] = st
         return stats
 
@@ -380,8 +570,10 @@ def main():
             f"updates {st.code_updates} prepare {st.secs_prepare:.3f}s quant {st.secs_quant:.3f}s")
     gram_ms = ph["gram"]["ms"]
     gram_launches = ph["gram"]["launches"]
-    # algorithmic work: n(n+1)T per symmetric H; one launch covers all of the layer's inputs
-    flops = args.steps * sum(gram_flops(n, T) for n in spec["inputs"].values())
+    # algorithmic work, one launch for all of the step's accumulations: n(n+1)T per symmetric H (one
+    # triangle), 2 n^2 T per cross-covariance
+    flops = args.steps * sum(gram_flops(j[0].shape[1], T) if j[0] is j[1] else 2.0 * j[0].shape[1] ** 2 * T
+                             for j in jobs)
     achieved = flops / (gram_ms * 1e-3) / 1e12 if gram_ms > 0 else 0.0
     phases = {k: round(v["ms"] / args.steps, 3) for k, v in ph.items()}
     log(f"[bench] device ms per step by phase: {phases}")
@@ -398,20 +590,22 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32+f64",
-        "data": "synthetic (counter-based N(0,1) activations with outlier channels, N(0,s^2) weights)",
+        "data": DATA_DESC[(spec.get("xgen") or {"kind": "outlier"})["kind"]],
         "config": {"workload": spec["workload"], "tokens": T,
                    "layers": {name: [d_out, spec["inputs"][key]] for name, d_out, key in spec["layers"]},
                    "quant": {**spec["cfg"], "passes": cfg.passes, "tol": cfg.tol}, "parallelism": "1 GPU"},
         "phases_ms_per_step": phases,
         "roofline": {
             "bound": "mfma",
-            "kernel": "k_gram_dma (H += X^T X for the layer's 4 inputs, K=1 f32 MFMA chains, f64 chunks)",
+            "kernel": f"k_gram_dma (the step's {len(jobs)} accumulations H += X^T Y in one launch, K=1 f32 MFMA "
+                      "chains, f64 chunks)",
             "achieved": round(achieved, 2),
             "peak": FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
             "traffic": recorded_traffic(f"gram_{args.config}_traffic"),
-            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, profiles/gram_c4_traffic.md)",
+            "traffic_unit": f"bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                            f"profiles/gram_{args.config}_traffic.md)",
             "launches": gram_launches,
         },
     }

@@ -113,6 +113,7 @@ def lib() -> C.CDLL:
         "cdclq_gram_accumulate": ([vp, vp, vp, sz, sz, vp], i32),
         "cdclq_gram_accumulate_device": ([vp, vp, vp, sz, sz, vp], i32),
         "cdclq_gram_accumulate_device_noalloc": ([vp, vp, vp, sz, sz, vp], i32),
+        "cdclq_ctx_last_midpoint_counts": ([vp, vp], i32),
         "cdclq_sgemm_device": ([vp, sz, sz, sz, C.c_float, vp, C.c_ssize_t, C.c_ssize_t, vp, C.c_ssize_t,
                                 C.c_ssize_t, C.c_float, vp, C.c_ssize_t, C.c_ssize_t], i32),
         "cdclq_dgemm_device": ([vp, sz, sz, sz, C.c_double, vp, C.c_ssize_t, C.c_ssize_t, vp, C.c_ssize_t,
@@ -148,6 +149,9 @@ def lib() -> C.CDLL:
         "cdclq_synth_normal_device": ([vp, u64, u64, sz, C.c_float, vp], i32),
         "cdclq_synth_outlier_scales": ([u64, sz, C.c_double, C.c_float, vp], i32),
         "cdclq_synth_tokens_device": ([vp, u64, u64, sz, sz, vp, vp], i32),
+        "cdclq_synth_tokens_heavy_device": ([vp, u64, u64, sz, sz, vp, vp, vp], i32),
+        "cdclq_synth_perturb_device": ([vp, u64, u64, sz, C.c_float, vp, vp], i32),
+        "cdclq_synth_lognormal_scales": ([u64, sz, C.c_float, vp], i32),
         "cdclq_f64_to_f32_device": ([vp, vp, sz, vp], i32),
         "cdclq_ctx_set_timing": ([vp, i32], i32),
         "cdclq_ctx_reset_timing": ([vp], i32),
@@ -171,9 +175,11 @@ def exported_symbols() -> list[str]:
         "cdclq_num_groups", "cdclq_ctx_create", "cdclq_ctx_destroy", "cdclq_last_error", "cdclq_ctx_clear_cache",
         "cdclq_quantize_layer", "cdclq_quantize_layer_device", "cdclq_gram_accumulate",
         "cdclq_gram_accumulate_device", "cdclq_gram_accumulate_device_noalloc", "cdclq_gram_accumulate_batch_device",
-        "cdclq_sgemm_device", "cdclq_dgemm_device", "cdclq_upper_chol_of_inverse", "cdclq_upper_chol_of_inverse_device",
+        "cdclq_sgemm_device", "cdclq_dgemm_device", "cdclq_ctx_last_midpoint_counts", "cdclq_upper_chol_of_inverse", "cdclq_upper_chol_of_inverse_device",
         "cdclq_proxy_loss", "cdclq_device_alloc", "cdclq_device_free", "cdclq_memcpy_h2d", "cdclq_memcpy_d2h",
-        "cdclq_memset_device", "cdclq_synth_normal_device", "cdclq_synth_outlier_scales", "cdclq_synth_tokens_device", "cdclq_f64_to_f32_device",
+        "cdclq_memset_device", "cdclq_synth_normal_device", "cdclq_synth_outlier_scales", "cdclq_synth_tokens_device",
+        "cdclq_synth_tokens_heavy_device", "cdclq_synth_perturb_device", "cdclq_synth_lognormal_scales",
+        "cdclq_f64_to_f32_device",
         "cdclq_ctx_set_timing", "cdclq_ctx_reset_timing", "cdclq_ctx_get_timing",
         "cdclq_row_bytes", "cdclq_pack_layer", "cdclq_pack_layer_device", "cdclq_dequantize_packed",
         "cdclq_dequantize_packed_device", "cdclq_dequantize_layer", "cdclq_dequantize_layer_device",
@@ -181,6 +187,9 @@ def exported_symbols() -> list[str]:
         "cdclq_rel_err_device", "cdclq_bench_run", "cdclq_quantize_model", "cdclq_dequantize_model",
         "cdclq_hessian_accumulate_device", "cdclq_hessian_finalize_device",
     ]
+
+
+MIDPOINT_FIELDS = ("code_decisions", "code_near", "zero_decisions", "zero_near", "cd_decisions", "cd_near")
 
 
 class Method(enum.IntEnum):
@@ -305,6 +314,13 @@ class Context:
     def clear_cache(self):
         self.check(lib().cdclq_ctx_clear_cache(self.ptr))
         self.cache_owner = None
+
+    def last_midpoint_counts(self) -> dict:
+        """Near-midpoint accounting of the last quantize_layer call on this context
+        (cdclq_midpoint_counts in include/cdclq.h)."""
+        mc = (C.c_uint64 * 6)()
+        self.check(lib().cdclq_ctx_last_midpoint_counts(self.ptr, mc))
+        return dict(zip(MIDPOINT_FIELDS, (int(v) for v in mc)))
 
     # ---- timing
     def set_timing(self, on: bool):
@@ -485,6 +501,38 @@ def synth_outlier_scales(seed: int, n: int, frac: float, factor: float) -> np.nd
     if rc != OK:
         raise CdclqError(rc, "cdclq_synth_outlier_scales failed")
     return out
+
+
+def synth_heavy_channels(seed: int, n: int, frac: float) -> np.ndarray:
+    """Mask of round(frac * n) channels (the seeded pick of synth_outlier_scales) that draw
+    Student-t(3) values in synth_tokens_device."""
+    return (synth_outlier_scales(seed, n, frac, 2.0) != 1.0).astype(np.uint8)
+
+
+def synth_lognormal_scales(seed: int, n: int, sigma: float) -> np.ndarray:
+    """exp(sigma * normal(seed, j)) per channel j (log-normal channel scales)."""
+    out = np.empty(n, np.float32)
+    rc = lib().cdclq_synth_lognormal_scales(seed, n, sigma, out.ctypes.data)
+    if rc != OK:
+        raise CdclqError(rc, "cdclq_synth_lognormal_scales failed")
+    return out
+
+
+def synth_tokens_device(ctx: "Context", seed: int, t: int, n: int, x: "DeviceArray", ch_scale=None, heavy=None,
+                        row0: int = 0):
+    """x (t x n, device) = counter-based tokens; ch_scale: n f32 channel scales, heavy: n-channel
+    mask of Student-t(3) channels (both host arrays or None)."""
+    cs = None if ch_scale is None else np.ascontiguousarray(ch_scale, np.float32)
+    hv = None if heavy is None else np.ascontiguousarray(heavy, np.uint8)
+    ctx.check(lib().cdclq_synth_tokens_heavy_device(ctx.ptr, seed, row0, t, n, None if cs is None else cs.ctypes.data,
+                                                    None if hv is None else hv.ctypes.data, x.ptr))
+
+
+def synth_perturb_device(ctx: "Context", seed: int, x: "DeviceArray", out: "DeviceArray", sigma: float,
+                         offset: int = 0):
+    """out = x + sigma * N(0, 1) (counter stream `seed`), elementwise on the device."""
+    count = int(np.prod(x.shape))
+    ctx.check(lib().cdclq_synth_perturb_device(ctx.ptr, seed, offset, count, sigma, x.ptr, out.ptr))
 
 
 # ---------------------------------------------------------------- packed container cdclq-v1

@@ -38,6 +38,23 @@ __device__ __forceinline__ float quant_dq(float x, float scale, float zero, floa
 
 __device__ __forceinline__ uint8_t code_of(float q) { return (q == q) ? (uint8_t)q : (uint8_t)0; }
 
+// Near-midpoint test of one rounding decision clamp(round(num / den) + zero, 0, maxq) (the
+// accounting of the parity contract): the pre-round value in f64 from the same f32 operands lies
+// within 1e-9 of k + 1/2, and the two candidate results differ after clamping. The f32 quotient is
+// then exactly k + 1/2 (half an f32 ulp of any |v| >= 1/2 exceeds 1e-9), which screens out all but
+// those cases before the f64 division.
+__device__ __forceinline__ bool near_midpoint(float num, float den, float zero, float maxq) {
+  const float q = num / den;
+  const float fl = __builtin_floorf(q);
+  if (q - fl != 0.5f) return false;
+  const double v = (double)num / (double)den;
+  if (__builtin_fabs(v - (__builtin_floor(v) + 0.5)) > 1e-9) return false;
+  return rs_clampf(fl + zero, 0.0f, maxq) != rs_clampf(fl + 1.0f + zero, 0.0f, maxq);
+}
+
+// Slots of the device counters of one quantize_layer call (unsigned long long each).
+enum { MID_CODE_NEAR = 0, MID_ZERO_NEAR = 1, MID_CD_NEAR = 2, MID_SLOTS = 8 };
+
 // find_params' `mk` closure (src/quant.rs:54-61).
 __device__ __forceinline__ void grid_mk(float lo, float hi, float maxq, float* s, float* z) {
   float scale = round_f16((hi - lo) / maxq);
@@ -132,6 +149,16 @@ __device__ __host__ __forceinline__ float synth_normal_at(uint64_t seed, uint64_
   double u2 = u01_at(seed, 2 * i + 1);
   double r = sqrt(-2.0 * synth_log(u1));
   return (float)(r * synth_cos2pi(u2));
+}
+// Student-t with 3 degrees of freedom, Z / sqrt(chi2_3 / 3): Z = normal i of `seed`, chi2_3 the sum
+// of squares of normals 3i, 3i+1, 3i+2 of a second stream; f64 basic operations, rounded once.
+__device__ __host__ __forceinline__ float synth_student3_at(uint64_t seed, uint64_t i) {
+  const uint64_t s2 = mix64(seed ^ 0x7F4A7C159E3779B9ULL);
+  const double z = (double)synth_normal_at(seed, i);
+  const double a = (double)synth_normal_at(s2, 3 * i), b = (double)synth_normal_at(s2, 3 * i + 1),
+               c = (double)synth_normal_at(s2, 3 * i + 2);
+  const double chi = a * a + b * b + c * c;
+  return (float)(z * sqrt(3.0 / chi));
 }
 
 // ---- direct-to-LDS loads

@@ -35,7 +35,7 @@ struct cdclq_ctx {
   DevBuf w_in, h_in, m_in, x_in, y_in, h64_in, u_out, codes_o, scales_o, zeros_o;
   DevBuf wp, wwork, wq, ebuf, gbits_d, perm_d, deadp_d, dead_d, diag_d, colsq_d, invd, colloss_d;
   DevBuf G, part, rlog, rcnt, clog, ccnt, sel_d, ld_d, mp, t1, t2, a64, y64, tbuf, tpart, status_d, rtiles_d,
-      tiles_d, proxy_p, cs_d, gemm_part;
+      tiles_d, proxy_p, cs_d, gemm_part, mid_d;
   // one-entry PrepCache (src/engine.rs:207-223): key, perm, damping and the device factors
   bool cache_valid = false;
   std::string cache_key;
@@ -52,6 +52,8 @@ struct cdclq_ctx {
   // the lookup's error
   void* gram_scratch = nullptr;
   hipError_t gram_scratch_err = hipSuccess;
+  // near-midpoint accounting of the last quantize_layer call
+  cdclq_midpoint_counts mid_last = {};
   // timing
   bool timing = false;
   // pinned host staging of the repair loop's per-pass transfers (grows; freed with the context)

@@ -191,9 +191,10 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
   if (!w || !h || !codes || !scales || !zeros || !perm_out || !gbits_out)
     return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
   if (d_out_ == 0 || n_ == 0) return fail(ctx, CDCLQ_INVALID_ARG, "empty layer (d_out and d_in must be > 0)");
-  if (n_ > 65536 || d_out_ > (size_t)1 << 20 || d_out_ * n_ > ((size_t)1 << 31) - 1)
-    return fail(ctx, CDCLQ_INVALID_ARG, "layer too large for this build (d_in <= 65536, d_out*d_in < 2^31)");
+  if (n_ > 65535 || d_out_ > (size_t)1 << 20 || d_out_ * n_ > ((size_t)1 << 31) - 1)
+    return fail(ctx, CDCLQ_INVALID_ARG, "layer too large for this build (d_in <= 65535, d_out*d_in < 2^31)");
   CK(validate(ctx, cfg, n_));
+  ctx->mid_last = cdclq_midpoint_counts{};
   const int d_out = (int)d_out_, n = (int)n_;
   const int g = (int)effective_group(cfg, n_);
   const int ng = (n + g - 1) / g;
@@ -344,6 +345,11 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
   const int nchunks = (d_out + rc - 1) / rc;
 
   const double t1 = now_secs();
+  // near-midpoint counters (MID_SLOTS u64) and the per-row descent evaluation counts (d_out u32)
+  CK(ensure(ctx, ctx->mid_d, MID_SLOTS * 8 + (size_t)d_out * 4));
+  unsigned long long* mid = P<unsigned long long>(ctx->mid_d);
+  uint32_t* cd_evals = reinterpret_cast<uint32_t*>(mid + MID_SLOTS);
+  HIPCK(zero_words(st, reinterpret_cast<int*>(mid), 2 * MID_SLOTS + d_out));
   // ---- phase 1: blocked GPTQ with lazy updates (src/engine.rs:397-479)
   CK(ensure(ctx, ctx->wwork, wn * 4));
   CK(ensure(ctx, ctx->wq, wn * 4));
@@ -362,7 +368,7 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
     for (int i1 = 0; i1 < n; i1 += bsz) {
       const int i2 = std::min(i1 + bsz, n), cnt = i2 - i1;
       HIPCK(gptq_block(st, d_out, n, i1, cnt, g, ng, wwork, U, P<float>(ctx->invd), P<uint8_t>(ctx->gbits_d),
-                       cfg->mse_grid, scales, zeros, codes, wq, eb));
+                       cfg->mse_grid, scales, zeros, codes, wq, eb, mid));
       if (i2 < n) {  // lazy update W[:, i2:] -= E[:, i1:i2] U[i1:i2, i2:] (src/engine.rs:452-471)
         if (chain_gemm_mfma_ok(d_out, n - i2, cnt, eb + i1, n, U + (long)i1 * n + i2, n))
           HIPCK(chain_gemm_mfma(st, d_out, n - i2, cnt, -1.0f, 1, eb + i1, n, U + (long)i1 * n + i2, n, wwork + i2, n));
@@ -502,7 +508,8 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
           CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32, rtiles + (size_t)(1 + s) * ntile, tcnt[1 + s]));
           HIPCK(cd_subblock(st, d_out, n, ng, g, c0, wd, s, n_sb, rc, (int)cfg->cd_sweeps, P<float>(ctx->G), H32,
                             P<uint8_t>(ctx->gbits_d), scales, zeros, codes, wq, eb, active,
-                            P<uint8_t>(ctx->sel_d), clog + (size_t)s * d_out * cap, ccnt + (size_t)s * d_out, cap));
+                            P<uint8_t>(ctx->sel_d), clog + (size_t)s * d_out * cap, ccnt + (size_t)s * d_out, cap,
+                            mid, cd_evals));
         }
       }
       HIPCK(pass_accum(st, d_out, rc, nchunks, do_refit ? ng : 0, rlog, rcnt, do_cd ? n_sb : 0, cap, clog, ccnt,
@@ -535,6 +542,21 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
   }
   HIPCK(hipStreamSynchronize(st));
   const double secs_quant = now_secs() - t1;
+  {
+    std::vector<unsigned long long> mh(MID_SLOTS);
+    std::vector<uint32_t> ev(d_out);
+    HIPCK(hipMemcpyAsync(mh.data(), mid, MID_SLOTS * 8, hipMemcpyDeviceToHost, st));
+    HIPCK(hipMemcpyAsync(ev.data(), cd_evals, (size_t)d_out * 4, hipMemcpyDeviceToHost, st));
+    HIPCK(hipStreamSynchronize(st));
+    cdclq_midpoint_counts mc{};
+    mc.code_decisions = (uint64_t)d_out * n;
+    mc.code_near = mh[MID_CODE_NEAR];
+    mc.zero_decisions = (uint64_t)d_out * ng;
+    mc.zero_near = mh[MID_ZERO_NEAR];
+    for (uint32_t v : ev) mc.cd_decisions += v;
+    mc.cd_near = mh[MID_CD_NEAR];
+    ctx->mid_last = mc;
+  }
 
   std::memcpy(perm_out, perm.data(), (size_t)n * 4);
   std::memcpy(gbits_out, gbits.data(), (size_t)ng);
@@ -575,8 +597,8 @@ int gram_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const f
   for (int i = 0; i < count; ++i) {
     if (!xs[i] || !ys[i] || !hs[i]) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
     if (ns[i] == 0 || ts[i] == 0) continue;
-    if (ns[i] > 65536 || ts[i] > ((size_t)1 << 31) - 4096)
-      return fail(ctx, CDCLQ_INVALID_ARG, "gram_accumulate: n <= 65536 and t < 2^31 in this build");
+    if (ns[i] > 65535 || ts[i] > ((size_t)1 << 31) - 4096)
+      return fail(ctx, CDCLQ_INVALID_ARG, "gram_accumulate: n <= 65535 and t < 2^31 in this build");
     jobs.push_back(GramJob{xs[i], ys[i], hs[i], (int)ns[i], (int)ts[i]});
     vec4 = vec4 && (ns[i] % 4 == 0) && ((uintptr_t)xs[i] % 16 == 0) && ((uintptr_t)ys[i] % 16 == 0);
   }
@@ -684,7 +706,7 @@ int gram_device(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t
 int uchol_device(cdclq_ctx* ctx, const double* h, size_t n_, float* u) {
   if (!h || !u) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
   if (n_ == 0) return CDCLQ_OK;
-  if (n_ > 65536) return fail(ctx, CDCLQ_INVALID_ARG, "n > 65536 is not supported in this build");
+  if (n_ > 65535) return fail(ctx, CDCLQ_INVALID_ARG, "n > 65535 is not supported in this build");
   HIPCK(hipSetDevice(ctx->device));
   const int n = (int)n_;
   CK(ensure(ctx, ctx->a64, (size_t)n * n * 8));
@@ -769,7 +791,7 @@ void cdclq_ctx_destroy(cdclq_ctx* ctx) {
                     &ctx->gbits_d, &ctx->perm_d, &ctx->deadp_d, &ctx->dead_d, &ctx->diag_d, &ctx->colsq_d,
                     &ctx->invd, &ctx->colloss_d, &ctx->G, &ctx->part, &ctx->rlog, &ctx->rcnt, &ctx->clog, &ctx->ccnt, &ctx->rtiles_d,
                     &ctx->sel_d, &ctx->ld_d, &ctx->mp, &ctx->t1, &ctx->t2, &ctx->a64, &ctx->y64,
-                    &ctx->tbuf, &ctx->tpart, &ctx->status_d, &ctx->tiles_d, &ctx->proxy_p, &ctx->cs_d, &ctx->gemm_part,
+                    &ctx->tbuf, &ctx->tpart, &ctx->status_d, &ctx->tiles_d, &ctx->proxy_p, &ctx->cs_d, &ctx->gemm_part, &ctx->mid_d,
                     &ctx->cache_u, &ctx->cache_h32, &ctx->pk_flag};
   for (DevBuf* b : bufs) free_buf(*b);
   for (DevBuf& b : ctx->pk_in) free_buf(b);
@@ -858,6 +880,12 @@ int cdclq_gram_accumulate_device_noalloc(cdclq_ctx* ctx, const float* x, const f
     return fail(ctx, CDCLQ_DEVICE, std::string("allocation-free scratch unavailable on this device (") +
                                        hipGetErrorString(ctx->gram_scratch_err) + ")");
   return gram_batch_device(ctx, 1, &x, &y, &t, &n, &h, static_cast<char*>(ctx->gram_scratch));
+}
+
+int cdclq_ctx_last_midpoint_counts(const cdclq_ctx* ctx, cdclq_midpoint_counts* out) {
+  if (!ctx || !out) return CDCLQ_INVALID_ARG;
+  *out = ctx->mid_last;
+  return CDCLQ_OK;
 }
 
 int cdclq_sgemm_device(cdclq_ctx* ctx, size_t m, size_t k, size_t n, float alpha, const float* a, ptrdiff_t rsa,
@@ -1061,18 +1089,45 @@ int cdclq_synth_outlier_scales(uint64_t seed, size_t n, double frac, float facto
   return CDCLQ_OK;
 }
 
-int cdclq_synth_tokens_device(cdclq_ctx* ctx, uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale,
-                              float* x) {
+int cdclq_synth_tokens_heavy_device(cdclq_ctx* ctx, uint64_t seed, uint64_t row0, size_t t, size_t n,
+                                    const float* ch_scale, const uint8_t* heavy, float* x) {
   if (!ctx || (!x && t && n)) return CDCLQ_INVALID_ARG;
   ctx->err.clear();
+  // channel scales (n f32) and the heavy-tail mask (n u8) staged in one buffer
+  const size_t off = (n * 4 + 255) & ~(size_t)255;
+  CK(ensure(ctx, ctx->cs_d, off + n));
   const float* cs = nullptr;
+  const uint8_t* hv = nullptr;
   if (ch_scale) {
-    CK(ensure(ctx, ctx->cs_d, n * 4));
     HIPCK(hipMemcpyAsync(ctx->cs_d.p, ch_scale, n * 4, hipMemcpyHostToDevice, ctx->st));
     cs = P<float>(ctx->cs_d);
   }
-  HIPCK(synth_tokens(ctx->st, seed, row0, t, n, cs, x));
+  if (heavy) {
+    HIPCK(hipMemcpyAsync(P<char>(ctx->cs_d) + off, heavy, n, hipMemcpyHostToDevice, ctx->st));
+    hv = reinterpret_cast<const uint8_t*>(P<char>(ctx->cs_d) + off);
+  }
+  HIPCK(synth_tokens(ctx->st, seed, row0, t, n, cs, hv, x));
   HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
+int cdclq_synth_tokens_device(cdclq_ctx* ctx, uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale,
+                              float* x) {
+  return cdclq_synth_tokens_heavy_device(ctx, seed, row0, t, n, ch_scale, nullptr, x);
+}
+
+int cdclq_synth_perturb_device(cdclq_ctx* ctx, uint64_t seed, uint64_t offset, size_t count, float sigma,
+                               const float* x, float* out) {
+  if (!ctx || ((!x || !out) && count)) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  HIPCK(synth_perturb(ctx->st, seed, offset, count, sigma, x, out));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
+}
+
+int cdclq_synth_lognormal_scales(uint64_t seed, size_t n, float sigma, float* scales) {
+  if (!scales && n) return CDCLQ_INVALID_ARG;
+  for (size_t j = 0; j < n; ++j) scales[j] = (float)std::exp((double)sigma * (double)synth_normal_at(seed, j));
   return CDCLQ_OK;
 }
 

@@ -14,6 +14,10 @@ namespace cdclq {
 namespace {
 
 inline unsigned nblk(long count) { return (unsigned)((count + 255) / 256); }
+// Grid of a grid-stride launch over `count` elements: at most 2^20 workgroups of 256, so the
+// dispatch stays far below 2^32 work-items whatever the element count (a 524,288-token input of
+// width 8192 alone has 2^32 elements).
+inline unsigned gs_blocks(long count) { return (unsigned)std::min<long>((count + 255) / 256, 1L << 20); }
 
 __device__ __forceinline__ int readlane_i(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 
@@ -76,7 +80,7 @@ __global__ __launch_bounds__(64 * GB_ROWS) void k_gptq_block(int rows, int n, in
                                                     const float* __restrict__ invd, const uint8_t* __restrict__ gbits,
                                                     int mse, float* __restrict__ scales, float* __restrict__ zeros,
                                                     uint8_t* __restrict__ codes, float* __restrict__ wq,
-                                                    float* __restrict__ err) {
+                                                    float* __restrict__ err, unsigned long long* __restrict__ mid) {
   constexpr bool STAGE = NPL <= 2;
   constexpr int UB = STAGE ? 64 * NPL : 1;  // staged block width
   __shared__ float ub[UB * UB];
@@ -116,6 +120,8 @@ __global__ __launch_bounds__(64 * GB_ROWS) void k_gptq_block(int rows, int n, in
   }
   // A block that starts inside a group (block < group) continues with the stored grid.
   float sc = 0.0f, zr = 0.0f, maxq = 0.0f;
+  // near-midpoint decisions of this row (wave-uniform: every lane evaluates the same column)
+  unsigned near_codes = 0, near_zeros = 0;
   if (i1 % g != 0) {
     const int gi = i1 / g;
     sc = scales[(long)r * ng + gi];
@@ -155,6 +161,7 @@ __global__ __launch_bounds__(64 * GB_ROWS) void k_gptq_block(int rows, int n, in
           xmax = 1.0f;
         }
         grid_mk(xmin, xmax, maxq, &sc, &zr);
+        float lo_used = xmin;  // the lower end of the grid chosen below, for the zero's accounting
         if (mse) {
           // 24 clip ratios, one per lane; each lane runs its candidate's sequential error sum over
           // the group in column order (src/quant.rs:65-81), then the first minimum wins.
@@ -197,7 +204,9 @@ __global__ __launch_bounds__(64 * GB_ROWS) void k_gptq_block(int rows, int n, in
           bc = readlane_i(bc, 0);
           sc = readlane(cs, bc);
           zr = readlane(cz, bc);
+          lo_used = (1.0f - 0.02f * (float)bc) * xmin;
         }
+        near_zeros += near_midpoint(-lo_used, sc, 0.0f, maxq) ? 1u : 0u;
         if (lane == 0) {
           scales[(long)r * ng + gi] = sc;
           zeros[(long)r * ng + gi] = zr;
@@ -215,6 +224,7 @@ __global__ __launch_bounds__(64 * GB_ROWS) void k_gptq_block(int rows, int n, in
       const float xv = readlane(x[s], ii);
       float q;
       const float dq = quant_dq(xv, sc, zr, maxq, &q);
+      near_codes += near_midpoint(xv, sc, zr, maxq) ? 1u : 0u;
       const float e = (xv - dq) * (STAGE ? di : invd[j]);
       if (lane == ii) {
         mq[s] = q;
@@ -241,6 +251,10 @@ __global__ __launch_bounds__(64 * GB_ROWS) void k_gptq_block(int rows, int n, in
       wq[o] = mwq[s];
       err[o] = me[s];
     }
+  }
+  if (lane == 0 && (near_codes | near_zeros)) {  // rare: counted with one atomic per row and kind
+    if (near_codes) atomicAdd(&mid[MID_CODE_NEAR], (unsigned long long)near_codes);
+    if (near_zeros) atomicAdd(&mid[MID_ZERO_NEAR], (unsigned long long)near_zeros);
   }
 }
 
@@ -379,22 +393,33 @@ __global__ __launch_bounds__(256) void k_pass_accum(int rows, int rc, int nref, 
 // ---------------------------------------------------------------- synthetic inputs
 __global__ __launch_bounds__(256) void k_synth_normal(uint64_t seed, uint64_t offset, long count, float sigma,
                                                       float* __restrict__ out) {
-  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-  if (idx < count) out[idx] = synth_normal_at(seed, offset + (uint64_t)idx) * sigma;
+  for (long idx = (long)blockIdx.x * 256 + threadIdx.x; idx < count; idx += (long)gridDim.x * 256)
+    out[idx] = synth_normal_at(seed, offset + (uint64_t)idx) * sigma;
 }
 
 __global__ __launch_bounds__(256) void k_synth_tokens(uint64_t seed, uint64_t row0, long t, int n,
-                                                      const float* __restrict__ cs, float* __restrict__ x) {
-  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= t * (long)n) return;
-  const long r = idx / n;
-  const int j = (int)(idx % n);
-  x[idx] = synth_normal_at(seed, (row0 + (uint64_t)r) * (uint64_t)n + (uint64_t)j) * (cs ? cs[j] : 1.0f);
+                                                      const float* __restrict__ cs, const uint8_t* __restrict__ heavy,
+                                                      float* __restrict__ x) {
+  const long count = t * (long)n;
+  for (long idx = (long)blockIdx.x * 256 + threadIdx.x; idx < count; idx += (long)gridDim.x * 256) {
+    const long r = idx / n;
+    const int j = (int)(idx % n);
+    const uint64_t i = (row0 + (uint64_t)r) * (uint64_t)n + (uint64_t)j;
+    const float v = (heavy && heavy[j]) ? synth_student3_at(seed, i) : synth_normal_at(seed, i);
+    x[idx] = v * (cs ? cs[j] : 1.0f);
+  }
+}
+
+// out = x + sigma * normal(seed, offset + i)
+__global__ __launch_bounds__(256) void k_synth_perturb(uint64_t seed, uint64_t offset, long count, float sigma,
+                                                       const float* __restrict__ x, float* __restrict__ out) {
+  for (long idx = (long)blockIdx.x * 256 + threadIdx.x; idx < count; idx += (long)gridDim.x * 256)
+    out[idx] = x[idx] + synth_normal_at(seed, offset + (uint64_t)idx) * sigma;
 }
 
 __global__ __launch_bounds__(256) void k_f64_to_f32(long count, const double* __restrict__ a, float* __restrict__ b) {
-  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-  if (idx < count) b[idx] = (float)a[idx];
+  for (long idx = (long)blockIdx.x * 256 + threadIdx.x; idx < count; idx += (long)gridDim.x * 256)
+    b[idx] = (float)a[idx];
 }
 
 // Block partial sums of (f64)e * (f64)eh for proxy_loss (src/engine.rs:814).
@@ -448,12 +473,12 @@ static int npl_for(int cnt) {
 
 hipError_t gptq_block(hipStream_t st, int rows, int n, int i1, int cnt, int g, int ng, float* w, const float* u,
                       const float* invd, const uint8_t* gbits, int mse, float* scales, float* zeros, uint8_t* codes,
-                      float* wq, float* err) {
+                      float* wq, float* err, unsigned long long* mid) {
   const dim3 grid((rows + GB_ROWS - 1) / GB_ROWS), blk(64 * GB_ROWS);
 #define GPTQ_CASE(N)                                                                                                   \
   case N:                                                                                                              \
     hipLaunchKernelGGL(k_gptq_block<N>, grid, blk, 0, st, rows, n, i1, cnt, g, ng, w, u, invd, gbits, mse, scales,    \
-                       zeros, codes, wq, err);                                                                         \
+                       zeros, codes, wq, err, mid);                                                                    \
     break;
   switch (npl_for(cnt)) {
     GPTQ_CASE(1)
@@ -489,21 +514,28 @@ hipError_t pass_accum(hipStream_t st, int rows, int rc, int nchunks, int nref, c
 
 hipError_t synth_normal(hipStream_t st, uint64_t seed, uint64_t offset, size_t count, float sigma, float* out) {
   if (!count) return hipSuccess;
-  hipLaunchKernelGGL(k_synth_normal, dim3(nblk((long)count)), dim3(256), 0, st, seed, offset, (long)count, sigma, out);
+  hipLaunchKernelGGL(k_synth_normal, dim3(gs_blocks((long)count)), dim3(256), 0, st, seed, offset, (long)count, sigma, out);
   return hipGetLastError();
 }
 
 hipError_t synth_tokens(hipStream_t st, uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale,
-                        float* x) {
+                        const uint8_t* heavy, float* x) {
   if (!t || !n) return hipSuccess;
-  hipLaunchKernelGGL(k_synth_tokens, dim3(nblk((long)(t * n))), dim3(256), 0, st, seed, row0, (long)t, (int)n, ch_scale,
-                     x);
+  hipLaunchKernelGGL(k_synth_tokens, dim3(gs_blocks((long)(t * n))), dim3(256), 0, st, seed, row0, (long)t, (int)n, ch_scale,
+                     heavy, x);
+  return hipGetLastError();
+}
+hipError_t synth_perturb(hipStream_t st, uint64_t seed, uint64_t offset, size_t count, float sigma, const float* x,
+                         float* out) {
+  if (!count) return hipSuccess;
+  hipLaunchKernelGGL(k_synth_perturb, dim3(gs_blocks((long)count)), dim3(256), 0, st, seed, offset, (long)count, sigma, x,
+                     out);
   return hipGetLastError();
 }
 
 hipError_t f64_to_f32(hipStream_t st, size_t count, const double* a, float* b) {
   if (!count) return hipSuccess;
-  hipLaunchKernelGGL(k_f64_to_f32, dim3(nblk((long)count)), dim3(256), 0, st, (long)count, a, b);
+  hipLaunchKernelGGL(k_f64_to_f32, dim3(gs_blocks((long)count)), dim3(256), 0, st, (long)count, a, b);
   return hipGetLastError();
 }
 

@@ -7,6 +7,8 @@
 #include <cstdint>
 
 #include "cdclq.h"
+#include <algorithm>
+
 #include "cdclq_dev.h"
 #include "kernels.h"
 
@@ -247,9 +249,8 @@ namespace {
 // xf = x * sqrt(w_t) per token (f32, as `xf * state["w"].sqrt().unsqueeze(1)`)
 __global__ __launch_bounds__(256) void k_token_scale(long t, int n, const float* __restrict__ x,
                                                      const float* __restrict__ w, float* __restrict__ out) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= t * n) return;
-  out[i] = x[i] * sqrtf(w[i / n]);
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < t * n; i += (long)gridDim.x * 256)
+    out[i] = x[i] * sqrtf(w[i / n]);
 }
 
 // h = (f32)(acc / count): the 1/N normalisation, rounded once from f64
@@ -263,7 +264,9 @@ __global__ __launch_bounds__(256) void k_normalize(long count, const double* __r
 
 hipError_t token_scale(hipStream_t st, long t, int n, const float* x, const float* w, float* out) {
   if (t * n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_token_scale, dim3((unsigned)((t * n + 255) / 256)), dim3(256), 0, st, t, n, x, w, out);
+  // grid-stride: at most 2^20 workgroups, far below 2^32 work-items for any t x n
+  hipLaunchKernelGGL(k_token_scale, dim3((unsigned)std::min<long>((t * n + 255) / 256, 1L << 20)), dim3(256), 0, st,
+                     t, n, x, w, out);
   return hipGetLastError();
 }
 

@@ -902,7 +902,8 @@ __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int 
                                             const float* __restrict__ zeros, uint8_t* __restrict__ codes,
                                             float* __restrict__ wq, float* __restrict__ e,
                                             const uint8_t* __restrict__ active, const uint8_t* __restrict__ sel,
-                                            double* __restrict__ dlog, uint32_t* __restrict__ dcnt, int cap) {
+                                            double* __restrict__ dlog, uint32_t* __restrict__ dcnt, int cap,
+                                            unsigned long long* __restrict__ mid, uint32_t* __restrict__ evals) {
   const int lane = threadIdx.x & 63;
   const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
   if (r >= rows) return;
@@ -930,13 +931,14 @@ __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int 
     zz[s] = zeros[(long)r * ng + gi];
     mq[s] = (float)((1u << gbits[gi]) - 1u);
   }
-  uint32_t moves = 0;
+  uint32_t moves = 0, nevals = 0, nnear = 0;
   double* dl = dlog + (long)r * cap;
   for (int sw = 0; sw < sweeps; ++sw) {
     bool changed = false;
 #pragma unroll
     for (int s = 0; s < NPL; ++s) {
       const bool in = s * 64 + lane < wd;
+      const uint64_t inmask = __ballot(in);
       int start = 0;
       while (start < 64) {
         // this lane's column, visited now: target = w_hat_j + g_j / H_jj (src/engine.rs:626-640)
@@ -945,6 +947,11 @@ __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int 
         const float newdq = quant_dq(target, sc[s], zz[s], mq[s], &qv);
         const int qc = (int)code_of(qv);
         const uint64_t mask = __ballot(in && lane >= start && qc != mc[s]);
+        // the sequential visit evaluated columns start .. (the move, or the slice's end) with this gradient
+        const int last = mask ? (int)__builtin_ctzll(mask) : 63;
+        const uint64_t seen = (~0ull << start) & (last == 63 ? ~0ull : ((1ull << (last + 1)) - 1ull)) & inmask;
+        nevals += (uint32_t)__builtin_popcountll(seen);
+        nnear += (uint32_t)__builtin_popcountll(__ballot(near_midpoint(target, sc[s], zz[s], mq[s])) & seen);
         if (mask == 0) break;
         const int jl = __builtin_amdgcn_readfirstlane(__builtin_ctzll(mask));
         const float cur = readlane(mwq[s], jl);
@@ -982,7 +989,11 @@ __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int 
       codes[o] = (uint8_t)mc[s];
     }
   }
-  if (lane == 0) dcnt[r] = moves;
+  if (lane == 0) {
+    dcnt[r] = moves;
+    evals[r] += nevals;  // one wave per row: no other writer in this launch
+    if (nnear) atomicAdd(&mid[MID_CD_NEAR], (unsigned long long)nnear);
+  }
 }
 
 int npl_for(int cnt) {
@@ -1175,11 +1186,12 @@ hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, i
 hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
                        int sweeps, const float* G, const float* h32, const uint8_t* gbits, const float* scales,
                        const float* zeros, uint8_t* codes, float* wq, float* e, const uint8_t* active,
-                       const uint8_t* sel, double* dlog, uint32_t* dcnt, int cap) {
+                       const uint8_t* sel, double* dlog, uint32_t* dcnt, int cap, unsigned long long* mid,
+                       uint32_t* evals) {
   const dim3 grid((rows + 3) / 4), blk(256);
 #define CD_CASE(N)                                                                                                     \
   hipLaunchKernelGGL((k_cd<N>), grid, blk, 0, st, rows, n, ng, g, c0, wd, sb, nsb, rc, sweeps, G, h32, gbits, scales,  \
-                     zeros, codes, wq, e, active, sel, dlog, dcnt, cap)
+                     zeros, codes, wq, e, active, sel, dlog, dcnt, cap, mid, evals)
   switch (npl_for(wd)) {
     case 1: CD_CASE(1); break;
     case 2: CD_CASE(2); break;

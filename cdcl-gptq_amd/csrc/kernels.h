@@ -69,7 +69,7 @@ hipError_t colsq(hipStream_t st, int d_out, int n, const float* w, const uint8_t
 hipError_t inv_diag(hipStream_t st, int n, const float* u, float* invd);
 hipError_t gptq_block(hipStream_t st, int rows, int n, int i1, int cnt, int g, int ng, float* w, const float* u,
                       const float* invd, const uint8_t* gbits, int mse, float* scales, float* zeros, uint8_t* codes,
-                      float* wq, float* err);
+                      float* wq, float* err, unsigned long long* mid);
 hipError_t colloss(hipStream_t st, int rows, int n, int rc, const float* err, double* out);
 hipError_t sub_f32(hipStream_t st, size_t count, const float* a, const float* b, float* out);
 // ---- k_repair.hip: phase 2
@@ -102,7 +102,8 @@ hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, i
 hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
                        int sweeps, const float* G, const float* h32, const uint8_t* gbits, const float* scales,
                        const float* zeros, uint8_t* codes, float* wq, float* e, const uint8_t* active,
-                       const uint8_t* sel, double* dlog, uint32_t* dcnt, int cap);
+                       const uint8_t* sel, double* dlog, uint32_t* dcnt, int cap, unsigned long long* mid,
+                       uint32_t* evals);
 // Folds one pass's logged deltas into the per-chunk loss (exact reference order); nref refit
 // steps (rlog/rcnt: [nref][rows]) then ncd CD steps (clog: [ncd][rows][cap], ccnt: [ncd][rows]).
 hipError_t pass_accum(hipStream_t st, int rows, int rc, int nchunks, int nref, const double* rlog,
@@ -153,8 +154,11 @@ hipError_t token_scale(hipStream_t st, long t, int n, const float* x, const floa
 hipError_t normalize_acc(hipStream_t st, long count, const double* acc, double tokens, float* h);
 
 hipError_t synth_normal(hipStream_t st, uint64_t seed, uint64_t offset, size_t count, float sigma, float* out);
+// x[r][j] = (heavy[j] ? student3 : normal)(seed, (row0 + r) n + j) * ch_scale[j] (null arrays: none / 1)
 hipError_t synth_tokens(hipStream_t st, uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale,
-                        float* x);
+                        const uint8_t* heavy, float* x);
+hipError_t synth_perturb(hipStream_t st, uint64_t seed, uint64_t offset, size_t count, float sigma, const float* x,
+                         float* out);
 hipError_t f64_to_f32(hipStream_t st, size_t count, const double* a, float* b);
 hipError_t proxy_reduce(hipStream_t st, size_t count, const float* e, const float* eh, double* partial, int nblocks);
 

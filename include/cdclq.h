@@ -116,6 +116,24 @@ int cdclq_quantize_layer_device(cdclq_ctx* ctx, const float* w, size_t d_out, si
                                 uint8_t* codes, float* scales, float* zeros, uint32_t* perm, uint8_t* gbits,
                                 cdclq_layer_stats* stats);
 
+/* Near-midpoint accounting of the last cdclq_quantize_layer[_device] call on ctx (no reference
+ * counterpart: the parity contract's record of rounding decisions an implementation with another
+ * operation order could legitimately resolve differently). A decision clamp(round(a / b) + z, 0,
+ * maxq) is near a midpoint when a / b evaluated in f64 from the same f32 operands lies within 1e-9
+ * of k + 1/2 and the two candidates differ after clamping. Counted: the phase-1 codes
+ * (src/quant.rs:92-95, d_out x d_in decisions), the group zero points of the chosen grid
+ * (src/quant.rs:59, d_out x ngroups), and the coordinate-descent evaluations in the reference's
+ * visit order (src/engine.rs:626-636). */
+typedef struct cdclq_midpoint_counts {
+  uint64_t code_decisions;
+  uint64_t code_near;
+  uint64_t zero_decisions;
+  uint64_t zero_near;
+  uint64_t cd_decisions;
+  uint64_t cd_near;
+} cdclq_midpoint_counts;
+int cdclq_ctx_last_midpoint_counts(const cdclq_ctx* ctx, cdclq_midpoint_counts* out);
+
 /* linalg::gram_accumulate (src/linalg.rs:388-418): h (n x n, f64) += x^T y, x and y token-major
  * t x n f32. y == x selects the symmetric Hessian path. */
 int cdclq_gram_accumulate(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h);
@@ -317,6 +335,16 @@ int cdclq_synth_outlier_scales(uint64_t seed, size_t n, double frac, float facto
 /* x[r][j] = normal(seed, (row0 + r) * n + j) * ch_scale[j]; ch_scale is a host array of n. */
 int cdclq_synth_tokens_device(cdclq_ctx* ctx, uint64_t seed, uint64_t row0, size_t t, size_t n,
                               const float* ch_scale, float* x);
+/* As cdclq_synth_tokens_device, with heavy-tailed channels: where heavy[j] != 0 (host array of n,
+ * may be NULL) channel j draws Student-t with 3 degrees of freedom, Z / sqrt(chi2_3 / 3), from the
+ * same counter stream (plus a second stream for chi2_3), identical on host and device. */
+int cdclq_synth_tokens_heavy_device(cdclq_ctx* ctx, uint64_t seed, uint64_t row0, size_t t, size_t n,
+                                    const float* ch_scale, const uint8_t* heavy, float* x);
+/* out[i] = x[i] + sigma * normal(seed, offset + i) (device memory; out may equal x). */
+int cdclq_synth_perturb_device(cdclq_ctx* ctx, uint64_t seed, uint64_t offset, size_t count, float sigma,
+                               const float* x, float* out);
+/* Host array of n log-normal channel scales: scales[j] = exp(sigma * normal(seed, j)). */
+int cdclq_synth_lognormal_scales(uint64_t seed, size_t n, float sigma, float* scales);
 /* h32[i] = (float)h64[i] (the cast at src/bench.rs:177). */
 int cdclq_f64_to_f32_device(cdclq_ctx* ctx, const double* h64, size_t count, float* h32);
 

@@ -139,6 +139,11 @@ def lib():
         L.orc_synth_normal.argtypes = [C.c_uint64, C.c_uint64, sz, C.c_float, f32p]
         L.orc_synth_outlier_scales.argtypes = [C.c_uint64, sz, C.c_double, C.c_float, f32p]
         L.orc_synth_tokens.argtypes = [C.c_uint64, C.c_uint64, sz, sz, C.c_void_p, f32p]
+        L.orc_synth_tokens_heavy.argtypes = [C.c_uint64, C.c_uint64, sz, sz, C.c_void_p, C.c_void_p, f32p]
+        L.orc_last_midpoint_counts.argtypes = [C.c_void_p]
+        L.orc_set_midpoint_map.argtypes = [C.c_void_p]
+        L.orc_synth_student3_at.argtypes = [C.c_uint64, C.c_uint64]
+        L.orc_synth_student3_at.restype = C.c_float
         L.orc_synth_log.argtypes = [C.c_double]
         L.orc_synth_log.restype = C.c_double
         L.orc_synth_cos2pi.argtypes = [C.c_double]
@@ -206,8 +211,11 @@ def effective_group(cfg: OrcConfig, n: int) -> int:
     return n if (cfg.group == 0 or cfg.group >= n) else int(cfg.group)
 
 
-def quantize_layer(w, h, cfg: OrcConfig, m=None, hkey="layer", cache: Cache | None = None, nthreads: int = 8) -> QLayer:
-    """engine::quantize_layer (src/engine.rs:690-799) on the CPU oracle."""
+def quantize_layer(w, h, cfg: OrcConfig, m=None, hkey="layer", cache: Cache | None = None, nthreads: int = 8,
+                   midmap: bool = False) -> QLayer:
+    """engine::quantize_layer (src/engine.rs:690-799) on the CPU oracle. The result's `midpoint`
+    holds the near-midpoint accounting; with midmap=True, `midmap` the per-element map (bit 0
+    phase-1 code, bit 1 descent, bit 2 zero point)."""
     w = np.ascontiguousarray(w, np.float32)
     h = np.ascontiguousarray(h, np.float32)
     d_out, n = w.shape
@@ -225,11 +233,25 @@ def quantize_layer(w, h, cfg: OrcConfig, m=None, hkey="layer", cache: Cache | No
     gbits = np.zeros(ng, np.uint8)
     st = OrcStats()
     err = C.create_string_buffer(512)
-    rc = lib().orc_quantize_layer(w, d_out, n, h, m.ctypes.data if m is not None else None, hkey.encode(), C.byref(cfg),
-                                  nthreads, cache.ptr, codes, scales, zeros, perm, gbits, C.byref(st), err, 512)
+    mmap = np.zeros((d_out, n), np.uint8) if midmap else None
+    lib().orc_set_midpoint_map(mmap.ctypes.data if midmap else None)
+    try:
+        rc = lib().orc_quantize_layer(w, d_out, n, h, m.ctypes.data if m is not None else None, hkey.encode(),
+                                      C.byref(cfg), nthreads, cache.ptr, codes, scales, zeros, perm, gbits, C.byref(st),
+                                      err, 512)
+    finally:
+        lib().orc_set_midpoint_map(None)
     if rc != 0:
         raise OracleError(rc, err.value.decode())
-    return QLayer(d_out, n, g, perm, gbits, codes, scales, zeros, st.as_dict())
+    q = QLayer(d_out, n, g, perm, gbits, codes, scales, zeros, st.as_dict())
+    mc = (C.c_uint64 * 6)()
+    lib().orc_last_midpoint_counts(mc)
+    q.midpoint = dict(zip(MIDPOINT_FIELDS, (int(v) for v in mc)))
+    q.midmap = mmap
+    return q
+
+
+MIDPOINT_FIELDS = ("code_decisions", "code_near", "zero_decisions", "zero_near", "cd_decisions", "cd_near")
 
 
 def gram_accumulate(x, y=None, h=None) -> np.ndarray:
@@ -452,13 +474,17 @@ def synth_outlier_scales(seed: int, n: int, frac: float, factor: float) -> np.nd
     return out
 
 
-def synth_tokens(seed: int, t: int, n: int, ch_scale=None, row0: int = 0) -> np.ndarray:
+def synth_tokens(seed: int, t: int, n: int, ch_scale=None, row0: int = 0, heavy=None) -> np.ndarray:
+    """Token-major t x n inputs; `heavy` (n bools, optional) marks Student-t(3) channels."""
     x = np.empty((t, n), np.float32)
-    cs = None
+    cs = hv = None
     if ch_scale is not None:
         ch_scale = np.ascontiguousarray(ch_scale, np.float32)
         cs = ch_scale.ctypes.data
-    lib().orc_synth_tokens(seed, row0, t, n, cs, x)
+    if heavy is not None:
+        heavy = np.ascontiguousarray(heavy, np.uint8)
+        hv = heavy.ctypes.data
+    lib().orc_synth_tokens_heavy(seed, row0, t, n, cs, hv, x)
     return x
 
 

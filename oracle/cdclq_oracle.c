@@ -147,6 +147,28 @@ float orc_quant_code(float x, float scale, float zero, float maxq, uint8_t* code
   return scale * (q - zero);
 }
 
+/* Near-midpoint accounting (test infrastructure for the parity contract, not a reference step):
+ * the decision clamp(round(num / den) + zero, 0, maxq) counts when num / den in f64 from the same
+ * f32 operands lies within 1e-9 of k + 1/2 and the two candidates differ after clamping. Within
+ * 1e-9 of a midpoint the f32 quotient is the midpoint itself (half an f32 ulp of |v| >= 1/2 is
+ * larger), so it screens the rest out. */
+static int near_midpoint(float num, float den, float zero, float maxq) {
+  const float q = num / den;
+  const float fl = floorf(q);
+  if (q - fl != 0.5f) return 0;
+  const double v = (double)num / (double)den;
+  if (fabs(v - (floor(v) + 0.5)) > 1e-9) return 0;
+  return rs_clampf(fl + zero, 0.0f, maxq) != rs_clampf(fl + 1.0f + zero, 0.0f, maxq);
+}
+
+static uint64_t g_mid[6]; /* code, code_near, zero, zero_near, cd, cd_near of the last quantize_layer */
+void orc_last_midpoint_counts(uint64_t* out) { memcpy(out, g_mid, sizeof g_mid); }
+/* Optional d_out x n map filled by the next orc_quantize_layer calls (NULL: off): bit 0 = the
+ * element's phase-1 code decision was near a midpoint, bit 1 = one of its descent evaluations was,
+ * bit 2 = its group's zero point was (marked on every column of the group). */
+static uint8_t* g_midmap = NULL;
+void orc_set_midpoint_map(uint8_t* map) { g_midmap = map; }
+
 static void grid_mk(float lo, float hi, float maxq, float* s, float* z) {
   float scale = orc_round_f16((hi - lo) / maxq);
   if (scale < F16_MIN_NORMAL) scale = F16_MIN_NORMAL;
@@ -154,7 +176,16 @@ static void grid_mk(float lo, float hi, float maxq, float* s, float* z) {
   *z = rs_clampf(roundf(-lo / scale), 0.0f, maxq);
 }
 
+static void find_params_lo(const float* vals, size_t len, uint32_t bits, int mse, float* s_out, float* z_out,
+                           float* lo_out);
 void orc_find_params(const float* vals, size_t len, uint32_t bits, int mse, float* s_out, float* z_out) {
+  float lo;
+  find_params_lo(vals, len, bits, mse, s_out, z_out, &lo);
+}
+
+/* src/quant.rs:40-83; *lo_out = the lower end of the chosen grid (for the zero point's accounting) */
+static void find_params_lo(const float* vals, size_t len, uint32_t bits, int mse, float* s_out, float* z_out,
+                           float* lo_out) {
   float maxq = (float)((1u << bits) - 1u);
   float xmin = 0.0f, xmax = 0.0f;
   for (size_t k = 0; k < len; ++k) {
@@ -165,7 +196,7 @@ void orc_find_params(const float* vals, size_t len, uint32_t bits, int mse, floa
     xmin = -1.0f;
     xmax = 1.0f;
   }
-  float bs, bz;
+  float bs, bz, blo = xmin;
   grid_mk(xmin, xmax, maxq, &bs, &bz);
   if (mse) {
     float best_err = INFINITY;
@@ -183,11 +214,13 @@ void orc_find_params(const float* vals, size_t len, uint32_t bits, int mse, floa
         best_err = err;
         bs = s;
         bz = z;
+        blo = p * xmin;
       }
     }
   }
   *s_out = bs;
   *z_out = bz;
+  *lo_out = blo;
 }
 
 /* ------------------------------------------------------------------ GEMM (src/linalg.rs:56-184) */
@@ -659,6 +692,7 @@ static int build_prepared(const float* h, size_t n, const uint32_t* perm, const 
 typedef struct {
   double loss_gptq, loss_final;
   size_t sb_total, sb_refined, updates;
+  uint64_t code_near, zero_near, cd_evals, cd_near; /* near-midpoint accounting */
 } chunk_stats;
 
 typedef struct {
@@ -714,7 +748,7 @@ static size_t refit_all(size_t rows, size_t n, size_t ng, size_t g, const float*
 /* src/engine.rs:366-674 */
 static void process_chunk(const float* wt, size_t rows, size_t n, size_t ng, size_t g, const float* u, const float* h,
                           const uint8_t* gbits, const orc_config* cfg, uint8_t* codes, float* scales, float* zeros,
-                          chunk_stats* out) {
+                          chunk_stats* out, uint8_t* midmap) {
   size_t bsz = cfg->block;
   size_t bmin = bsz < n ? bsz : n;
   float* w = (float*)xcalloc(rows * n, sizeof(float));
@@ -740,10 +774,15 @@ static void process_chunk(const float* wt, size_t rows, size_t n, size_t ng, siz
         for (size_t r = 0; r < rows; ++r) {
           for (size_t col = j; col < gend; ++col)
             tmp[col - j] = (col < i2) ? w1[r * cnt + (col - i1)] : w[r * n + col];
-          float s, z;
-          orc_find_params(tmp, gend - j, bits, cfg->mse_grid, &s, &z);
+          float s, z, lo;
+          find_params_lo(tmp, gend - j, bits, cfg->mse_grid, &s, &z, &lo);
           scales[r * ng + gi] = s;
           zeros[r * ng + gi] = z;
+          if (near_midpoint(-lo, s, 0.0f, (float)((1u << bits) - 1u))) {
+            out->zero_near++;
+            if (midmap)
+              for (size_t col = j; col < gend; ++col) midmap[r * n + col] |= 4;
+          }
         }
       }
       size_t gi = j / g;
@@ -756,6 +795,10 @@ static void process_chunk(const float* wt, size_t rows, size_t n, size_t ng, siz
         float wv = w1[r * cnt + i];
         uint8_t c;
         float dq = orc_quant_code(wv, scales[r * ng + gi], zeros[r * ng + gi], maxq, &c);
+        if (near_midpoint(wv, scales[r * ng + gi], zeros[r * ng + gi], maxq)) {
+          out->code_near++;
+          if (midmap) midmap[r * n + j] |= 1;
+        }
         codes[r * n + j] = c;
         wq[r * n + j] = dq;
         float e = (wv - dq) * inv_d;
@@ -863,6 +906,11 @@ static void process_chunk(const float* wt, size_t rows, size_t n, size_t ng, siz
                 float cur = wq[r * n + j];
                 float target = cur + gsr[jj] / hjj;
                 float q = rs_clampf(roundf(target / sc) + z, 0.0f, maxq);
+                out->cd_evals++;
+                if (near_midpoint(target, sc, z, maxq)) {
+                  out->cd_near++;
+                  if (midmap) midmap[r * n + j] |= 2;
+                }
                 float newdq = sc * (q - z);
                 uint8_t qc = (q == q) ? (uint8_t)q : 0;
                 if (qc != codes[r * n + j]) {
@@ -902,7 +950,7 @@ static void process_chunk(const float* wt, size_t rows, size_t n, size_t ng, siz
   free(colloss);
   out->loss_gptq = loss_gptq;
   out->loss_final = loss_gptq + loss_delta;
-  out->sb_total = n_sb;
+  out->sb_total = n_sb;  /* (the near-midpoint counters accumulated above) */
   out->sb_refined = refined;
   out->updates = updates;
 }
@@ -1002,7 +1050,7 @@ int orc_quantize_layer(const float* w, size_t d_out, size_t d_in, const float* h
     size_t r0 = c * rc_rows;
     size_t rows = (d_out - r0 < rc_rows) ? d_out - r0 : rc_rows;
     process_chunk(wp + r0 * n, rows, n, ng, g, U, H32, gbits, cfg, codes + r0 * n, scales + r0 * ng, zeros + r0 * ng,
-                  &cs[c]);
+                  &cs[c], g_midmap ? g_midmap + r0 * n : NULL);
   }
   double secs_quant = now_secs() - t1;
 
@@ -1015,6 +1063,15 @@ int orc_quantize_layer(const float* w, size_t d_out, size_t d_in, const float* h
     st->subblocks_total += cs[c].sb_total;
     st->subblocks_refined += cs[c].sb_refined;
     st->code_updates += cs[c].updates;
+  }
+  memset(g_mid, 0, sizeof g_mid);
+  g_mid[0] = (uint64_t)d_out * n;
+  g_mid[2] = (uint64_t)d_out * ng;
+  for (size_t c = 0; c < nchunks; ++c) {
+    g_mid[1] += cs[c].code_near;
+    g_mid[3] += cs[c].zero_near;
+    g_mid[4] += cs[c].cd_evals;
+    g_mid[5] += cs[c].cd_near;
   }
   st->skeleton_groups = nskel;
   size_t row_bits = 0;
@@ -1197,6 +1254,28 @@ void orc_synth_tokens(uint64_t seed, uint64_t row0, size_t t, size_t n, const fl
   for (size_t r = 0; r < t; ++r)
     for (size_t j = 0; j < n; ++j)
       x[r * n + j] = orc_synth_normal_at(seed, (row0 + r) * (uint64_t)n + j) * (ch_scale ? ch_scale[j] : 1.0f);
+}
+
+/* Student-t(3) draw i: Z / sqrt(chi2_3 / 3), chi2_3 from normals 3i..3i+2 of the stream
+ * mix64(seed ^ 0x7F4A7C159E3779B9) (the benchmark's heavy-tailed channels). */
+float orc_synth_student3_at(uint64_t seed, uint64_t i) {
+  const uint64_t s2 = mix64(seed ^ 0x7F4A7C159E3779B9ULL);
+  const double z = (double)orc_synth_normal_at(seed, i);
+  const double a = (double)orc_synth_normal_at(s2, 3 * i), b = (double)orc_synth_normal_at(s2, 3 * i + 1),
+               c = (double)orc_synth_normal_at(s2, 3 * i + 2);
+  const double chi = a * a + b * b + c * c;
+  return (float)(z * sqrt(3.0 / chi));
+}
+
+void orc_synth_tokens_heavy(uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale,
+                            const uint8_t* heavy, float* x) {
+#pragma omp parallel for schedule(static)
+  for (size_t r = 0; r < t; ++r)
+    for (size_t j = 0; j < n; ++j) {
+      const uint64_t i = (row0 + r) * (uint64_t)n + j;
+      const float v = (heavy && heavy[j]) ? orc_synth_student3_at(seed, i) : orc_synth_normal_at(seed, i);
+      x[r * n + j] = v * (ch_scale ? ch_scale[j] : 1.0f);
+    }
 }
 
 /* ------------------------------------------------------------------ packed container (cdclq-v1)

@@ -173,6 +173,15 @@ void orc_synth_normal(uint64_t seed, uint64_t offset, size_t n, float sigma, flo
 void orc_synth_outlier_scales(uint64_t seed, size_t n, double frac, float factor, float* scales);
 /* X (t x n, token-major): x[r][j] = normal_at(seed, (row0 + r)*n + j) * ch_scale[j]. */
 void orc_synth_tokens(uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale, float* x);
+float orc_synth_student3_at(uint64_t seed, uint64_t i);
+/* Near-midpoint accounting of the last orc_quantize_layer call: code decisions, near; zero-point
+ * decisions, near; descent evaluations, near (same definitions as cdclq_midpoint_counts). */
+void orc_last_midpoint_counts(uint64_t* out);
+/* d_out x n map of near-midpoint decisions filled by the next orc_quantize_layer calls (NULL: off):
+ * bit 0 phase-1 code, bit 1 a descent evaluation, bit 2 the group's zero point. */
+void orc_set_midpoint_map(uint8_t* map);
+void orc_synth_tokens_heavy(uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale,
+                            const uint8_t* heavy, float* x);
 double orc_synth_log(double x);
 double orc_synth_cos2pi(double u);
 

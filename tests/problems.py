@@ -143,3 +143,45 @@ def gemm_order_failures() -> list:
         if O.sgemm(a, a.T.copy())[0, 0] != np.float32(2.0 ** 24 + 256.0 * (full - 1) + rem):
             bad.append(f"sgemm KC panels, k {k}")
     return bad
+
+
+def row_chunk(d_out: int, row_chunk_cfg: int, nthreads: int) -> int:
+    """The reference's row-chunk size (src/engine.rs:768-770)."""
+    if row_chunk_cfg > 0:
+        rc = row_chunk_cfg
+    else:
+        rc = min(max(-(-d_out // max(nthreads, 1)), 32), 256)
+    return max(min(rc, d_out), 1)
+
+
+def classify_mismatches(got_codes, want_codes, midmap, rc: int) -> dict:
+    """Near-midpoint classification of code mismatches (the parity contract's exemption).
+
+    A mismatching element whose oracle decision was near a midpoint (any bit of `midmap`, see
+    oracle.quantize_layer) is exempt: there the reference's own rounding input lies within 1e-9 of
+    k + 1/2. Other mismatches in a row chunk of `rc` rows that holds an exempt one are cascaded: a
+    different code changes that row's later errors and gradients, and the chunk's shared
+    convergence decisions reach its other rows. The rest are non-exempt, i.e. real differences.
+    Returns counts: mismatches, exempt, cascaded, non_exempt, rows (with a mismatch), exempt_chunks."""
+    bad = np.asarray(got_codes) != np.asarray(want_codes)
+    rows = np.nonzero(bad.any(axis=1))[0]
+    ex = bad & (np.asarray(midmap) != 0)
+    ex_chunks = set((np.nonzero(ex.any(axis=1))[0] // rc).tolist())
+    total, n_ex = int(bad.sum()), int(ex.sum())
+    casc = sum(int(bad[r].sum() - ex[r].sum()) for r in rows if r // rc in ex_chunks)
+    return dict(mismatches=total, exempt=n_ex, cascaded=casc, non_exempt=total - n_ex - casc, rows=int(len(rows)),
+                exempt_chunks=len(ex_chunks))
+
+
+def tie_problem(d_out: int = 48, n: int = 256, g: int = 64, seed: int = 5):
+    """A layer whose rounding decisions sit exactly on midpoints: every weight is (k + 1/2) 2^-6 and
+    every group spans -4.5 2^-6 .. 10.5 2^-6, so with 4 bits the scale is exactly 2^-6 and each
+    x / scale (codes) and -lo / scale (zero points) is an f32 tie; H is diagonal, so the phase-1
+    compensation and the descent targets leave the weights on the ties. Natural order, g | n."""
+    rng = np.random.default_rng(seed)
+    w = ((rng.integers(-5, 11, (d_out, n)) + 0.5) * 2.0 ** -6).astype(np.float32)
+    for c0 in range(0, n, g):
+        w[:, c0] = np.float32(-4.5 * 2.0 ** -6)
+        w[:, c0 + 1] = np.float32(10.5 * 2.0 ** -6)
+    h = np.diag(rng.uniform(0.5, 2.0, n)).astype(np.float32)
+    return w, h
