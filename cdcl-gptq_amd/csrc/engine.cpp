@@ -200,10 +200,6 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
   const int ng = (n + g - 1) / g;
   const int bsz = (int)std::min<uint64_t>(cfg->block, (uint64_t)n);
   const int sbw = (int)std::min<uint64_t>(cfg->sub_block, (uint64_t)n);
-  if (std::min<uint64_t>(cfg->block, n_) > 1024)
-    return fail(ctx, CDCLQ_INVALID_ARG, "block > 1024 columns is not supported by the GPU block sweep");
-  if (cfg->method == CDCLQ_METHOD_CDCL && std::min<uint64_t>(cfg->sub_block, n_) > 1024)
-    return fail(ctx, CDCLQ_INVALID_ARG, "sub_block > 1024 columns is not supported by the GPU repair sweep");
   hipStream_t st = ctx->st;
   HIPCK(hipSetDevice(ctx->device));
   const double t0 = now_secs();

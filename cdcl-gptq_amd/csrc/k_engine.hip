@@ -258,6 +258,109 @@ __global__ __launch_bounds__(64 * GB_ROWS) void k_gptq_block(int rows, int n, in
   }
 }
 
+// Phase-1 block sweep for blocks wider than 1024 columns (the register kernel above holds at most
+// 16 values per lane). Same per-element operations and order; the block's working values live in
+// the row of w itself (columns i1..i2, dead after the block: the lazy update reads only columns
+// >= i2), and each column step reads what the previous steps wrote. One wavefront per row, four
+// rows per workgroup. A lane's stores are ordered before the wave's next loads by a workgroup-scope
+// fence (all lanes of a wave share the CU's vector cache).
+__global__ __launch_bounds__(256) void k_gptq_block_mem(int rows, int n, int i1, int cnt, int g, int ng,
+                                                        float* __restrict__ w, const float* __restrict__ u,
+                                                        const float* __restrict__ invd,
+                                                        const uint8_t* __restrict__ gbits, int mse,
+                                                        float* __restrict__ scales, float* __restrict__ zeros,
+                                                        uint8_t* __restrict__ codes, float* __restrict__ wq,
+                                                        float* __restrict__ err, unsigned long long* __restrict__ mid) {
+  const int lane = threadIdx.x & 63;
+  const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (r >= rows) return;
+  float* wr = w + (long)r * n;
+  float sc = 0.0f, zr = 0.0f, maxq = 0.0f;
+  unsigned near_codes = 0, near_zeros = 0;
+  if (i1 % g != 0) {
+    const int gi = i1 / g;
+    sc = scales[(long)r * ng + gi];
+    zr = zeros[(long)r * ng + gi];
+    maxq = (float)((1u << gbits[gi]) - 1u);
+  }
+  for (int i = 0; i < cnt; ++i) {
+    const int j = i1 + i;
+    if (j % g == 0) {
+      // group grid from the current values of columns j..gend: in-block columns hold the working
+      // values, columns >= i2 the full-width values (src/engine.rs:410-423)
+      const int gi = j / g;
+      const int gend = min(j + g, n);
+      maxq = (float)((1u << gbits[gi]) - 1u);
+      float lmin = INFINITY, lmax = -INFINITY;
+      for (int col = j + lane; col < gend; col += 64) {
+        const float v = wr[col];
+        lmin = rs_minf(lmin, v);
+        lmax = rs_maxf(lmax, v);
+      }
+      float xmin = rs_minf(0.0f, wave_min(lmin));
+      float xmax = rs_maxf(0.0f, wave_max(lmax));
+      if (xmin == 0.0f && xmax == 0.0f) {
+        xmin = -1.0f;
+        xmax = 1.0f;
+      }
+      grid_mk(xmin, xmax, maxq, &sc, &zr);
+      float lo_used = xmin;
+      if (mse) {  // one candidate per lane, sequential error sum in column order (src/quant.rs:65-81)
+        const int cand = lane < 24 ? lane : 0;
+        const float p = 1.0f - 0.02f * (float)cand;
+        float cs, cz;
+        grid_mk(p * xmin, p * xmax, maxq, &cs, &cz);
+        float errs = 0.0f;
+        for (int col = j; col < gend; ++col) {
+          const float v = wr[col];
+          float qq;
+          const float d = quant_dq(v, cs, cz, maxq, &qq);
+          const float ee = d - v;
+          errs = errs + ee * ee;
+        }
+        float be = (lane < 24 && errs == errs) ? errs : INFINITY;
+        int bc = (lane < 24) ? lane : (1 << 20);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          const float oe = __shfl_xor(be, o, 64);
+          const int oc = __shfl_xor(bc, o, 64);
+          if (oe < be || (oe == be && oc < bc)) {
+            be = oe;
+            bc = oc;
+          }
+        }
+        bc = readlane_i(bc, 0);
+        sc = readlane(cs, bc);
+        zr = readlane(cz, bc);
+        lo_used = (1.0f - 0.02f * (float)bc) * xmin;
+      }
+      near_zeros += near_midpoint(-lo_used, sc, 0.0f, maxq) ? 1u : 0u;
+      if (lane == 0) {
+        scales[(long)r * ng + gi] = sc;
+        zeros[(long)r * ng + gi] = zr;
+      }
+    }
+    const float xv = wr[j];
+    float q;
+    const float dq = quant_dq(xv, sc, zr, maxq, &q);
+    near_codes += near_midpoint(xv, sc, zr, maxq) ? 1u : 0u;
+    const float e = (xv - dq) * invd[j];
+    if (lane == 0) {
+      const long o = (long)r * n + j;
+      codes[o] = code_of(q);
+      wq[o] = dq;
+      err[o] = e;
+    }
+    const float* urow = u + (long)j * n;
+    for (int c = j + 1 + lane; c < i1 + cnt; c += 64) wr[c] = wr[c] - e * urow[c];
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  }
+  if (lane == 0 && (near_codes | near_zeros)) {
+    if (near_codes) atomicAdd(&mid[MID_CODE_NEAR], (unsigned long long)near_codes);
+    if (near_zeros) atomicAdd(&mid[MID_ZERO_NEAR], (unsigned long long)near_zeros);
+  }
+}
+
 // colloss[chunk][j] = sum over the chunk's rows, in row order, of (f64)(eps*eps) (src/engine.rs:438).
 __global__ __launch_bounds__(256) void k_colloss(int rows, int n, int rc, const float* __restrict__ err,
                                                  double* __restrict__ out) {
@@ -486,8 +589,10 @@ hipError_t gptq_block(hipStream_t st, int rows, int n, int i1, int cnt, int g, i
     GPTQ_CASE(4)
     GPTQ_CASE(8)
     GPTQ_CASE(16)
-    default:
-      return hipErrorInvalidValue;
+    default:  // wider than 1024 columns: the working values stay in w
+      hipLaunchKernelGGL(k_gptq_block_mem, dim3((rows + 3) / 4), dim3(256), 0, st, rows, n, i1, cnt, g, ng, w, u, invd,
+                         gbits, mse, scales, zeros, codes, wq, err, mid);
+      break;
   }
 #undef GPTQ_CASE
   return hipGetLastError();

@@ -996,6 +996,92 @@ __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int 
   }
 }
 
+// Coordinate descent for sub-blocks wider than 1024 columns (k_cd keeps at most 16 columns per
+// lane). Same decisions, order and accounting as k_cd; the row's gradient lives in G (this step's
+// buffer, updated in place) and the per-column state in wq / e / codes, visited 64 columns at a
+// time. After a move the whole gradient row is updated in memory and the current slice reloaded;
+// a workgroup-scope fence orders the wave's stores before its next loads.
+__global__ __launch_bounds__(256) void k_cd_mem(int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb,
+                                                int rc, int sweeps, float* __restrict__ G,
+                                                const float* __restrict__ h32, const uint8_t* __restrict__ gbits,
+                                                const float* __restrict__ scales, const float* __restrict__ zeros,
+                                                uint8_t* __restrict__ codes, float* __restrict__ wq,
+                                                float* __restrict__ e, const uint8_t* __restrict__ active,
+                                                const uint8_t* __restrict__ sel, double* __restrict__ dlog,
+                                                uint32_t* __restrict__ dcnt, int cap,
+                                                unsigned long long* __restrict__ mid, uint32_t* __restrict__ evals) {
+  const int lane = threadIdx.x & 63;
+  const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (r >= rows) return;
+  const int chunk = r / rc;
+  if (!active[chunk] || !sel[(long)chunk * nsb + sb]) {
+    if (lane == 0) dcnt[r] = 0;
+    return;
+  }
+  float* gr = G + (long)r * wd;
+  uint32_t moves = 0, nevals = 0, nnear = 0;
+  double* dl = dlog + (long)r * cap;
+  for (int sw = 0; sw < sweeps; ++sw) {
+    bool changed = false;
+    for (int s0 = 0; s0 < wd; s0 += 64) {
+      const int k = s0 + lane;
+      const bool in = k < wd;
+      const int j = c0 + min(k, wd - 1);
+      const long o = (long)r * n + j;
+      const int gi = j / g;
+      const float hd = h32[(long)j * n + j], sc = scales[(long)r * ng + gi], zz = zeros[(long)r * ng + gi];
+      const float mq = (float)((1u << gbits[gi]) - 1u);
+      float mwq = in ? wq[o] : 0.0f, me = in ? e[o] : 0.0f;
+      int mc = in ? (int)codes[o] : 0;
+      float gg = in ? gr[k] : 0.0f;
+      const uint64_t inmask = __ballot(in);
+      int start = 0;
+      while (start < 64) {
+        const float target = mwq + gg / hd;
+        float qv;
+        const float newdq = quant_dq(target, sc, zz, mq, &qv);
+        const int qc = (int)code_of(qv);
+        const uint64_t mask = __ballot(in && lane >= start && qc != mc);
+        const int last = mask ? (int)__builtin_ctzll(mask) : 63;
+        const uint64_t seen = (~0ull << start) & (last == 63 ? ~0ull : ((1ull << (last + 1)) - 1ull)) & inmask;
+        nevals += (uint32_t)__builtin_popcountll(seen);
+        nnear += (uint32_t)__builtin_popcountll(__ballot(near_midpoint(target, sc, zz, mq)) & seen);
+        if (mask == 0) break;
+        const int jl = __builtin_amdgcn_readfirstlane(__builtin_ctzll(mask));
+        const float cur = readlane(mwq, jl);
+        const float nd = readlane(newdq, jl);
+        const float gj = readlane(gg, jl);
+        const float hjj = readlane(hd, jl);
+        const float de = cur - nd;
+        const float d32 = (2.0f * de) * gj + (de * de) * hjj;
+        if (lane == 0) dl[moves] = (double)d32;
+        ++moves;
+        if (lane == jl) {
+          mwq = nd;
+          mc = qc;
+          me = me + de;
+          wq[o] = mwq;
+          e[o] = me;
+          codes[o] = (uint8_t)mc;
+        }
+        // g_k = g_k + de * H[j, c0 + k] over the whole sub-block row (src/engine.rs:641-646)
+        const float* hrow = h32 + (long)(c0 + s0 + jl) * n + c0;
+        for (int k2 = lane; k2 < wd; k2 += 64) gr[k2] = gr[k2] + de * hrow[k2];
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        gg = in ? gr[k] : 0.0f;
+        changed = true;
+        start = jl + 1;
+      }
+    }
+    if (!changed) break;
+  }
+  if (lane == 0) {
+    dcnt[r] = moves;
+    evals[r] += nevals;
+    if (nnear) atomicAdd(&mid[MID_CD_NEAR], (unsigned long long)nnear);
+  }
+}
+
 int npl_for(int cnt) {
   if (cnt <= 64) return 1;
   if (cnt <= 128) return 2;
@@ -1184,7 +1270,7 @@ hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, i
 }
 
 hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
-                       int sweeps, const float* G, const float* h32, const uint8_t* gbits, const float* scales,
+                       int sweeps, float* G, const float* h32, const uint8_t* gbits, const float* scales,
                        const float* zeros, uint8_t* codes, float* wq, float* e, const uint8_t* active,
                        const uint8_t* sel, double* dlog, uint32_t* dcnt, int cap, unsigned long long* mid,
                        uint32_t* evals) {
@@ -1198,7 +1284,10 @@ hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, i
     case 4: CD_CASE(4); break;
     case 8: CD_CASE(8); break;
     case 16: CD_CASE(16); break;
-    default: return hipErrorInvalidValue;
+    default:  // wider than 1024 columns: gradient row and column state in memory
+      hipLaunchKernelGGL(k_cd_mem, grid, blk, 0, st, rows, n, ng, g, c0, wd, sb, nsb, rc, sweeps, G,
+                         h32, gbits, scales, zeros, codes, wq, e, active, sel, dlog, dcnt, cap, mid, evals);
+      break;
   }
 #undef CD_CASE
   return hipGetLastError();

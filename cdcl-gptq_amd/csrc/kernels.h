@@ -100,7 +100,7 @@ hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, i
                        const float* h32, const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
                        const uint8_t* active, double* dlog, uint32_t* dcnt);
 hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
-                       int sweeps, const float* G, const float* h32, const uint8_t* gbits, const float* scales,
+                       int sweeps, float* G, const float* h32, const uint8_t* gbits, const float* scales,
                        const float* zeros, uint8_t* codes, float* wq, float* e, const uint8_t* active,
                        const uint8_t* sel, double* dlog, uint32_t* dcnt, int cap, unsigned long long* mid,
                        uint32_t* evals);

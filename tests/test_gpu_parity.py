@@ -319,6 +319,17 @@ def test_quantize_wide_gradient_tiles(ctx):
                 label="wide gradient tiles")
 
 
+@pytest.mark.parametrize("block,group,sub_block,mse", [(2048, 128, 1280, False), (1536, 1536, 1100, True),
+                                                       (4096, 0, 64, False)])
+def test_quantize_blocks_wider_than_1024(ctx, block, group, sub_block, mse):
+    """block and sub_block above 1024 columns (the reference accepts any value > 0,
+    src/engine.rs:244): the sweeps keep the working values in memory instead of registers, with the
+    same per-element operations. n = 3072 gives a ragged last block / sub-block."""
+    w, x, h, _ = synth_layer(61 + block % 7, 40, 3072, 3500)
+    assert_same(*run_both(ctx, w, h, bits=3, group=group, block=block, sub_block=sub_block, act_order=True,
+                          mse_grid=mse, row_chunk=16, passes=2), label=f"B{block} g{group} sb{sub_block}")
+
+
 def test_quantize_skeleton_and_dead_columns(ctx):
     w, x, h, _ = synth_layer(33, 64, 256, 800)
     h = h.copy()
