@@ -618,8 +618,11 @@ int gram_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const f
   // Jobs whose tiles are all interior go to the direct-to-LDS kernel, the rest to k_gram_mfma.
   std::vector<int4> tiles[2];
   for (size_t i = 0; i < jobs.size(); ++i) {
-    const int kind = gram_dma_eligible(jobs[i].n, jobs[i].t, jobs[i].x, jobs[i].y) ? 1 : 0;
-    gram_mfma_tiles((int)i, jobs[i].n, jobs[i].x == jobs[i].y && flags[4 * i] == 0, tiles[kind]);
+    const bool sym = jobs[i].x == jobs[i].y && flags[4 * i] == 0;
+    if (gram_dma_eligible(jobs[i].n, jobs[i].t, jobs[i].x, jobs[i].y))
+      gram_dma_tiles((int)i, jobs[i].n, sym, tiles[1]);
+    else
+      gram_mfma_tiles((int)i, jobs[i].n, sym, tiles[0]);
   }
   // XCD-aware order: workgroup w runs on XCD w % 8, so give each XCD a contiguous run of tiles
   // (neighbouring tiles share X stripes in that XCD's L2).

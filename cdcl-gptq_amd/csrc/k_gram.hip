@@ -201,50 +201,49 @@ __global__ __launch_bounds__(256, 2) void k_gram_mfma(const GramJob* __restrict_
 }
 
 // Direct-to-LDS variant for jobs whose tiles are all interior and whose token count is a multiple
-// of KT (n % 128 == 0, T % 32 == 0, 16-byte aligned rows; every config-4 input). The workgroup's
-// stages are filled with global_load_lds_dwordx4 (lane L's 16 bytes land at the instruction's LDS
-// base + 16 L), so no registers hold prefetched data and no LDS stores are issued; a ring of DNB
-// stages keeps two stages in flight behind the one being multiplied, with one barrier per stage.
-// Arithmetic, per-element operation order, panel and chunk folds are those of k_gram_mfma.
-constexpr int DNB = 3;                   // stages in the ring
-constexpr int DSTAGE = KT * (TI + TJ);   // floats per stage: X [32][128], Y [32][64]
-constexpr int DPW = DSTAGE / 256 / 4;    // 1 KB load instructions per wave and stage (6)
+// of KT (n % 128 == 0, T % 32 == 0, 16-byte aligned rows; every config-4 input). A 512-thread
+// workgroup owns a 128 x 128 tile (one per CU): wave w holds rows 64 (w >> 2) .. +63 x columns
+// 32 (w & 3) .. +31 as one 2-block K=1 accumulator, two waves per SIMD. Stages are filled with
+// global_load_lds_dwordx4 (lane L's 16 bytes land at the instruction's LDS base + 16 L), so no
+// registers hold prefetched data and no LDS stores are issued; a ring of three stages keeps two in
+// flight behind the one being multiplied, one bare barrier per stage. The wider tile streams X once
+// per 128 x 128 outputs instead of per 128 x 64 (a third less traffic per flop than k_gram_mfma's
+// tiles). Arithmetic, per-element operation order, panel and chunk folds are those of k_gram_mfma.
+constexpr int DTJ = 128;                  // tile columns
+constexpr int DSTAGE = KT * (TI + DTJ);   // floats per stage: X [32][128], Y [32][128]
+constexpr int DPW = DSTAGE / 512 / 4;     // 1 KB load instructions per wave and stage (4)
 
-__global__ __launch_bounds__(256, 2) void k_gram_dma(const GramJob* __restrict__ jobs,
+__global__ __launch_bounds__(512, 1) void k_gram_dma(const GramJob* __restrict__ jobs,
                                                      const int4* __restrict__ tiles) {
-  __shared__ float R[DNB][DSTAGE];
+  __shared__ float R[3][DSTAGE];
   const int4 tl = tiles[blockIdx.x];
   const GramJob jb = jobs[tl.x];
   const int n = jb.n, T = jb.t;
   __attribute__((address_space(1))) double* H = (__attribute__((address_space(1))) double*)jb.h;
-  const int i0 = tl.y * TI, j0 = tl.z * TJ;
+  const int i0 = tl.y * TI, j0 = tl.z * DTJ;
   const bool mirror = tl.w != 0;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int wi = wv >> 1, wj = wv & 1;
-  const int rbase = i0 + 64 * wi + 4 * (lane >> 5);
-  const int col = j0 + 32 * wj + (lane & 31);
+  const int wr = wv >> 2, wc = wv & 3;
+  const int rbase = i0 + 64 * wr + 4 * (lane >> 5);
+  const int col = j0 + 32 * wc + (lane & 31);
   double h[32];
 #pragma unroll
   for (int r = 0; r < 32; ++r) h[r] = H[(long)(rbase + 32 * (r >> 4) + 8 * ((r & 15) >> 2) + (r & 3)) * n + col];
-  // Stage layout: X [32 tokens][128 cols] (instructions 0..15, two tokens each: lane -> token
-  // lane >> 5, columns 4 (lane & 31)), then Y [32][64] (instructions 16..23, four tokens each:
-  // lane -> token lane >> 4, columns 4 (lane & 15)). Wave w issues instructions w, w + 4, ...
+  // Stage layout: X [32 tokens][128 rows] (instructions 0..15), then Y [32][128 cols]
+  // (instructions 16..31); instruction q: lane -> token 2 (q & 15) + (lane >> 5), columns
+  // 4 (lane & 31). Wave w issues instructions w, w + 8, w + 16, w + 24.
   const float* src[DPW];
   int dst[DPW];
 #pragma unroll
   for (int q = 0; q < DPW; ++q) {
-    const int ins = wv + 4 * q;
-    if (ins < 16) {
-      src[q] = jb.x + (long)(2 * ins + (lane >> 5)) * n + i0 + 4 * (lane & 31);
-      dst[q] = 256 * ins;
-    } else {
-      src[q] = jb.y + (long)(4 * (ins - 16) + (lane >> 4)) * n + j0 + 4 * (lane & 15);
-      dst[q] = 256 * ins;
-    }
+    const int ins = wv + 8 * q;
+    const int tok = 2 * (ins & 15) + (lane >> 5);
+    src[q] = (ins < 16 ? jb.x + i0 : jb.y + j0) + (long)tok * n + 4 * (lane & 31);
+    dst[q] = 256 * ins;
   }
   const int nstage = T / KT;
   auto issue = [&](int s) {
-    float* buf = &R[s % DNB][0];
+    float* buf = &R[s % 3][0];
     const long t0n = (long)s * KT * n;
 #pragma unroll
     for (int q = 0; q < DPW; ++q) dma16(src[q] + t0n, buf + dst[q]);
@@ -265,10 +264,10 @@ __global__ __launch_bounds__(256, 2) void k_gram_dma(const GramJob* __restrict__
     // a bare barrier: a fenced one would also wait for the next stage's loads still in flight
     __builtin_amdgcn_s_barrier();
     if (s + 2 < nstage) issue(s + 2);  // into the buffer of stage s - 1
-    const float* xs = &R[s % DNB][64 * wi + lane];
-    const float* ys = &R[s % DNB][KT * TI + 32 * wj + (lane & 31)];
+    const float* xs = &R[s % 3][64 * wr + lane];
+    const float* ys = &R[s % 3][KT * TI + 32 * wc + (lane & 31)];
 #pragma unroll
-    for (int kk = 0; kk < KT; ++kk) acc = mfma32(xs[kk * TI], ys[kk * TJ], acc);
+    for (int kk = 0; kk < KT; ++kk) acc = mfma32(xs[kk * TI], ys[kk * DTJ], acc);
     const int tn = (s + 1) * KT;
     if ((tn % CDCLQ_KC) == 0 || tn >= T) {  // panel end: tmp = fma(1, chain, tmp)
 #pragma unroll
@@ -340,8 +339,14 @@ hipError_t gram_mfma(hipStream_t st, const GramJob* jobs, const int4* tiles, int
 
 hipError_t gram_dma(hipStream_t st, const GramJob* jobs, const int4* tiles, int ntiles) {
   if (ntiles <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_gram_dma, dim3(ntiles), dim3(256), 0, st, jobs, tiles);
+  hipLaunchKernelGGL(k_gram_dma, dim3(ntiles), dim3(512), 0, st, jobs, tiles);
   return hipGetLastError();
+}
+
+void gram_dma_tiles(int job, int n, bool sym, std::vector<int4>& out) {
+  const int nb = n / TI;  // n % 128 == 0 for these jobs
+  for (int I = 0; I < nb; ++I)
+    for (int J = sym ? I : 0; J < nb; ++J) out.push_back(make_int4(job, I, J, (sym && J != I) ? 1 : 0));
 }
 
 bool gram_dma_eligible(int n, int t, const void* x, const void* y) {

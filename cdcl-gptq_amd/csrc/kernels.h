@@ -33,8 +33,10 @@ struct GramJob {
 // Appends the workgroup tiles of job `job` (int4: job, row block of 128, col block of 64,
 // mirror flag). `sym`: Y == X and the incoming H is symmetric.
 void gram_mfma_tiles(int job, int n, bool sym, std::vector<int4>& out);
-// direct-to-LDS gram for jobs that satisfy gram_dma_eligible (all tiles interior, T % 32 == 0)
+// direct-to-LDS gram for jobs that satisfy gram_dma_eligible (all tiles interior, T % 32 == 0), on
+// 128 x 128 tiles (int4: job, row block of 128, col block of 128, mirror flag)
 hipError_t gram_dma(hipStream_t st, const GramJob* jobs, const int4* tiles, int ntiles);
+void gram_dma_tiles(int job, int n, bool sym, std::vector<int4>& out);
 bool gram_dma_eligible(int n, int t, const void* x, const void* y);
 hipError_t gram_mfma(hipStream_t st, const GramJob* jobs, const int4* tiles, int ntiles, bool vec4);
 hipError_t sym_check(hipStream_t st, int n, const double* h, int* flag);
