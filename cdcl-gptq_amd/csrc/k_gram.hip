@@ -201,21 +201,26 @@ __global__ __launch_bounds__(256, 2) void k_gram_mfma(const GramJob* __restrict_
 }
 
 // Direct-to-LDS variant for jobs whose tiles are all interior and whose token count is a multiple
-// of KT (n % 128 == 0, T % 32 == 0, 16-byte aligned rows; every config-4 input). A 512-thread
+// of DKT (n % 128 == 0, T % 64 == 0, 16-byte aligned rows; every config-4 input). A 512-thread
 // workgroup owns a 128 x 128 tile (one per CU): wave w holds rows 64 (w >> 2) .. +63 x columns
-// 32 (w & 3) .. +31 as one 2-block K=1 accumulator, two waves per SIMD. Stages are filled with
-// global_load_lds_dwordx4 (lane L's 16 bytes land at the instruction's LDS base + 16 L), so no
-// registers hold prefetched data and no LDS stores are issued; a ring of three stages keeps two in
-// flight behind the one being multiplied, one bare barrier per stage. The wider tile streams X once
-// per 128 x 128 outputs instead of per 128 x 64 (a third less traffic per flop than k_gram_mfma's
-// tiles). Arithmetic, per-element operation order, panel and chunk folds are those of k_gram_mfma.
+// 32 (w & 3) .. +31 as one 2-block K=1 accumulator, two waves per SIMD. Stages of 64 tokens are
+// filled with global_load_lds_dwordx4 (lane L's 16 bytes land at the instruction's LDS base + 16 L),
+// so no registers hold prefetched data and no LDS stores are issued; two stages (128 KB) alternate,
+// the next one loading while the current one is multiplied, one bare barrier per stage. Within a
+// stage each wave reads its operands two token pairs ahead of the matrix core (the issue order is
+// pinned, so an LDS read's latency hides behind the two MFMA pairs before its use). The wider tile
+// streams X once per 128 x 128 outputs instead of per 128 x 64 (a third less traffic per flop than
+// k_gram_mfma's tiles). Arithmetic, per-element operation order, panel and chunk folds are those of
+// k_gram_mfma.
 constexpr int DTJ = 128;                  // tile columns
-constexpr int DSTAGE = KT * (TI + DTJ);   // floats per stage: X [32][128], Y [32][128]
-constexpr int DPW = DSTAGE / 512 / 4;     // 1 KB load instructions per wave and stage (4)
+constexpr int DKT = 64;                   // tokens per stage
+constexpr int DSTAGE = DKT * (TI + DTJ);  // floats per stage: X [64][128], Y [64][128]
+constexpr int DPW = DSTAGE / 512 / 4;     // 1 KB load instructions per wave and stage (8)
+constexpr int DLA = 2;                    // token pairs read ahead of the matrix core
 
 __global__ __launch_bounds__(512, 1) void k_gram_dma(const GramJob* __restrict__ jobs,
                                                      const int4* __restrict__ tiles) {
-  __shared__ float R[3][DSTAGE];
+  __shared__ float R[2][DSTAGE];
   const int4 tl = tiles[blockIdx.x];
   const GramJob jb = jobs[tl.x];
   const int n = jb.n, T = jb.t;
@@ -229,46 +234,62 @@ __global__ __launch_bounds__(512, 1) void k_gram_dma(const GramJob* __restrict__
   double h[32];
 #pragma unroll
   for (int r = 0; r < 32; ++r) h[r] = H[(long)(rbase + 32 * (r >> 4) + 8 * ((r & 15) >> 2) + (r & 3)) * n + col];
-  // Stage layout: X [32 tokens][128 rows] (instructions 0..15), then Y [32][128 cols]
-  // (instructions 16..31); instruction q: lane -> token 2 (q & 15) + (lane >> 5), columns
-  // 4 (lane & 31). Wave w issues instructions w, w + 8, w + 16, w + 24.
+  // Stage layout: X [64 tokens][128 rows] (instructions 0..31), then Y [64][128 cols]
+  // (instructions 32..63); instruction q: lane -> token 2 (q & 31) + (lane >> 5), columns
+  // 4 (lane & 31). Wave w issues instructions w, w + 8, ..., w + 56.
   const float* src[DPW];
   int dst[DPW];
 #pragma unroll
   for (int q = 0; q < DPW; ++q) {
     const int ins = wv + 8 * q;
-    const int tok = 2 * (ins & 15) + (lane >> 5);
-    src[q] = (ins < 16 ? jb.x + i0 : jb.y + j0) + (long)tok * n + 4 * (lane & 31);
+    const int tok = 2 * (ins & 31) + (lane >> 5);
+    src[q] = (ins < 32 ? jb.x + i0 : jb.y + j0) + (long)tok * n + 4 * (lane & 31);
     dst[q] = 256 * ins;
   }
-  const int nstage = T / KT;
+  const int nstage = T / DKT;
   auto issue = [&](int s) {
-    float* buf = &R[s % 3][0];
-    const long t0n = (long)s * KT * n;
+    float* buf = &R[s & 1][0];
+    const long t0n = (long)s * DKT * n;
 #pragma unroll
     for (int q = 0; q < DPW; ++q) dma16(src[q] + t0n, buf + dst[q]);
   };
   issue(0);
-  if (nstage > 1) issue(1);
   v32f acc = {};
   float tmp[32];
 #pragma unroll
   for (int r = 0; r < 32; ++r) tmp[r] = 0.0f;
   for (int s = 0; s < nstage; ++s) {
-    // this wave's part of stage s has landed once at most stage s + 1's loads are outstanding;
-    // the barrier then publishes every wave's part and retires all reads of stage s - 1
-    if (s + 1 < nstage)
-      wait_vmcnt<DPW>();
-    else
-      wait_vmcnt<0>();
-    // a bare barrier: a fenced one would also wait for the next stage's loads still in flight
+    // this wave's part of stage s has landed; the barrier publishes every wave's part and retires
+    // all reads of stage s - 1, whose buffer the next stage's loads then fill
+    wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
-    if (s + 2 < nstage) issue(s + 2);  // into the buffer of stage s - 1
-    const float* xs = &R[s % 3][64 * wr + lane];
-    const float* ys = &R[s % 3][KT * TI + 32 * wc + (lane & 31)];
+    if (s + 1 < nstage) issue(s + 1);
+    const float* xs = &R[s & 1][64 * wr + lane];
+    const float* ys = &R[s & 1][DKT * TI + 32 * wc + (lane & 31)];
+    float a0[DKT / 2], a1[DKT / 2], b0[DKT / 2], b1[DKT / 2];
+    auto ld = [&](int p) {
+      a0[p] = xs[(2 * p) * TI];
+      a1[p] = xs[(2 * p + 1) * TI];
+      b0[p] = ys[(2 * p) * DTJ];
+      b1[p] = ys[(2 * p + 1) * DTJ];
+    };
 #pragma unroll
-    for (int kk = 0; kk < KT; ++kk) acc = mfma32(xs[kk * TI], ys[kk * DTJ], acc);
-    const int tn = (s + 1) * KT;
+    for (int p = 0; p < DLA; ++p) ld(p);
+#pragma unroll
+    for (int p = 0; p < DKT / 2; ++p) {
+      if (p + DLA < DKT / 2) ld(p + DLA);
+      acc = mfma32(a0[p], b0[p], acc);
+      acc = mfma32(a1[p], b1[p], acc);
+    }
+    // issue order: the first DLA pairs' reads, then per pair the reads DLA ahead and its 2 MFMAs
+#pragma unroll
+    for (int p = 0; p < DLA; ++p) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+    for (int p = 0; p < DKT / 2; ++p) {
+      if (p + DLA < DKT / 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+    const int tn = (s + 1) * DKT;
     if ((tn % CDCLQ_KC) == 0 || tn >= T) {  // panel end: tmp = fma(1, chain, tmp)
 #pragma unroll
       for (int r = 0; r < 32; ++r) tmp[r] = __builtin_fmaf(1.0f, acc[r], tmp[r]);
@@ -350,7 +371,7 @@ void gram_dma_tiles(int job, int n, bool sym, std::vector<int4>& out) {
 }
 
 bool gram_dma_eligible(int n, int t, const void* x, const void* y) {
-  return n % 128 == 0 && t % KT == 0 && t > 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0;
+  return n % 128 == 0 && t % DKT == 0 && t > 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0;
 }
 
 hipError_t gram_scratch(int device, void** ptr) {

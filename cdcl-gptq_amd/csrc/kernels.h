@@ -33,7 +33,7 @@ struct GramJob {
 // Appends the workgroup tiles of job `job` (int4: job, row block of 128, col block of 64,
 // mirror flag). `sym`: Y == X and the incoming H is symmetric.
 void gram_mfma_tiles(int job, int n, bool sym, std::vector<int4>& out);
-// direct-to-LDS gram for jobs that satisfy gram_dma_eligible (all tiles interior, T % 32 == 0), on
+// direct-to-LDS gram for jobs that satisfy gram_dma_eligible (all tiles interior, T % 64 == 0), on
 // 128 x 128 tiles (int4: job, row block of 128, col block of 128, mirror flag)
 hipError_t gram_dma(hipStream_t st, const GramJob* jobs, const int4* tiles, int ntiles);
 void gram_dma_tiles(int job, int n, bool sym, std::vector<int4>& out);

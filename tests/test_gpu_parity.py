@@ -121,8 +121,12 @@ def test_synth_tokens_beyond_2_32_elements(ctx):
 
 
 # ---------------------------------------------------------------- H accumulation
+# n % 128 == 0 with T % 64 == 0 takes the direct-to-LDS kernel (64-token stages): T = 64, a run
+# ending mid-panel (4160) and one crossing a chunk boundary mid-panel (2112); the other shapes take
+# the generic kernel, including T % 64 == 32 at n % 128 == 0.
 @pytest.mark.parametrize("t,n", [(1, 8), (2047, 64), (2048, 100), (2049, 130), (4100, 96), (5000, 200),
-                                 (32, 128), (4128, 128), (2080, 384)])
+                                 (32, 128), (4128, 128), (2080, 384), (64, 128), (4160, 128), (2112, 256),
+                                 (2112, 384)])
 @pytest.mark.parametrize("sym", [True, False])
 def test_gram_bitexact(ctx, t, n, sym):
     rng = np.random.default_rng(t * 31 + n)
