@@ -400,7 +400,7 @@ __global__ __launch_bounds__(256) void k_pass_accum(int rows, int rc, int nref, 
                                                     const uint32_t* __restrict__ ccnt,
                                                     const uint8_t* __restrict__ active, double* __restrict__ ld,
                                                     uint64_t* __restrict__ upd) {
-  __shared__ double vals[2][ACC_LDS];
+  __shared__ double vals[2][ACC_LDS + 32];  // padding: wave 0 reads up to 32 past the batch's end
   __shared__ uint32_t offs[ACC_ENT + 1];  // exclusive offsets of the batch's entries; offs[ne] = total
   __shared__ uint32_t wsum[4];
   const int c = blockIdx.x;
@@ -471,15 +471,41 @@ __global__ __launch_bounds__(256) void k_pass_accum(int rows, int rc, int nref, 
     for (uint32_t done = 0; done < total; done += ACC_LDS) {
       const uint32_t m = min((uint32_t)ACC_LDS, total - done);
       if (wv == 0) {
+        // Three register batches of 8 rotate: each is read two batches before it is added, so
+        // the adds never wait on the most recent reads. Reads past m (inside the padding) are
+        // never added.
+        const double* vb = &vals[buf][0];
+        const uint32_t m8 = m & ~7u;
+        double va[8], vb8[8], vc[8];
+        auto rd = [&](uint32_t at, double* d) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) d[q] = vb[at + q];
+          asm volatile("" : "+v"(acc) : : "memory");  // the reads stay ahead of the adds that follow
+        };
+        auto add = [&](const double* d) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc = acc + d[q];
+        };
+        rd(0, va);
+        rd(8, vb8);
         uint32_t i = 0;
-        for (; i + 8 <= m; i += 8) {
-          double v[8];
-#pragma unroll
-          for (int q = 0; q < 8; ++q) v[q] = vals[buf][i + q];
-#pragma unroll
-          for (int q = 0; q < 8; ++q) acc = acc + v[q];
+        for (; i + 24 <= m8; i += 24) {
+          rd(i + 16, vc);
+          add(va);
+          rd(i + 24, va);
+          add(vb8);
+          rd(i + 32, vb8);
+          add(vc);
         }
-        for (; i < m; ++i) acc = acc + vals[buf][i];
+        if (i < m8) {  // at most two batches left, already in va and vb8
+          add(va);
+          i += 8;
+          if (i < m8) {
+            add(vb8);
+            i += 8;
+          }
+        }
+        for (; i < m; ++i) acc = acc + vb[i];
       } else if (done + ACC_LDS < total) {
         gather(done + ACC_LDS, buf ^ 1, 64, 192);
       }
