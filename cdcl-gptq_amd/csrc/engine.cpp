@@ -90,6 +90,9 @@ void sort_desc_index(std::vector<size_t>& idx, const std::vector<double>& key) {
   });
 }
 
+// Blocks of the Cholesky applied per deferred trailing pass (see factor()).
+constexpr int kCholDefer = 4;
+
 // U from the flipped matrix `a` (n x n f64, overwritten by L): blocked Cholesky, triangular inverse
 // of L into y, then U_ij = (f32) y[n-1-i][n-1-j] (src/linalg.rs:362-375).
 int factor(cdclq_ctx* ctx, int n, double* a, double* y, float* u) {
@@ -99,35 +102,39 @@ int factor(cdclq_ctx* ctx, int n, double* a, double* y, float* u) {
   int* status = P<int>(ctx->status_d);
   double* pivot = reinterpret_cast<double*>(P<char>(ctx->status_d) + 8);
   HIPCK(hipMemsetAsync(ctx->status_d.p, 0, 16, st));
-  // Right-looking blocked Cholesky with one block of look-ahead: after block k's panel, the main
-  // stream first applies block k to block column k + 1 only, then the side stream factors block
-  // k + 1 (diagonal block and panel) while the main stream applies block k to the rest of the
-  // trailing matrix. The two touch disjoint elements, and every element still receives block
-  // k's update (one k = 96 chain, src/linalg.rs:243-270) before block k + 1's.
+  // Blocked Cholesky with deferred trailing updates. Block columns are taken in periods of
+  // kCholDefer blocks. Before block c is factored, the earlier blocks of its period are applied to
+  // its block column (rows c.., in block order). At the end of a period its blocks are applied, in
+  // order, to every column beyond it: to the next period's block columns on the main stream,
+  // then to the rest on the side stream, which runs while the next period is factored and is
+  // waited for before the next period's own pass touches the same columns. Each block's update
+  // is still one k = 96 chain folded into the element (src/linalg.rs:243-270), and every element
+  // receives the blocks' updates in block order; only the grouping of launches differs.
   hipStream_t st2 = ctx->st2;
-  HIPCK(chol_diag(st, n, a, 0, std::min(NB, n), status, pivot));
-  if (NB < n) HIPCK(chol_panel(st, n, a, 0, NB, status));
-  for (int k = 0; k < n; k += NB) {
-    const int kb = std::min(NB, n - k), kend = k + kb;
-    if (kend >= n) break;
-    const int kb1 = std::min(NB, n - kend), knext = kend + kb1;
-    // block k applied to block column k + 1 (rows kend.., cols kend..knext)
-    const long off = (long)kend * n + k;
-    HIPCK(gemm_chain<double>(st, n - kend, kb1, kb, -1.0, 1, a + off, n, 1, a + off, 1, n, a + (long)kend * n + kend,
-                             n, 1, true, (double*)nullptr));
-    HIPCK(hipEventRecord(ctx->ev_col, st));
-    HIPCK(hipStreamWaitEvent(st2, ctx->ev_col, 0));
-    HIPCK(chol_diag(st2, n, a, kend, kb1, status, pivot));
-    if (knext < n) HIPCK(chol_panel(st2, n, a, kend, kb1, status));
-    HIPCK(hipEventRecord(ctx->ev_panel, st2));
-    // block k applied to the rest of the trailing matrix (rows and cols knext..)
-    if (knext < n) {
-      const long off2 = (long)knext * n + k;
-      HIPCK(gemm_chain<double>(st, n - knext, n - knext, kb, -1.0, 1, a + off2, n, 1, a + off2, 1, n,
-                               a + (long)knext * n + knext, n, 1, true, (double*)nullptr));
+  const int nb = (n + NB - 1) / NB;
+  bool side_pending = false;
+  for (int c = 0; c < nb; ++c) {
+    const int kc = c * NB, kb = std::min(NB, n - kc), kend = kc + kb;
+    const int g0 = (c / kCholDefer) * kCholDefer, kg = g0 * NB;
+    if (c > g0)  // blocks g0 .. c - 1 applied to block column c
+      HIPCK(chol_update(st, n - kc, kb, kc - kg, a + (long)kc * n + kg, n, a + (long)kc * n + kc, n));
+    HIPCK(chol_diag(st, n, a, kc, kb, status, pivot));
+    if (kend < n) HIPCK(chol_panel(st, n, a, kc, kb, status));
+    const bool period_end = (c - g0 == kCholDefer - 1) || c + 1 == nb;
+    if (!period_end || kend >= n) continue;
+    const int c2 = std::min(n, kend + kCholDefer * NB);  // end of the next period's block columns
+    if (side_pending) HIPCK(hipStreamWaitEvent(st, ctx->ev_panel, 0));  // it wrote columns >= kend
+    side_pending = false;
+    HIPCK(chol_update(st, n - kend, c2 - kend, kend - kg, a + (long)kend * n + kg, n, a + (long)kend * n + kend, n));
+    if (c2 < n) {
+      HIPCK(hipEventRecord(ctx->ev_col, st));
+      HIPCK(hipStreamWaitEvent(st2, ctx->ev_col, 0));
+      HIPCK(chol_update(st2, n - c2, n - c2, kend - kg, a + (long)c2 * n + kg, n, a + (long)c2 * n + c2, n));
+      HIPCK(hipEventRecord(ctx->ev_panel, st2));
+      side_pending = true;
     }
-    HIPCK(hipStreamWaitEvent(st, ctx->ev_panel, 0));
   }
+  if (side_pending) HIPCK(hipStreamWaitEvent(st, ctx->ev_panel, 0));
   struct {
     int status;
     int pad;

@@ -55,86 +55,71 @@ __global__ __launch_bounds__(256) void k_build_flipped_f64(int n, const double* 
 // is final (right-looking) performs exactly the same operations on every element in the same
 // order, with the trailing triangle updated in parallel.
 //
-// Element (i, j) lives in a register of thread (i % DGR, j % DGR) of a DGR x DGR thread grid for
-// the whole factorisation (2-D cyclic, so every step's trailing triangle is spread over all
-// threads; 32 x 32 threads hold 3 x 3 slots each).
-// Per step t: the pivot and the divisions of column t run one per thread from the LDS copy of the
-// column (pre), then every thread applies column t to its elements (slot rows and columns that lie
-// wholly before t are skipped by the wave); the owners of column t + 1 copy it to LDS for the next
-// step.
-constexpr int DGR = 32;         // thread grid side
-constexpr int DS = NBC / DGR;   // row / column slots per thread
-constexpr int DGT = DGR * DGR;  // threads
-__global__ __launch_bounds__(DGT) void k_chol_diag(int n, double* __restrict__ a, int k, int kb, int* status,
-                                                   double* pivot) {
+// One wavefront, no barriers: the lanes form an 8 x 8 grid and element (i, j) lives in register
+// slot (i / 8, j / 8) of lane (i % 8, j % 8) for the whole factorisation (2-D cyclic, so every
+// step's trailing triangle is spread over all lanes; 12 x 12 slots, the lower 78 of them used).
+// Step t: the lanes holding column t publish it (updated through step t - 1) to LDS, every lane
+// divides one or two of its entries by l_tt and publishes column t of L, and every lane applies
+// that column to its slots. LDS accesses of one wavefront complete in order, so a read issued
+// after a write sees it. Slot columns left of t's are skipped; the registers of finished columns
+// (and of the upper triangle) that are still updated are never read again.
+constexpr int DGL = 8;           // lane grid side
+constexpr int DSL = NBC / DGL;   // row / column slots per lane
+__global__ __launch_bounds__(64) void k_chol_diag(int n, double* __restrict__ a, int k, int kb, int* status,
+                                                  double* pivot) {
   __shared__ double pre[NBC];  // column t with all earlier columns applied, before the division
   __shared__ double col[NBC];  // column t of L (zero above row t)
   if (*status) return;
-  const int tid = threadIdx.x, tr = tid / DGR, tc = tid % DGR;
-  const int wrow_max = (64 / DGR) * ((tid >> 6) + 1) - 1;  // the wave's largest tr
-  double v[DS][DS];
+  const int lane = threadIdx.x, tr = lane >> 3, tc = lane & 7;
+  double v[DSL][DSL];
 #pragma unroll
-  for (int r = 0; r < DS; ++r)
+  for (int r = 0; r < DSL; ++r)
 #pragma unroll
-    for (int c = 0; c < DS; ++c) {
-      const int i = DGR * r + tr, j = DGR * c + tc;
+    for (int c = 0; c <= r; ++c) {
+      const int i = DGL * r + tr, j = DGL * c + tc;
       v[r][c] = a[(long)(k + min(i, kb - 1)) * n + k + min(j, kb - 1)];
     }
-  __builtin_amdgcn_sched_barrier(0);
+  // A pivot that is not positive and finite records the first failing step; the remaining steps
+  // run on (their values are discarded with the error), so the loops have no early exit.
+  bool failed = false;
 #pragma unroll
-  for (int r = 0; r < DS; ++r)
+  for (int ct = 0; ct < DSL; ++ct) {
+    const int nlt = min(DGL, kb - DGL * ct);  // uniform; <= 0 past the block
+    for (int lt = 0; lt < nlt; ++lt) {
+      const int t = DGL * ct + lt;
+      if (tc == lt) {
 #pragma unroll
-    for (int c = 0; c < DS; ++c) {
-      const int i = DGR * r + tr, j = DGR * c + tc;
-      if (j == 0 && i < kb) pre[i] = v[r][c];
-    }
-  if (tid < NBC) col[tid] = 0.0;
-  __syncthreads();
-  // Column t is final once divided: it goes to a from the LDS copy, and the registers of columns
-  // <= t (and of the upper triangle) are not read again. So every slot still in the trailing
-  // square takes v - l_it l_jt without a predicate; only slots of the lower triangle with
-  // j > t are ever read later, and those see exactly the reference's subtraction sequence.
-  for (int t = 0; t < kb; ++t) {
-    const double d = pre[t];  // every thread reads the same pivot: the branch below is uniform
-    if (!(d > 0.0) || !isfinite(d)) {
-      if (tid == 0) {
-        *status = k + t + 1;
-        *pivot = d;
+        for (int r = ct; r < DSL; ++r) pre[DGL * r + tr] = v[r][ct];
       }
-      return;
-    }
-    const double ltt = sqrt(d);
-    if (tid == t) col[t] = ltt;
-    if (tid > t && tid < kb) col[tid] = pre[tid] / ltt;
-    if (tid == t - 1) col[t - 1] = 0.0;  // rows above t: zero (col held column t - 1 there)
-    __syncthreads();
-    if (tid >= t && tid < kb) a[(long)(k + tid) * n + k + t] = col[tid];
-    double ci[DS], cj[DS];
-#pragma unroll
-    for (int q = 0; q < DS; ++q) {
-      ci[q] = col[DGR * q + tr];
-      cj[q] = col[DGR * q + tc];
-    }
-#pragma unroll
-    for (int r = 0; r < DS; ++r) {
-      if (DGR * r + wrow_max < t) continue;  // the wave's rows in this slot are all finished
-#pragma unroll
-      for (int c = 0; c < DS; ++c) {
-        if (DGR * c + DGR - 1 < t) continue;  // all columns of this slot are finished
-        v[r][c] = v[r][c] - ci[r] * cj[c];
+      const double d = pre[t];  // the same pivot in every lane: the branch below is uniform
+      if ((!(d > 0.0) || !isfinite(d)) && !failed) {
+        failed = true;
+        if (lane == 0) {
+          *status = k + t + 1;
+          *pivot = d;
+        }
       }
-    }
-    // the owners of column t + 1 publish it for the next step's pivot and divisions
-    const int jn = t + 1;
-    if (jn < kb && tc == jn % DGR) {
-      const int cn = jn / DGR;  // uniform: selects the slot without indexing registers
+      const double ltt = sqrt(d);
 #pragma unroll
-      for (int r = 0; r < DS; ++r) {
-        const int i = DGR * r + tr;
-        if (i >= jn && i < kb) pre[i] = cn == 0 ? v[r][0] : (cn == 1 ? v[r][1] : v[r][2]);
+      for (int h = 0; h < 2; ++h) {
+        const int i = lane + 64 * h;
+        if (i < NBC) {
+          const double c = (i == t) ? ltt : ((i > t && i < kb) ? pre[i] / ltt : 0.0);
+          col[i] = c;
+          if (i >= t && i < kb) a[(long)(k + i) * n + k + t] = c;
+        }
       }
+      double ci[DSL], cj[DSL];
+#pragma unroll
+      for (int q = ct; q < DSL; ++q) {
+        ci[q] = col[DGL * q + tr];
+        cj[q] = col[DGL * q + tc];
+      }
+#pragma unroll
+      for (int r = ct; r < DSL; ++r)
+#pragma unroll
+        for (int c = ct; c <= r; ++c) v[r][c] = v[r][c] - ci[r] * cj[c];
     }
-    __syncthreads();
   }
 }
 
@@ -267,7 +252,7 @@ hipError_t build_flipped_f64(hipStream_t st, int n, const double* h, double* a) 
 }
 
 hipError_t chol_diag(hipStream_t st, int n, double* a, int k, int kb, int* status, double* pivot) {
-  hipLaunchKernelGGL(k_chol_diag, dim3(1), dim3(DGT), 0, st, n, a, k, kb, status, pivot);
+  hipLaunchKernelGGL(k_chol_diag, dim3(1), dim3(64), 0, st, n, a, k, kb, status, pivot);
   return hipGetLastError();
 }
 

@@ -143,7 +143,9 @@ __global__ __launch_bounds__(256) void k_gemm(int m, int n, int k, T alpha, T be
 // which a 64-row tile would cover with a quarter of its rows idle); wave (wi, wj) owns rows
 // (BM / 2) wi.., cols 32 wj.. as (BM / 32) x 2 blocks; k is staged 16 at a time through
 // double-buffered LDS. Operand loads are 16-byte pairs along the contiguous dimension when the
-// host found it aligned (mode 1: along k, mode 2: along i / j).
+// host found it aligned (mode 1: along k, mode 2: along i / j). Without SPLIT the chain restarts
+// and is folded into C every `kfold` steps of k: KC for a GEMM, the 96-column block width for
+// the Cholesky's deferred trailing updates (several blocks' updates, each folded in order).
 typedef double v4d __attribute__((ext_vector_type(4)));
 typedef double v2d __attribute__((ext_vector_type(2)));
 constexpr int DBM = 64, DBN = 64, DKT = 16, DPAD = 16;
@@ -153,7 +155,7 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
                                                     const double* __restrict__ A, long rsa, long csa, int amode,
                                                     const double* __restrict__ B, long rsb, long csb, int bmode,
                                                     double* __restrict__ C, long rsc, long csc, double* __restrict__ P,
-                                                    int b_tri) {
+                                                    int b_tri, int kfold) {
   static_assert(BM == 64 || BM == 96, "64- or 96-row tiles");
   constexpr int WR = BM / 2;        // rows per wave
   constexpr int NBI = WR / 16;      // 16-row blocks per wave
@@ -283,7 +285,7 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
     __syncthreads();
     if (!SPLIT) {
       const int kn = k0 + DKT;
-      if ((kn % CDCLQ_KC) == 0 || kn >= kend) {
+      if ((kn % kfold) == 0 || kn >= kend) {
 #pragma unroll
         for (int bi = 0; bi < NBI; ++bi)
 #pragma unroll
@@ -377,10 +379,10 @@ hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, T beta, cons
       if (m == 96) {  // the triangular inverse's block rows: one 96-row tile
         g3.y = 1;
         hipLaunchKernelGGL((k_dgemm_mfma<true, false, 96>), g3, dim3(256), 0, st, m, n, k, alpha, beta, A, rsa,
-                           csa, am, B, rsb, csb, bm, C, rsc, csc, partials, bt);
+                           csa, am, B, rsb, csb, bm, C, rsc, csc, partials, bt, CDCLQ_KC);
       } else {
         hipLaunchKernelGGL((k_dgemm_mfma<true, false>), g3, dim3(256), 0, st, m, n, k, alpha, beta, A, rsa, csa,
-                           am, B, rsb, csb, bm, C, rsc, csc, partials, bt);
+                           am, B, rsb, csb, bm, C, rsc, csc, partials, bt, CDCLQ_KC);
       }
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
@@ -390,10 +392,10 @@ hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, T beta, cons
     }
     if (lower)
       hipLaunchKernelGGL((k_dgemm_mfma<false, true>), grid, dim3(256), 0, st, m, n, k, alpha, beta, A, rsa, csa,
-                         am, B, rsb, csb, bm, C, rsc, csc, (double*)nullptr, bt);
+                         am, B, rsb, csb, bm, C, rsc, csc, (double*)nullptr, bt, CDCLQ_KC);
     else
       hipLaunchKernelGGL((k_dgemm_mfma<false, false>), grid, dim3(256), 0, st, m, n, k, alpha, beta, A, rsa, csa,
-                         am, B, rsb, csb, bm, C, rsc, csc, (double*)nullptr, bt);
+                         am, B, rsb, csb, bm, C, rsc, csc, (double*)nullptr, bt, CDCLQ_KC);
     return hipGetLastError();
   }
   if (np > 1 && partials != nullptr && !lower) {
@@ -413,6 +415,15 @@ hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, T beta, cons
   else
     hipLaunchKernelGGL((k_gemm<T, false, false>), grid, dim3(256), 0, st, m, n, k, alpha, beta, A, rsa, csa, B,
                        rsb, csb, C, rsc, csc, (T*)nullptr, bt);
+  return hipGetLastError();
+}
+
+hipError_t chol_update(hipStream_t st, int m, int n, int k, const double* P, long ldp, double* C, long ldc) {
+  if (m <= 0 || n <= 0 || k <= 0) return hipSuccess;
+  const dim3 grid((n + DBN - 1) / DBN, (m + DBM - 1) / DBM, 1);
+  const int pm = dmode(P, 1, ldp);  // both operands run along k = the rows of P
+  hipLaunchKernelGGL((k_dgemm_mfma<false, true>), grid, dim3(256), 0, st, m, n, k, -1.0, 1.0, P, ldp, 1L, pm, P,
+                     1L, ldp, pm, C, ldc, 1L, (double*)nullptr, 0, 96);
   return hipGetLastError();
 }
 

@@ -21,6 +21,11 @@ hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, T beta, cons
                       const T* B, long rsb, long csb, T* C, long rsc, long csc, bool lower, T* partials,
                       bool b_lower_tri = false);
 size_t gemm_partials_elems(int m, int n, int k);
+// Cholesky trailing update of the lower tiles of C (m x n) by k / 96 consecutive 96-column blocks
+// of L rows P (m x k, row stride ldp; P's first n rows are also the right operand, transposed):
+// for each block b in order, C = fma(-1, chain_b, C) with chain_b the 96-step FMA chain of
+// P[:, b] P[0:n, b]^T (src/linalg.rs:243-270, one dgemm per block).
+hipError_t chol_update(hipStream_t st, int m, int n, int k, const double* P, long ldp, double* C, long ldc);
 
 // ---- k_gram.hip: H (n x n, f64) += X^T Y over 2048-token chunks on the matrix cores.
 struct GramJob {
