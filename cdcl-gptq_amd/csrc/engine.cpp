@@ -157,10 +157,17 @@ int factor(cdclq_ctx* ctx, int n, double* a, double* y, float* u) {
     const int e = std::min(s + NB, n), w = e - s;
     double* t = P<double>(ctx->tbuf);
     // t = L[s:e, 0:s] Y[0:s, 0:s]; Y[s:e, 0:s] = -Y_ss t  (src/linalg.rs:307-343)
-    HIPCK(gemm_chain<double>(st, w, s, s, 1.0, 0, a + (long)s * n, n, 1, y, n, 1, t, s, 1, false,
-                             s > 256 ? P<double>(ctx->tpart) : nullptr, /*b_lower_tri=*/true));
-    HIPCK(gemm_chain<double>(st, w, s, w, -1.0, 0, y + (long)s * n + s, n, 1, t, s, 1, y + (long)s * n, n, 1, false,
-                             (double*)nullptr));
+    double* tp = s > 256 ? P<double>(ctx->tpart) : nullptr;
+    if (inv_gemm_eligible(w, s, s, a + (long)s * n, n, y, n))
+      HIPCK(inv_gemm(st, w, s, s, 1.0, a + (long)s * n, n, y, n, t, s, tp, /*b_lower_tri=*/true));
+    else
+      HIPCK(gemm_chain<double>(st, w, s, s, 1.0, 0, a + (long)s * n, n, 1, y, n, 1, t, s, 1, false, tp,
+                               /*b_lower_tri=*/true));
+    if (inv_gemm_eligible(w, s, w, y + (long)s * n + s, n, t, s))
+      HIPCK(inv_gemm(st, w, s, w, -1.0, y + (long)s * n + s, n, t, s, y + (long)s * n, n, nullptr, false));
+    else
+      HIPCK(gemm_chain<double>(st, w, s, w, -1.0, 0, y + (long)s * n + s, n, 1, t, s, 1, y + (long)s * n, n, 1, false,
+                               (double*)nullptr));
   }
   HIPCK(scatter_u(st, n, y, u));
   return CDCLQ_OK;

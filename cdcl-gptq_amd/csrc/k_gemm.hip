@@ -314,6 +314,187 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
       }
 }
 
+// Pipelined f64 chain GEMM for the factorisation's large products (same per-element sequence as
+// k_dgemm_mfma: chains of v_mfma_f64_16x16x4f64 restarted and folded every `kfold` steps of k).
+// Requirements (checked by the host): A rows run along k (A[i][k], k contiguous); B either along
+// k (BT: B[k][j] = Bt[j][k]) or along j (B[k][j]); every row start 16-byte aligned; k, the k range
+// of every tile and kfold multiples of DMK; n even when B runs along j. Workgroup tile BM x 128
+// (BM = 128: the Cholesky's trailing updates; 96: the inverse's block rows), BM / 32 x 2 waves,
+// wave (wr, wc) owning rows 32 wr .. +31 and columns 64 wc .. +63 as 2 x 4 blocks of 16 x 16.
+// Stages of DMK = 16 k are filled with global_load_lds_dwordx4 into a ring of DMS, DMS - 1 stages
+// in flight, one bare barrier per stage. A k-contiguous operand is staged as [row][8 slots of 16 B]
+// with k-pair p of row r in slot p ^ ((r >> 1) & 7), so the 16 rows a matrix-core fragment reads
+// at one k fall on distinct banks; B along j is staged as [k][128]. Rows and columns past the
+// matrix are read from clamped addresses and only reach outputs that are never stored. b_tri
+// (B lower triangular, beta == 0) starts each tile's k loop at its first column, as in k_dgemm_mfma.
+constexpr int DMK = 16, DMS = 4, DMN = 128;
+template <int BM, bool BT, bool SPLIT>
+__global__ __launch_bounds__(BM * 4) void k_dmm(int m, int n, int k, double alpha, double beta,
+                                               const double* __restrict__ A, long lda, const double* __restrict__ B,
+                                               long ldb, double* __restrict__ C, long ldc, double* __restrict__ P,
+                                               int kfold, int lower, int b_tri) {
+  constexpr int NW = BM / 16;                    // waves: BM / 32 row groups x 2 column groups
+  constexpr int ABYTES = BM * DMK * 8;           // A part of a stage
+  constexpr int SBYTES = ABYTES + DMN * DMK * 8;  // stage
+  constexpr int NI = SBYTES / 1024;              // 1 KB load instructions per stage
+  constexpr int LMAX = (NI + NW - 1) / NW, LMIN = NI / NW;
+  __shared__ double R[DMS * SBYTES / 8];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wv >> 1, wc = wv & 1;
+  const int i0 = blockIdx.y * BM, j0 = blockIdx.x * DMN;
+  if (lower && j0 > i0 + BM - 1) return;  // tile strictly above the diagonal
+  int kbeg = 0, kend = k;
+  if (SPLIT) {
+    kbeg = blockIdx.z * CDCLQ_KC;
+    kend = min(k, kbeg + CDCLQ_KC);
+  }
+  const int kfirst = b_tri ? max(kbeg, (j0 / DMK) * DMK) : kbeg;
+  const int nst = kend > kfirst ? (kend - kfirst) / DMK : 0;
+  const int nload = (NI - wv + NW - 1) / NW;  // this wave's loads per stage (LMIN or LMAX)
+  // per-lane source offsets of this wave's loads, relative to the stage's k0
+  const double* src[LMAX];
+  uint32_t dst[LMAX];
+#pragma unroll
+  for (int q = 0; q < LMAX; ++q) {
+    const int ins = min(wv + NW * q, NI - 1);
+    dst[q] = (uint32_t)ins * 1024u;
+    if (ins < BM / 8) {  // A rows 8 ins .. +7
+      const int r = 8 * ins + (lane >> 3), pr = (lane & 7) ^ ((r >> 1) & 7);
+      src[q] = A + (long)min(i0 + r, m - 1) * lda + 2 * pr;
+    } else if (BT) {  // Bt rows (B columns) 8 (ins - BM / 8) .. +7
+      const int r = 8 * (ins - BM / 8) + (lane >> 3), pr = (lane & 7) ^ ((r >> 1) & 7);
+      src[q] = B + (long)min(j0 + r, n - 1) * ldb + 2 * pr;
+    } else {  // B k row ins - BM / 8, columns 2 lane, 2 lane + 1
+      src[q] = B + (long)(ins - BM / 8) * ldb + min(j0 + 2 * lane, n - 2);
+    }
+  }
+  const uint32_t lds0 = lds_offset(&R[0]);
+  auto issue = [&](int st) {  // stage st (k0 = kfirst + DMK st) into ring slot st % DMS
+    const long koff = (long)(kfirst + DMK * st);
+    const uint32_t base = lds0 + (uint32_t)((st % DMS) * SBYTES);
+#pragma unroll
+    for (int q = 0; q < LMAX; ++q) {
+      if (q >= nload) continue;  // uniform
+      const int ins = wv + NW * q;
+      const double* g = src[q];
+      if (ins < BM / 8 || BT)
+        g += koff;  // along k within the row
+      else
+        g += koff * ldb;  // k rows
+      dma16_untracked(reinterpret_cast<const float*>(g), base + dst[q]);
+    }
+  };
+  v4d acc[2][4], cv[2][4];
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        acc[bi][bj][r] = 0.0;
+        cv[bi][bj][r] = 0.0;
+      }
+  for (int st = 0; st < DMS - 1 && st < nst; ++st) issue(st);
+  if (!SPLIT && beta != 0.0) {  // C' = beta * C; 1 * C is C itself
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+      for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int gi = min(i0 + 32 * wr + 16 * bi + (lane >> 4) + 4 * r, m - 1);
+          const int gj = min(j0 + 64 * wc + 16 * bj + (lane & 15), n - 1);
+          cv[bi][bj][r] = C[(long)gi * ldc + gj];
+        }
+    // one wait here (with the first stages in flight) instead of one the compiler would place at
+    // every fold inside the loop, where it would also drain the stage ring
+    wait_vmcnt<0>();
+    if (beta != 1.0) {
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) cv[bi][bj][r] = beta * cv[bi][bj][r];
+    }
+  }
+  // LDS element offsets (doubles) of this lane's fragment reads within a stage, for k-step 0
+  int aoff[2], boff[4];
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi) aoff[bi] = (32 * wr + 16 * bi + (lane & 15)) * DMK;
+#pragma unroll
+  for (int bj = 0; bj < 4; ++bj) boff[bj] = BT ? ABYTES / 8 + (64 * wc + 16 * bj + (lane & 15)) * DMK
+                                              : ABYTES / 8 + (lane >> 4) * DMN + 64 * wc + 16 * bj + (lane & 15);
+  for (int st = 0; st < nst; ++st) {
+    // this wave's loads of stage st have landed once at most those of the later stages in flight
+    // remain; the barrier then publishes every wave's part and retires all reads of stage st - 1
+    const int later = min(DMS - 2, nst - 1 - st);
+    if (later >= 2) {
+      if (nload == LMAX) wait_vmcnt<2 * LMAX>(); else wait_vmcnt<2 * LMIN>();
+    } else if (later == 1) {
+      if (nload == LMAX) wait_vmcnt<LMAX>(); else wait_vmcnt<LMIN>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    __builtin_amdgcn_s_barrier();
+    if (st + DMS - 1 < nst) issue(st + DMS - 1);  // into the slot of stage st - 1
+    const double* S = &R[(st % DMS) * (SBYTES / 8)];
+#pragma unroll
+    for (int k4 = 0; k4 < DMK; k4 += 4) {
+      const int kk = k4 + (lane >> 4);
+      double a[2], b[4];
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi) {
+        const int r = 32 * wr + 16 * bi + (lane & 15);
+        a[bi] = S[aoff[bi] + 2 * ((kk >> 1) ^ ((r >> 1) & 7)) + (kk & 1)];
+      }
+#pragma unroll
+      for (int bj = 0; bj < 4; ++bj) {
+        if (BT) {
+          const int r = 64 * wc + 16 * bj + (lane & 15);
+          b[bj] = S[boff[bj] + 2 * ((kk >> 1) ^ ((r >> 1) & 7)) + (kk & 1)];
+        } else {
+          b[bj] = S[boff[bj] + k4 * DMN];
+        }
+      }
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj)
+          acc[bi][bj] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[bi], b[bj], acc[bi][bj], 0, 0, 0);
+    }
+    if (!SPLIT) {
+      const int kn = kfirst + DMK * (st + 1);
+      if ((kn % kfold) == 0 || kn >= kend) {
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+          for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              cv[bi][bj][r] = __builtin_fma(alpha, acc[bi][bj][r], cv[bi][bj][r]);
+              acc[bi][bj][r] = 0.0;
+            }
+      }
+    }
+  }
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int gi = i0 + 32 * wr + 16 * bi + (lane >> 4) + 4 * r, gj = j0 + 64 * wc + 16 * bj + (lane & 15);
+        if (gi < m && gj < n) {
+          if (SPLIT)
+            P[((long)blockIdx.z * m + gi) * n + gj] = acc[bi][bj][r];
+          else
+            C[(long)gi * ldc + gj] = cv[bi][bj][r];
+        }
+      }
+}
+
 // operand load mode for k_dgemm_mfma from the strides along k and along the other index:
 // 1 = 16-byte pairs along k, 2 = pairs along the other index, 0 = scalar loads
 inline int dmode(const double* p, long k_stride, long other_stride) {
@@ -418,12 +599,48 @@ hipError_t gemm_chain(hipStream_t st, int m, int n, int k, T alpha, T beta, cons
   return hipGetLastError();
 }
 
+namespace {
+bool aligned16(const void* p) { return (uintptr_t)p % 16 == 0; }
+}  // namespace
+
 hipError_t chol_update(hipStream_t st, int m, int n, int k, const double* P, long ldp, double* C, long ldc) {
   if (m <= 0 || n <= 0 || k <= 0) return hipSuccess;
+  if (n >= 512 && m >= 2 && k % DMK == 0 && aligned16(P) && ldp % 2 == 0) {  // the bulk passes
+    const dim3 grid((n + DMN - 1) / DMN, (m + 127) / 128, 1);
+    hipLaunchKernelGGL((k_dmm<128, true, false>), grid, dim3(512), 0, st, m, n, k, -1.0, 1.0, P, ldp, P, ldp, C,
+                       ldc, (double*)nullptr, 96, 1, 0);
+    return hipGetLastError();
+  }
   const dim3 grid((n + DBN - 1) / DBN, (m + DBM - 1) / DBM, 1);
   const int pm = dmode(P, 1, ldp);  // both operands run along k = the rows of P
   hipLaunchKernelGGL((k_dgemm_mfma<false, true>), grid, dim3(256), 0, st, m, n, k, -1.0, 1.0, P, ldp, 1L, pm, P,
                      1L, ldp, pm, C, ldc, 1L, (double*)nullptr, 0, 96);
+  return hipGetLastError();
+}
+
+bool inv_gemm_eligible(int m, int n, int k, const double* A, long lda, const double* B, long ldb) {
+  return m > 0 && m <= 96 && n >= 2 && n % 2 == 0 && k > 0 && k % DMK == 0 && aligned16(A) && lda % 2 == 0 &&
+         aligned16(B) && ldb % 2 == 0;
+}
+
+hipError_t inv_gemm(hipStream_t st, int m, int n, int k, double alpha, const double* A, long lda, const double* B,
+                    long ldb, double* C, long ldc, double* partials, bool b_lower_tri) {
+  if (m <= 0 || n <= 0 || k <= 0) return hipSuccess;
+  const int np = (k + CDCLQ_KC - 1) / CDCLQ_KC;
+  const int bt = b_lower_tri ? 1 : 0;
+  dim3 grid((n + DMN - 1) / DMN, 1, 1);
+  if (np > 1 && partials) {
+    grid.z = np;
+    hipLaunchKernelGGL((k_dmm<96, false, true>), grid, dim3(384), 0, st, m, n, k, alpha, 0.0, A, lda, B, ldb, C, ldc,
+                       partials, CDCLQ_KC, 0, bt);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_combine<double>), dim3((unsigned)(((long)m * n + 255) / 256)), dim3(256), 0, st, m, n, np,
+                       alpha, 0.0, (const double*)partials, C, ldc, 1L);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL((k_dmm<96, false, false>), grid, dim3(384), 0, st, m, n, k, alpha, 0.0, A, lda, B, ldb, C, ldc,
+                     (double*)nullptr, CDCLQ_KC, 0, bt);
   return hipGetLastError();
 }
 

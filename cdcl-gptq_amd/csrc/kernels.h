@@ -26,6 +26,13 @@ size_t gemm_partials_elems(int m, int n, int k);
 // for each block b in order, C = fma(-1, chain_b, C) with chain_b the 96-step FMA chain of
 // P[:, b] P[0:n, b]^T (src/linalg.rs:243-270, one dgemm per block).
 hipError_t chol_update(hipStream_t st, int m, int n, int k, const double* P, long ldp, double* C, long ldc);
+// The triangular inverse's block-row products C = alpha * A B (beta = 0, m <= 96 rows, A along k,
+// B along n; src/linalg.rs:307-343) on the pipelined kernel, panels in parallel into `partials`
+// and folded in order when k spans several KC panels. inv_gemm_eligible lists the requirements
+// (else use gemm_chain).
+bool inv_gemm_eligible(int m, int n, int k, const double* A, long lda, const double* B, long ldb);
+hipError_t inv_gemm(hipStream_t st, int m, int n, int k, double alpha, const double* A, long lda, const double* B,
+                    long ldb, double* C, long ldc, double* partials, bool b_lower_tri);
 
 // ---- k_gram.hip: H (n x n, f64) += X^T Y over 2048-token chunks on the matrix cores.
 struct GramJob {
