@@ -515,11 +515,17 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
           for (int c = 0; c < nchunks && !any; ++c) any = act[c] && sel[(size_t)c * n_sb + s];
           if (!any) continue;
           const int c0 = s * sbw, wd = std::min(c0 + sbw, n) - c0;
-          CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32, rtiles + (size_t)(1 + s) * ntile, tcnt[1 + s]));
+          const int* tl_s = rtiles + (size_t)(1 + s) * ntile;
+          // the descent kernel folds the per-panel chains itself where it can (one launch less)
+          const bool fused = cd_folds_chains(wd);
+          if (fused)
+            HIPCK(panel_gemm(st, d_out, wd, n, eb, n, H32 + c0, n, P<float>(ctx->part), tl_s, tcnt[1 + s]));
+          else
+            CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32, tl_s, tcnt[1 + s]));
           HIPCK(cd_subblock(st, d_out, n, ng, g, c0, wd, s, n_sb, rc, (int)cfg->cd_sweeps, P<float>(ctx->G), H32,
                             P<uint8_t>(ctx->gbits_d), scales, zeros, codes, wq, eb, active,
                             P<uint8_t>(ctx->sel_d), clog + (size_t)s * d_out * cap, ccnt + (size_t)s * d_out, cap,
-                            mid, cd_evals));
+                            mid, cd_evals, fused ? P<float>(ctx->part) : nullptr, fused ? (n + 255) / 256 : 0));
         }
       }
       HIPCK(pass_accum(st, d_out, rc, nchunks, do_refit ? ng : 0, rlog, rcnt, do_cd ? n_sb : 0, cap, clog, ccnt,

@@ -897,6 +897,22 @@ __global__ __launch_bounds__(256) void k_refit_mfma(int rows, int n, int ng, int
 // order, since the columns before it saw exactly this gradient and kept their codes. The move is
 // applied (gradient update over the whole sub-block, wave-parallel), the cursor jumps past it and
 // the columns after it are evaluated again. A sweep therefore costs one round per move plus one.
+// One element of G = E H[:, c0:c0+wd] from the per-panel chains of the gradient GEMM (stride
+// pstride between panels): the ordered fold of k_fold, C = fma(1, P_p, C) from C = 0.
+__device__ __forceinline__ float fold_chains(const float* __restrict__ src, long pstride, int np) {
+  float acc = 0.0f;
+  int p = 0;
+  for (; p + 8 <= np; p += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(src + (long)(p + u) * pstride);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(1.0f, v[u], acc);
+  }
+  for (; p < np; ++p) acc = __builtin_fmaf(1.0f, __builtin_nontemporal_load(src + (long)p * pstride), acc);
+  return acc;
+}
+
 template <int NPL>
 __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
                                             int sweeps, const float* __restrict__ G, const float* __restrict__ h32,
@@ -905,7 +921,8 @@ __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int 
                                             float* __restrict__ wq, float* __restrict__ e,
                                             const uint8_t* __restrict__ active, const uint8_t* __restrict__ sel,
                                             double* __restrict__ dlog, uint32_t* __restrict__ dcnt, int cap,
-                                            unsigned long long* __restrict__ mid, uint32_t* __restrict__ evals) {
+                                            unsigned long long* __restrict__ mid, uint32_t* __restrict__ evals,
+                                            const float* __restrict__ P, int np) {
   const int lane = threadIdx.x & 63;
   const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
   if (r >= rows) return;
@@ -914,7 +931,8 @@ __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int 
     if (lane == 0) dcnt[r] = 0;
     return;
   }
-  // per-column state and parameters, one column per lane and slice
+  // per-column state and parameters, one column per lane and slice; the gradient is either G or,
+  // with P, folded here from the GEMM's per-panel chains (P[p][row][col], rows x wd per panel)
   float gg[NPL], mwq[NPL], me[NPL], hd[NPL], sc[NPL], zz[NPL], mq[NPL];
   int mc[NPL];
 #pragma unroll
@@ -924,7 +942,10 @@ __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int 
     const int j = c0 + min(k, wd - 1);
     const long o = (long)r * n + j;
     const int gi = j / g;
-    gg[s] = in ? G[(long)r * wd + k] : 0.0f;
+    if (P)
+      gg[s] = in ? fold_chains(P + (long)r * wd + k, (long)rows * wd, np) : 0.0f;
+    else
+      gg[s] = in ? G[(long)r * wd + k] : 0.0f;
     mwq[s] = in ? wq[o] : 0.0f;
     me[s] = in ? e[o] : 0.0f;
     mc[s] = in ? (int)codes[o] : 0;
@@ -1271,15 +1292,18 @@ hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, i
   return hipGetLastError();
 }
 
+bool cd_folds_chains(int wd) { return wd > 0 && wd <= 1024; }  // the register-resident k_cd<NPL>
+
 hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
                        int sweeps, float* G, const float* h32, const uint8_t* gbits, const float* scales,
                        const float* zeros, uint8_t* codes, float* wq, float* e, const uint8_t* active,
                        const uint8_t* sel, double* dlog, uint32_t* dcnt, int cap, unsigned long long* mid,
-                       uint32_t* evals) {
+                       uint32_t* evals, const float* P, int np) {
   const dim3 grid((rows + 3) / 4), blk(256);
+  if (P && !cd_folds_chains(wd)) return hipErrorInvalidValue;
 #define CD_CASE(N)                                                                                                     \
   hipLaunchKernelGGL((k_cd<N>), grid, blk, 0, st, rows, n, ng, g, c0, wd, sb, nsb, rc, sweeps, G, h32, gbits, scales,  \
-                     zeros, codes, wq, e, active, sel, dlog, dcnt, cap, mid, evals)
+                     zeros, codes, wq, e, active, sel, dlog, dcnt, cap, mid, evals, P, np)
   switch (npl_for(wd)) {
     case 1: CD_CASE(1); break;
     case 2: CD_CASE(2); break;

@@ -113,11 +113,15 @@ hipError_t transpose_f32(hipStream_t st, int n, const float* src, float* dst);
 hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, int rc, const float* G,
                        const float* h32, const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
                        const uint8_t* active, double* dlog, uint32_t* dcnt);
+// Coordinate descent over one sub-block. The gradient comes from G, or, when P is non-null, from
+// the np per-panel chains of panel_gemm (P[p][rows][wd]), folded in panel order by the kernel
+// itself (no separate fold launch); cd_folds_chains(wd) says whether that form is available.
+bool cd_folds_chains(int wd);
 hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
                        int sweeps, float* G, const float* h32, const uint8_t* gbits, const float* scales,
                        const float* zeros, uint8_t* codes, float* wq, float* e, const uint8_t* active,
                        const uint8_t* sel, double* dlog, uint32_t* dcnt, int cap, unsigned long long* mid,
-                       uint32_t* evals);
+                       uint32_t* evals, const float* P = nullptr, int np = 0);
 // Folds one pass's logged deltas into the per-chunk loss (exact reference order); nref refit
 // steps (rlog/rcnt: [nref][rows]) then ncd CD steps (clog: [ncd][rows][cap], ccnt: [ncd][rows]).
 hipError_t pass_accum(hipStream_t st, int rows, int rc, int nchunks, int nref, const double* rlog,
