@@ -92,6 +92,8 @@ void sort_desc_index(std::vector<size_t>& idx, const std::vector<double>& key) {
 
 // Blocks of the Cholesky applied per deferred trailing pass (see factor()).
 constexpr int kCholDefer = 4;
+// Blocks of phase 1 applied per deferred lazy-update pass (see quantize_device()).
+constexpr int kLazyDefer = 4;
 
 // U from the flipped matrix `a` (n x n f64, overwritten by L): blocked Cholesky, triangular inverse
 // of L into y, then U_ij = (f32) y[n-1-i][n-1-j] (src/linalg.rs:362-375).
@@ -375,18 +377,53 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
     PhaseScope ps(ctx, CDCLQ_PHASE_GPTQ);
     HIPCK(hipMemcpyAsync(wwork, wp, wn * 4, hipMemcpyDeviceToDevice, st));
     HIPCK(inv_diag(st, n, U, P<float>(ctx->invd)));
-    for (int i1 = 0; i1 < n; i1 += bsz) {
-      const int i2 = std::min(i1 + bsz, n), cnt = i2 - i1;
+    // Lazy update of W's columns [c0, c1) by blocks b0 .. b1 - 1 (full blocks of bsz columns), in
+    // block order, each W -= E[:, block] U[block, c0:c1] as its own chain (src/engine.rs:452-471).
+    auto lazy = [&](hipStream_t s, int c0, int c1, int b0, int b1) -> int {
+      if (c1 <= c0 || b1 <= b0) return CDCLQ_OK;
+      const int k0 = b0 * bsz, k = (b1 - b0) * bsz;
+      if (chain_gemm_mfma_ok(d_out, c1 - c0, k, eb + k0, n, U + (long)k0 * n + c0, n, bsz)) {
+        HIPCK(chain_gemm_mfma(s, d_out, c1 - c0, k, -1.0f, 1, eb + k0, n, U + (long)k0 * n + c0, n, wwork + c0, n,
+                              bsz));
+        return CDCLQ_OK;
+      }
+      for (int b = b0; b < b1; ++b)
+        HIPCK(gemm_chain<float>(s, d_out, c1 - c0, bsz, -1.0f, 1, eb + (long)b * bsz, n, 1,
+                                U + (long)b * bsz * n + c0, n, 1, wwork + c0, n, 1, false, nullptr));
+      return CDCLQ_OK;
+    };
+    // Blocks are taken in periods of kLazyDefer. Before block b's sweep, the earlier blocks of its
+    // period are applied to its columns; at a period's end its blocks are applied to the next
+    // period's columns (main stream) and to the rest (side stream, overlapping the next period's
+    // sweeps and waited for before the next period's pass reaches the same columns). Every column
+    // still receives the blocks' updates in block order. This needs groups that stay inside a
+    // block (the group grid reads no column past the block) and blocks of at most one KC panel;
+    // otherwise every block's update follows its sweep.
+    const int nb = (n + bsz - 1) / bsz;
+    const bool in_block = bsz % g == 0;  // groups never reach past their block
+    const int defer = (in_block && bsz <= CDCLQ_KC) ? kLazyDefer : 1;
+    bool side_pending = false;
+    for (int b = 0; b < nb; ++b) {
+      const int i1 = b * bsz, i2 = std::min(i1 + bsz, n), cnt = i2 - i1;
+      const int p0 = (b / defer) * defer;
+      if (b > p0) CK(lazy(st, i1, i2, p0, b));
       HIPCK(gptq_block(st, d_out, n, i1, cnt, g, ng, wwork, U, P<float>(ctx->invd), P<uint8_t>(ctx->gbits_d),
                        cfg->mse_grid, scales, zeros, codes, wq, eb, mid));
-      if (i2 < n) {  // lazy update W[:, i2:] -= E[:, i1:i2] U[i1:i2, i2:] (src/engine.rs:452-471)
-        if (chain_gemm_mfma_ok(d_out, n - i2, cnt, eb + i1, n, U + (long)i1 * n + i2, n))
-          HIPCK(chain_gemm_mfma(st, d_out, n - i2, cnt, -1.0f, 1, eb + i1, n, U + (long)i1 * n + i2, n, wwork + i2, n));
-        else
-          HIPCK(gemm_chain<float>(st, d_out, n - i2, cnt, -1.0f, 1, eb + i1, n, 1, U + (long)i1 * n + i2, n, 1,
-                                  wwork + i2, n, 1, false, nullptr));
+      if ((b - p0 != defer - 1 && b + 1 != nb) || i2 >= n) continue;
+      // with groups reaching past a block, the next sweep reads W beyond its block: no overlap
+      const int c2 = in_block ? std::min(n, i2 + defer * bsz) : n;
+      if (side_pending) HIPCK(hipStreamWaitEvent(st, ctx->ev_panel, 0));  // it wrote columns >= i2
+      side_pending = false;
+      CK(lazy(st, i2, c2, p0, b + 1));
+      if (c2 < n) {
+        HIPCK(hipEventRecord(ctx->ev_col, st));
+        HIPCK(hipStreamWaitEvent(ctx->st2, ctx->ev_col, 0));
+        CK(lazy(ctx->st2, c2, n, p0, b + 1));
+        HIPCK(hipEventRecord(ctx->ev_panel, ctx->st2));
+        side_pending = true;
       }
     }
+    if (side_pending) HIPCK(hipStreamWaitEvent(st, ctx->ev_panel, 0));
     HIPCK(cdclq::colloss(st, d_out, n, rc, eb, P<double>(ctx->colloss_d)));
   }
   HIPCK(hipMemcpyAsync(colloss.data(), ctx->colloss_d.p, colloss.size() * 8, hipMemcpyDeviceToHost, st));

@@ -194,14 +194,17 @@ constexpr int DNB = 3;
 constexpr int DSTAGE = DSK * PR + DSK * PC;  // floats per stage (E 4096 + B 2048)
 constexpr int DPW = DSTAGE / 256 / 4;        // 1 KB loads per wave and stage (6)
 
-// DIRECT (C != null, k <= 256, one panel: the GPTQ lazy trailing update): the unit's chain is
-// final and is folded straight into C: C = fma(alpha, chain, beta_one ? C : 0), the single-panel
-// case of the GEMM fold. Otherwise (the repair gradient) the chains go to P.
+// DIRECT (C != null: the GPTQ lazy trailing update): the unit covers all of k, one chain per
+// kfold steps (kfold <= 256: one KC panel), each folded straight into the C values held in
+// registers in k order, C = fma(alpha, chain, C), starting from beta_one ? C : 0 -- one block's
+// update (src/engine.rs:452-471) per kfold, several consecutive blocks per launch.
+// Otherwise (the repair gradient) the chains go to P.
 template <bool DIRECT>
 __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const float* __restrict__ A, long lda,
                                                    const float* __restrict__ B, long ldb, float* __restrict__ P,
                                                    int nunits, const int* __restrict__ rtiles, int nrt,
-                                                   float* __restrict__ C, long ldc, float alpha, int beta_one) {
+                                                   float* __restrict__ C, long ldc, float alpha, int beta_one,
+                                                   int kfold) {
   __shared__ float R[DNB][DSTAGE];
   const int np = k / CDCLQ_KC + (k % CDCLQ_KC != 0);
   // With a full grid (two workgroups per CU), workgroups j and j + G/2 end up on the same CU: the
@@ -220,19 +223,21 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
   };
   auto unit = [&](int u) {
     Unit t;
-    if (DIRECT) {  // one panel; column tiles fastest, so consecutive units share their E tile
+    if (DIRECT) {  // all of k; column tiles fastest, so consecutive units share their E tile
       const int nct = (wd + PC - 1) / PC;
       t.r0 = (u / nct) * PR;
       t.cb = (u % nct) * PC;
       t.p = 0;
+      t.k0 = 0;
+      t.nst = k / DSK;
     } else {
       const int ct = u / (nrt * np), rem = u % (nrt * np);
       t.r0 = (rtiles ? rtiles[rem / np] : rem / np) * PR;
       t.p = rem % np;
       t.cb = ct * PC;
+      t.k0 = t.p * CDCLQ_KC;
+      t.nst = min(CDCLQ_KC, k - t.k0) / DSK;
     }
-    t.k0 = t.p * CDCLQ_KC;
-    t.nst = min(CDCLQ_KC, k - t.k0) / DSK;
     return t;
   };
   const uint32_t lds0 = lds_offset(&R[0][0]);
@@ -333,6 +338,11 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
         acc = mfma32(a.w, hs[(4 * q + 3) * PC], acc);
       }
       ++fc;
+      if (DIRECT && cs + 1 < cu.nst && ((cs + 1) * DSK) % kfold == 0) {  // a block's chain is complete
+#pragma unroll
+        for (int r = 0; r < 32; ++r) cv[r] = __builtin_fmaf(alpha, acc[r], cv[r]);
+        acc = v32f{};
+      }
     }
     if (DIRECT) {
 #pragma unroll
@@ -364,7 +374,7 @@ template <bool DIRECT>
 __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const float* __restrict__ A, long lda,
                                                    const float* __restrict__ B, long ldb, float* __restrict__ C,
                                                    long ldc, float alpha, int nunits, float* __restrict__ P,
-                                                   const int* __restrict__ rtiles) {
+                                                   const int* __restrict__ rtiles, int kfold) {
   __shared__ float R[DNB][LSTAGE];
   const int nct = (wd + LPC - 1) / LPC;
   const int np = k / CDCLQ_KC + (k % CDCLQ_KC != 0);
@@ -379,17 +389,19 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
   };
   auto unit = [&](int u) {
     Unit t;
-    if (DIRECT) {  // one panel, column tiles fastest
+    if (DIRECT) {  // all of k (chains folded every kfold), column tiles fastest
       t.r0 = (u / nct) * PR;
       t.cb = (u % nct) * LPC;
       t.p = 0;
+      t.k0 = 0;
+      t.nst = k / DSK;
     } else {  // the repair gradient, wd == 128: (row tile, panel), panels fastest
       t.r0 = (rtiles ? rtiles[u / np] : u / np) * PR;
       t.cb = 0;
       t.p = u % np;
+      t.k0 = t.p * CDCLQ_KC;
+      t.nst = min(CDCLQ_KC, k - t.k0) / DSK;
     }
-    t.k0 = t.p * CDCLQ_KC;
-    t.nst = min(CDCLQ_KC, k - t.k0) / DSK;
     return t;
   };
   const uint32_t lds0 = lds_offset(&R[0][0]);
@@ -482,6 +494,11 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
         acc = mfma32(a.w, hs[(4 * q + 3) * LPC], acc);
       }
       ++fc;
+      if (DIRECT && cs + 1 < cu.nst && ((cs + 1) * DSK) % kfold == 0) {  // a block's chain is complete
+#pragma unroll
+        for (int r = 0; r < 32; ++r) cv[r] = __builtin_fmaf(alpha, acc[r], cv[r]);
+        acc = v32f{};
+      }
     }
     if (DIRECT) {
 #pragma unroll
@@ -1206,7 +1223,7 @@ hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long
       const long wunits = (long)ntiles * ((k + CDCLQ_KC - 1) / CDCLQ_KC);
       if (wunits >= 4L * ws) {
         hipLaunchKernelGGL(k_lazy_wide<false>, dim3(ws), dim3(512), 0, st, m, wd, k, A, lda, B, ldb, (float*)nullptr,
-                           0L, 0.0f, (int)wunits, P, rtiles);
+                           0L, 0.0f, (int)wunits, P, rtiles, CDCLQ_KC);
         return hipGetLastError();
       }
     }
@@ -1214,7 +1231,7 @@ hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long
     const hipError_t err = dma_slots(&dslots);
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(k_panel_dma<false>, dim3((int)std::min<long>(nunits, dslots)), dim3(256), 0, st, m, wd, k, A, lda,
-                       B, ldb, P, (int)nunits, rtiles, ntiles, (float*)nullptr, 0L, 0.0f, 0);
+                       B, ldb, P, (int)nunits, rtiles, ntiles, (float*)nullptr, 0L, 0.0f, 0, CDCLQ_KC);
     return hipGetLastError();
   }
   if (vec4)
@@ -1226,21 +1243,23 @@ hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long
   return hipGetLastError();
 }
 
-bool chain_gemm_mfma_ok(int m, int n, int k, const float* A, long lda, const float* B, long ldb) {
-  return m > 0 && n >= 4 && k > 0 && k <= CDCLQ_KC && k % DSK == 0 && n % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0 &&
-         (uintptr_t)A % 16 == 0 && (uintptr_t)B % 16 == 0;
+bool chain_gemm_mfma_ok(int m, int n, int k, const float* A, long lda, const float* B, long ldb, int kfold) {
+  const int kf = kfold > 0 ? kfold : k;
+  return m > 0 && n >= 4 && k > 0 && kf <= CDCLQ_KC && kf % DSK == 0 && k % kf == 0 && n % 4 == 0 &&
+         lda % 4 == 0 && ldb % 4 == 0 && (uintptr_t)A % 16 == 0 && (uintptr_t)B % 16 == 0;
 }
 
 hipError_t chain_gemm_mfma(hipStream_t st, int m, int n, int k, float alpha, int beta_one, const float* A, long lda,
-                           const float* B, long ldb, float* C, long ldc) {
-  if (!chain_gemm_mfma_ok(m, n, k, A, lda, B, ldb)) return hipErrorInvalidValue;
+                           const float* B, long ldb, float* C, long ldc, int kfold) {
+  if (!chain_gemm_mfma_ok(m, n, k, A, lda, B, ldb, kfold)) return hipErrorInvalidValue;
+  const int kf = kfold > 0 ? kfold : k;
   int ws = 0;
   const hipError_t e2 = wide_slots(&ws);
   if (e2 != hipSuccess) return e2;
   const long wunits = (long)((m + PR - 1) / PR) * ((n + LPC - 1) / LPC);
   if (beta_one && wunits >= ws && wunits <= INT32_MAX) {
     hipLaunchKernelGGL(k_lazy_wide<true>, dim3(ws), dim3(512), 0, st, m, n, k, A, lda, B, ldb, C, ldc, alpha,
-                       (int)wunits, (float*)nullptr, (const int*)nullptr);
+                       (int)wunits, (float*)nullptr, (const int*)nullptr, kf);
     return hipGetLastError();
   }
   int dslots = 0;
@@ -1249,7 +1268,7 @@ hipError_t chain_gemm_mfma(hipStream_t st, int m, int n, int k, float alpha, int
   const int ntiles = (m + PR - 1) / PR;
   const long nunits = (long)ntiles * ((n + PC - 1) / PC);
   hipLaunchKernelGGL(k_panel_dma<true>, dim3((int)std::min<long>(nunits, dslots)), dim3(256), 0, st, m, n, k, A, lda, B, ldb,
-                     (float*)nullptr, (int)nunits, (const int*)nullptr, ntiles, C, ldc, alpha, beta_one);
+                     (float*)nullptr, (int)nunits, (const int*)nullptr, ntiles, C, ldc, alpha, beta_one, kf);
   return hipGetLastError();
 }
 

@@ -96,12 +96,14 @@ hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long
                       float* P, const int* rtiles, int ntiles);
 hipError_t fold_panels(hipStream_t st, int m, int wd, int np, const float* P, float* G, const int* rtiles,
                        int ntiles);
-// Single-panel f32 chain GEMM on the matrix cores: C = fma(alpha, chain, beta_one ? C : 0) with
-// A m x k (row stride lda), B k x n (row stride ldb), k <= 256 and k % 32 == 0; the _ok test
-// lists every requirement (else use gemm_chain).
-bool chain_gemm_mfma_ok(int m, int n, int k, const float* A, long lda, const float* B, long ldb);
+// f32 chain GEMM on the matrix cores folding one chain per kfold steps of k straight into C:
+// starting from beta_one ? C : 0, C = fma(alpha, chain_b, C) for b = 0 .. k / kfold - 1 in order
+// (kfold = 0: one chain over all of k). A m x k (row stride lda), B k x n (row stride ldb),
+// kfold <= 256 (one KC panel) and kfold % 32 == 0; the _ok test lists every requirement (else use
+// gemm_chain). One block of the GPTQ lazy update per chain (src/engine.rs:452-471).
+bool chain_gemm_mfma_ok(int m, int n, int k, const float* A, long lda, const float* B, long ldb, int kfold = 0);
 hipError_t chain_gemm_mfma(hipStream_t st, int m, int n, int k, float alpha, int beta_one, const float* A, long lda,
-                           const float* B, long ldb, float* C, long ldc);
+                           const float* B, long ldb, float* C, long ldc, int kfold = 0);
 // ---- k_gemm_wide.hip: multi-panel f32 chain GEMM C = A B (alpha 1, beta 0) on the matrix cores,
 // panels folded in registers (the asymmetric target's three GEMMs). tri: 0 dense B, 1 B upper
 // triangular (B[k][j] = 0 for k > j), 2 B lower triangular (B[k][j] = 0 for k < j).
