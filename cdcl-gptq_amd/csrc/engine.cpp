@@ -408,7 +408,7 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
       const int p0 = (b / defer) * defer;
       if (b > p0) CK(lazy(st, i1, i2, p0, b));
       HIPCK(gptq_block(st, d_out, n, i1, cnt, g, ng, wwork, U, P<float>(ctx->invd), P<uint8_t>(ctx->gbits_d),
-                       cfg->mse_grid, scales, zeros, codes, wq, eb, mid));
+                       cfg->mse_grid, scales, zeros, codes, wq, eb, mid, in_block));
       if ((b - p0 != defer - 1 && b + 1 != nb) || i2 >= n) continue;
       // with groups reaching past a block, the next sweep reads W beyond its block: no overlap
       const int c2 = in_block ? std::min(n, i2 + defer * bsz) : n;

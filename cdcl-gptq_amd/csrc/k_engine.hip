@@ -258,6 +258,136 @@ __global__ __launch_bounds__(64 * GB_ROWS) void k_gptq_block(int rows, int n, in
   }
 }
 
+// Phase-1 block sweep with L lanes per row (64 / L rows per wavefront), for blocks of at most 128
+// columns whose groups lie inside the block, without the MSE grid. Per column the wave-per-row
+// kernel above runs the quantization of one value on all 64 lanes; here L lanes share it, so the
+// redundant part of every column step shrinks 64 / L times while the update of the later columns
+// (the row's working values, VPL = 128 / L per lane, lane ll holding columns VPL ll .. +VPL - 1)
+// stays lane-parallel. Column i's value comes from its owner lane by a shuffle inside the row's
+// lane group; the group grid reduces min / max over the same L lanes. Each element sees exactly
+// the reference's operations in the reference's order (src/engine.rs:397-451); the registers of
+// columns already quantized keep taking updates that are never read.
+template <int L>
+__global__ __launch_bounds__(256) void k_gptq_rows(int rows, int n, int i1, int cnt, int g, int ng,
+                                                   const float* __restrict__ w, const float* __restrict__ u,
+                                                   const float* __restrict__ invd,
+                                                   const uint8_t* __restrict__ gbits, float* __restrict__ scales,
+                                                   float* __restrict__ zeros, uint8_t* __restrict__ codes,
+                                                   float* __restrict__ wq, float* __restrict__ err,
+                                                   unsigned long long* __restrict__ mid) {
+  constexpr int VPL = 128 / L;  // columns per lane
+  constexpr int R = 64 / L;     // rows per wavefront
+  __shared__ float ub[128 * 128];
+  __shared__ float idv[128];
+  {  // stage the block of U (zero outside cnt x cnt) and 1 / U_ii: clamped, unconditional loads
+    constexpr int PER = 128 * 128 / 256, BATCH = 16;
+#pragma unroll
+    for (int b = 0; b < PER; b += BATCH) {
+      float v[BATCH];
+#pragma unroll
+      for (int q = 0; q < BATCH; ++q) {
+        const int x = threadIdx.x + 256 * (b + q), i = x >> 7, c = x & 127;
+        v[q] = u[(long)(i1 + min(i, cnt - 1)) * n + i1 + min(c, cnt - 1)];
+      }
+#pragma unroll
+      for (int q = 0; q < BATCH; ++q) {
+        const int x = threadIdx.x + 256 * (b + q), i = x >> 7, c = x & 127;
+        ub[x] = (i < cnt && c < cnt) ? v[q] : 0.0f;
+      }
+    }
+    if (threadIdx.x < 128) idv[threadIdx.x] = invd[i1 + min((int)threadIdx.x, cnt - 1)];
+    __syncthreads();
+  }
+  const int lane = threadIdx.x & 63;
+  const int rr = lane / L, ll = lane % L;
+  const int r = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R + rr;
+  if (__builtin_amdgcn_readfirstlane(r - rr) >= rows) return;  // the wave's first row
+  const bool live = r < rows;
+  const float* wr = w + (long)min(r, rows - 1) * n + i1;
+  float x[VPL], mq[VPL], mwq[VPL], me[VPL];
+#pragma unroll
+  for (int t = 0; t < VPL; ++t) {
+    const int c = VPL * ll + t;
+    x[t] = (c < cnt) ? wr[c] : 0.0f;
+    mq[t] = 0.0f;
+    mwq[t] = 0.0f;
+    me[t] = 0.0f;
+  }
+  float sc = 0.0f, zr = 0.0f, maxq = 0.0f;
+  unsigned near_codes = 0, near_zeros = 0;  // counted once per row, by its lane 0
+  const int base = rr * L;                  // the row group's first lane
+  for (int oi = 0; oi < L; ++oi) {          // owner lane of the columns VPL oi .. +VPL - 1
+#pragma unroll
+    for (int t = 0; t < VPL; ++t) {
+      const int i = VPL * oi + t;
+      if (i < cnt) {  // uniform
+        const int j = i1 + i;
+        if (j % g == 0) {  // group grid over the group's columns, all inside the block
+          const int gi = j / g, gend = min(i + g, cnt);
+          maxq = (float)((1u << gbits[gi]) - 1u);
+          float lmin = INFINITY, lmax = -INFINITY;
+#pragma unroll
+          for (int t2 = 0; t2 < VPL; ++t2) {
+            const int c = VPL * ll + t2;
+            if (c >= i && c < gend) {
+              lmin = rs_minf(lmin, x[t2]);
+              lmax = rs_maxf(lmax, x[t2]);
+            }
+          }
+#pragma unroll
+          for (int o = L / 2; o > 0; o >>= 1) {
+            lmin = rs_minf(lmin, __shfl_xor(lmin, o, 64));
+            lmax = rs_maxf(lmax, __shfl_xor(lmax, o, 64));
+          }
+          float xmin = rs_minf(0.0f, lmin), xmax = rs_maxf(0.0f, lmax);
+          if (xmin == 0.0f && xmax == 0.0f) {
+            xmin = -1.0f;
+            xmax = 1.0f;
+          }
+          grid_mk(xmin, xmax, maxq, &sc, &zr);
+          if (ll == 0) {
+            near_zeros += near_midpoint(-xmin, sc, 0.0f, maxq) ? 1u : 0u;
+            if (live) {
+              scales[(long)r * ng + gi] = sc;
+              zeros[(long)r * ng + gi] = zr;
+            }
+          }
+        }
+        float uv[VPL];
+#pragma unroll
+        for (int t2 = 0; t2 < VPL; ++t2) uv[t2] = ub[i * 128 + VPL * ll + t2];
+        const float di = idv[i];
+        const float xv = __shfl(x[t], base + oi, 64);
+        float q;
+        const float dq = quant_dq(xv, sc, zr, maxq, &q);
+        if (ll == 0) near_codes += near_midpoint(xv, sc, zr, maxq) ? 1u : 0u;
+        const float e = (xv - dq) * di;
+        if (ll == oi) {
+          mq[t] = q;
+          mwq[t] = dq;
+          me[t] = e;
+        }
+#pragma unroll
+        for (int t2 = 0; t2 < VPL; ++t2) x[t2] = x[t2] - e * uv[t2];
+      }
+    }
+  }
+  if (live) {
+#pragma unroll
+    for (int t = 0; t < VPL; ++t) {
+      const int c = VPL * ll + t;
+      if (c < cnt) {
+        const long o = (long)r * n + i1 + c;
+        codes[o] = code_of(mq[t]);
+        wq[o] = mwq[t];
+        err[o] = me[t];
+      }
+    }
+    if (near_codes) atomicAdd(&mid[MID_CODE_NEAR], (unsigned long long)near_codes);
+    if (near_zeros) atomicAdd(&mid[MID_ZERO_NEAR], (unsigned long long)near_zeros);
+  }
+}
+
 // Phase-1 block sweep for blocks wider than 1024 columns (the register kernel above holds at most
 // 16 values per lane). Same per-element operations and order; the block's working values live in
 // the row of w itself (columns i1..i2, dead after the block: the lazy update reads only columns
@@ -602,7 +732,23 @@ static int npl_for(int cnt) {
 
 hipError_t gptq_block(hipStream_t st, int rows, int n, int i1, int cnt, int g, int ng, float* w, const float* u,
                       const float* invd, const uint8_t* gbits, int mse, float* scales, float* zeros, uint8_t* codes,
-                      float* wq, float* err, unsigned long long* mid) {
+                      float* wq, float* err, unsigned long long* mid, bool groups_in_block) {
+  // Lanes per row: as few as keep about two wavefronts per SIMD busy (1024 SIMDs), at least 8.
+  if (groups_in_block && !mse && cnt <= 128 && i1 % g == 0 && rows >= 2048) {
+    const int lanes = rows >= 16384 ? 8 : (rows >= 8192 ? 16 : 32);
+    const int rpw = 64 / lanes, wg_rows = 4 * rpw;
+    const dim3 grid2((rows + wg_rows - 1) / wg_rows), blk2(256);
+    if (lanes == 8)
+      hipLaunchKernelGGL(k_gptq_rows<8>, grid2, blk2, 0, st, rows, n, i1, cnt, g, ng, w, u, invd, gbits, scales, zeros,
+                         codes, wq, err, mid);
+    else if (lanes == 16)
+      hipLaunchKernelGGL(k_gptq_rows<16>, grid2, blk2, 0, st, rows, n, i1, cnt, g, ng, w, u, invd, gbits, scales,
+                         zeros, codes, wq, err, mid);
+    else
+      hipLaunchKernelGGL(k_gptq_rows<32>, grid2, blk2, 0, st, rows, n, i1, cnt, g, ng, w, u, invd, gbits, scales,
+                         zeros, codes, wq, err, mid);
+    return hipGetLastError();
+  }
   const dim3 grid((rows + GB_ROWS - 1) / GB_ROWS), blk(64 * GB_ROWS);
 #define GPTQ_CASE(N)                                                                                                   \
   case N:                                                                                                              \

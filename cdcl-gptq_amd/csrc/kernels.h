@@ -81,9 +81,12 @@ hipError_t permute_m(hipStream_t st, int n, const float* m, const uint32_t* perm
 hipError_t diag_extract(hipStream_t st, int n, const float* h, float* diag);
 hipError_t colsq(hipStream_t st, int d_out, int n, const float* w, const uint8_t* dead, double* out);
 hipError_t inv_diag(hipStream_t st, int n, const float* u, float* invd);
+// Phase-1 sweep of block [i1, i1 + cnt) for all rows. groups_in_block: every group grid of the
+// block reads only columns of the block (the block width is a multiple of the group size), which
+// allows the lanes-per-row kernel.
 hipError_t gptq_block(hipStream_t st, int rows, int n, int i1, int cnt, int g, int ng, float* w, const float* u,
                       const float* invd, const uint8_t* gbits, int mse, float* scales, float* zeros, uint8_t* codes,
-                      float* wq, float* err, unsigned long long* mid);
+                      float* wq, float* err, unsigned long long* mid, bool groups_in_block);
 hipError_t colloss(hipStream_t st, int rows, int n, int rc, const float* err, double* out);
 hipError_t sub_f32(hipStream_t st, size_t count, const float* a, const float* b, float* out);
 // ---- k_repair.hip: phase 2

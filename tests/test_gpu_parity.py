@@ -313,6 +313,16 @@ def test_quantize_refit_row_tilings(ctx, d_out):
                 label=f"refit rows {d_out}")
 
 
+@pytest.mark.parametrize("d_out", [2500, 4500, 8200])
+def test_quantize_block_sweep_lane_groups(ctx, d_out):
+    """The phase-1 sweep with several rows per wavefront (32, 16 and 8 lanes per row for 2500, 4500
+    and 8200 rows; ragged last workgroup), group 64 inside the 128-column block (two group grids
+    per block) and a ragged last block (n = 320)."""
+    w, x, h, _ = synth_layer(50 + d_out % 11, d_out, 320, 1100)
+    assert_same(*run_both(ctx, w, h, bits=3, group=64, block=128, act_order=True, passes=2, row_chunk=64),
+                label=f"sweep lanes {d_out}")
+
+
 def test_quantize_wide_gradient_tiles(ctx):
     """128-column repair gradients with at least four (row tile, panel) units per CU take the
     128 x 128 / 8-wave tile (one E tile read per unit): 131150 rows x 768 columns is 1025 row
