@@ -317,7 +317,8 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
         store_p(pu);
         acc = v32f{};
       }
-      if (!DIRECT || cs + 1 < cu.nst) issue_next();  // into the slot of stage fc - 1
+      // C is loaded before the stage after next, so the next stage's wait (everything but the
+      // newest stage's loads) covers it rather than also holding back that stage.
       if (DIRECT && cs == 0) {
 #pragma unroll
         for (int r = 0; r < 32; ++r) {  // clamped addresses; values outside m x wd are never used
@@ -326,6 +327,7 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
           cv[r] = beta_one ? C[(long)row * ldc + col] : 0.0f;
         }
       }
+      if (!DIRECT || cs + 1 < cu.nst) issue_next();  // into the slot of stage fc - 1
       const float* buf = &R[fc % DNB][0];
       const float* es = buf + 32 * er;
       const float* hs = buf + DSK * PR + lane;
@@ -473,8 +475,7 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
         store_p(pu);
         acc = v32f{};
       }
-      if (!DIRECT || cs + 1 < cu.nst) issue_next();
-      if (DIRECT && cs == 0) {
+      if (DIRECT && cs == 0) {  // before the stage after next, as in k_panel_dma
 #pragma unroll
         for (int r = 0; r < 32; ++r) {
           const int row = min(cu.r0 + 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), m - 1);
@@ -482,6 +483,7 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
           cv[r] = C[(long)row * ldc + col];
         }
       }
+      if (!DIRECT || cs + 1 < cu.nst) issue_next();
       const float* buf = &R[fc % DNB][0];
       const float* es = buf + 32 * er;
       const float* hs = buf + DSK * PR + 64 * wc + lane;
