@@ -916,24 +916,41 @@ __global__ __launch_bounds__(256) void k_refit_mfma(int rows, int n, int ng, int
 // order, since the columns before it saw exactly this gradient and kept their codes. The move is
 // applied (gradient update over the whole sub-block, wave-parallel), the cursor jumps past it and
 // the columns after it are evaluated again. A sweep therefore costs one round per move plus one.
-// One element of G = E H[:, c0:c0+wd] from the per-panel chains of the gradient GEMM (stride
-// pstride between panels): the ordered fold of k_fold, C = fma(1, P_p, C) from C = 0.
-__device__ __forceinline__ float fold_chains(const float* __restrict__ src, long pstride, int np) {
-  float acc = 0.0f;
-  int p = 0;
-  for (; p + 8 <= np; p += 8) {
-    float v[8];
+// NPL elements of one row of G = E H[:, c0:c0+wd] (columns 64 s + lane) from the per-panel chains
+// of the gradient GEMM (P[p][row][col], stride pstride between panels): the ordered fold of
+// k_fold, C = fma(1, P_p, C) for p = 0, 1, ... from C = 0. Loads go out in batches of B panels
+// for every column (NPL * B loads in flight); the last batch is predicated, not split into
+// single loads, and only loaded panels are added.
+template <int NPL, int B>
+__device__ __forceinline__ void fold_chains(const float* __restrict__ src, long pstride, int np, int wd, int lane,
+                                            float (&gg)[NPL]) {
+  float acc[NPL];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(src + (long)(p + u) * pstride);
+  for (int s = 0; s < NPL; ++s) acc[s] = 0.0f;
+  for (int p = 0; p < np; p += B) {
+    float v[NPL][B];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(1.0f, v[u], acc);
+    for (int u = 0; u < B; ++u) {
+      const int pu = min(p + u, np - 1);
+#pragma unroll
+      for (int s = 0; s < NPL; ++s)
+        v[s][u] = __builtin_nontemporal_load(src + (long)pu * pstride + min(s * 64 + lane, wd - 1));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before the first add
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      if (p + u < np) {  // uniform
+#pragma unroll
+        for (int s = 0; s < NPL; ++s) acc[s] = __builtin_fmaf(1.0f, v[s][u], acc[s]);
+      }
+    }
   }
-  for (; p < np; ++p) acc = __builtin_fmaf(1.0f, __builtin_nontemporal_load(src + (long)p * pstride), acc);
-  return acc;
+#pragma unroll
+  for (int s = 0; s < NPL; ++s) gg[s] = s * 64 + lane < wd ? acc[s] : 0.0f;
 }
 
 template <int NPL>
-__global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NPL == 1 ? 8 : 1))) void k_cd(int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
                                             int sweeps, const float* __restrict__ G, const float* __restrict__ h32,
                                             const uint8_t* __restrict__ gbits, const float* __restrict__ scales,
                                             const float* __restrict__ zeros, uint8_t* __restrict__ codes,
@@ -942,36 +959,70 @@ __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int 
                                             double* __restrict__ dlog, uint32_t* __restrict__ dcnt, int cap,
                                             unsigned long long* __restrict__ mid, uint32_t* __restrict__ evals,
                                             const float* __restrict__ P, int np) {
+  // Sub-blocks of up to 64 columns keep H_CC (the sub-block's rows and columns of h32, 16 KB) in
+  // LDS, shared by the workgroup's rows: the gradient update after a move reads its row from there.
+  constexpr int HW = NPL * 64;
+  constexpr bool HLDS = NPL == 1;
+  __shared__ float hs[HLDS ? HW * HW : 1];
   const int lane = threadIdx.x & 63;
   const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
-  if (r >= rows) return;
-  const int chunk = r / rc;
-  if (!active[chunk] || !sel[(long)chunk * nsb + sb]) {
-    if (lane == 0) dcnt[r] = 0;
-    return;
+  // The H_CC loads go out with the row's selection test and are written to LDS after the fold.
+  constexpr int HPER = HLDS ? HW * HW / 256 : 1;
+  float hv[HPER];
+  if (HLDS) {  // clamped addresses; entries outside wd x wd are never read
+#pragma unroll
+    for (int q = 0; q < HPER; ++q) {
+      const int x = threadIdx.x + 256 * q, i = x / HW, c = x % HW;
+      hv[q] = h32[(long)(c0 + min(i, wd - 1)) * n + c0 + min(c, wd - 1)];
+    }
   }
+  const int chunk = min(r, rows - 1) / rc;
+  uint32_t act = active[chunk], pick = sel[(long)chunk * nsb + sb];
+  asm volatile("" : "+v"(act), "+v"(pick));  // both loads issued before either is tested
+  const bool live = r < rows && act && pick;
   // per-column state and parameters, one column per lane and slice; the gradient is either G or,
   // with P, folded here from the GEMM's per-panel chains (P[p][row][col], rows x wd per panel)
   float gg[NPL], mwq[NPL], me[NPL], hd[NPL], sc[NPL], zz[NPL], mq[NPL];
   int mc[NPL];
+  uint8_t gb[NPL];
+  if (live) {
+    // unconditional clamped loads; lanes past wd are never selected or stored
 #pragma unroll
-  for (int s = 0; s < NPL; ++s) {
-    const int k = s * 64 + lane;
-    const bool in = k < wd;
-    const int j = c0 + min(k, wd - 1);
-    const long o = (long)r * n + j;
-    const int gi = j / g;
-    if (P)
-      gg[s] = in ? fold_chains(P + (long)r * wd + k, (long)rows * wd, np) : 0.0f;
-    else
-      gg[s] = in ? G[(long)r * wd + k] : 0.0f;
-    mwq[s] = in ? wq[o] : 0.0f;
-    me[s] = in ? e[o] : 0.0f;
-    mc[s] = in ? (int)codes[o] : 0;
-    hd[s] = h32[(long)j * n + j];
-    sc[s] = scales[(long)r * ng + gi];
-    zz[s] = zeros[(long)r * ng + gi];
-    mq[s] = (float)((1u << gbits[gi]) - 1u);
+    for (int s = 0; s < NPL; ++s) {
+      const int j = c0 + min(s * 64 + lane, wd - 1);
+      const long o = (long)r * n + j;
+      const int gi = j / g;
+      mwq[s] = wq[o];
+      me[s] = e[o];
+      mc[s] = (int)codes[o];
+      hd[s] = h32[(long)j * n + j];
+      sc[s] = scales[(long)r * ng + gi];
+      zz[s] = zeros[(long)r * ng + gi];
+      gb[s] = gbits[gi];
+    }
+    if (P) {
+      fold_chains<NPL, (NPL <= 2 ? 16 / NPL : 2)>(P + (long)r * wd, (long)rows * wd, np, wd, lane, gg);
+    } else {
+#pragma unroll
+      for (int s = 0; s < NPL; ++s) gg[s] = s * 64 + lane < wd ? G[(long)r * wd + s * 64 + lane] : 0.0f;
+    }
+#pragma unroll
+    for (int s = 0; s < NPL; ++s) {
+      const bool in = s * 64 + lane < wd;
+      mwq[s] = in ? mwq[s] : 0.0f;
+      me[s] = in ? me[s] : 0.0f;
+      mc[s] = in ? mc[s] : 0;
+      mq[s] = (float)((1u << gb[s]) - 1u);
+    }
+  }
+  if (HLDS) {
+#pragma unroll
+    for (int q = 0; q < HPER; ++q) hs[threadIdx.x + 256 * q] = hv[q];
+    __syncthreads();
+  }
+  if (!live) {
+    if (r < rows && lane == 0) dcnt[r] = 0;
+    return;
   }
   uint32_t moves = 0, nevals = 0, nnear = 0;
   double* dl = dlog + (long)r * cap;
@@ -1004,7 +1055,7 @@ __global__ __launch_bounds__(256) void k_cd(int rows, int n, int ng, int g, int 
         const float d32 = (2.0f * de) * gj + (de * de) * hjj;
         if (lane == 0) dl[moves] = (double)d32;
         ++moves;
-        const float* hrow = h32 + (long)(c0 + s * 64 + jl) * n + c0;
+        const float* hrow = HLDS ? &hs[(s * 64 + jl) * HW] : h32 + (long)(c0 + s * 64 + jl) * n + c0;
 #pragma unroll
         for (int s2 = 0; s2 < NPL; ++s2) {  // lanes past wd (never selected, never stored) take
           const int k = s2 * 64 + lane;       // garbage: no predicate, clamped address
