@@ -487,6 +487,9 @@ def main():
                     help="with --workload container: counter-collection run (1 GiB copy + one step)")
     ap.add_argument("--cpu-validate", action="store_true",
                     help="time the CPU baseline's rows x n^2 model against a down_proj-width sample and exit")
+    ap.add_argument("--floor-rows", type=int, default=0,
+                    help="latency-floor run (under a kernel trace): the config's matrices cut to their first "
+                         "FLOOR_ROWS rows, same inputs and settings, one untimed step; prints the phase times")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
@@ -497,6 +500,11 @@ def main():
     import cdclq
 
     spec = CONFIGS[args.config]
+    if args.floor_rows > 0:
+        # the same matrices with fewer rows in flight: each sweep launch then runs its rows'
+        # dependent chains with no other waves on their SIMDs
+        spec = dict(spec, layers=[(name, min(d_out, args.floor_rows), key) for name, d_out, key in spec["layers"]])
+        args.steps, args.warmup, args.no_cpu_baseline = 1, 0, True
     if args.cpu_validate:
         cpu_validate(spec, min(os.cpu_count() or 1, 16))
         return
@@ -577,6 +585,12 @@ def main():
     achieved = flops / (gram_ms * 1e-3) / 1e12 if gram_ms > 0 else 0.0
     phases = {k: round(v["ms"] / args.steps, 3) for k, v in ph.items()}
     log(f"[bench] device ms per step by phase: {phases}")
+    if args.floor_rows > 0:
+        print(json.dumps({"profile": "floor-rows", "workload": spec["workload"], "rows": args.floor_rows,
+                          "layers": {name: [d_out, spec["inputs"][key]] for name, d_out, key in spec["layers"]},
+                          "phases_ms": phases}), flush=True)
+        ctx.close()
+        return
     result = {
         "metric": "sec per Llama-3-8B-shaped layer (H-accum+U+GPTQ+repair); MFMA util, HBM GB/s"
         if args.config == "c4" else f"sec per layer ({spec['workload']})",

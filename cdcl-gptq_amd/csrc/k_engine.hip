@@ -266,9 +266,10 @@ __global__ __launch_bounds__(64 * GB_ROWS) void k_gptq_block(int rows, int n, in
 // stays lane-parallel. Column i's value comes from its owner lane by a shuffle inside the row's
 // lane group; the group grid reduces min / max over the same L lanes. Each element sees exactly
 // the reference's operations in the reference's order (src/engine.rs:397-451); the registers of
-// columns already quantized keep taking updates that are never read.
-template <int L>
-__global__ __launch_bounds__(256) void k_gptq_rows(int rows, int n, int i1, int cnt, int g, int ng,
+// columns already quantized keep taking updates that are never read. W wavefronts per workgroup
+// share the staged block of U (64 KB, so two workgroups per CU).
+template <int L, int W>
+__global__ __launch_bounds__(64 * W) void k_gptq_rows(int rows, int n, int i1, int cnt, int g, int ng,
                                                    const float* __restrict__ w, const float* __restrict__ u,
                                                    const float* __restrict__ invd,
                                                    const uint8_t* __restrict__ gbits, float* __restrict__ scales,
@@ -280,18 +281,18 @@ __global__ __launch_bounds__(256) void k_gptq_rows(int rows, int n, int i1, int 
   __shared__ float ub[128 * 128];
   __shared__ float idv[128];
   {  // stage the block of U (zero outside cnt x cnt) and 1 / U_ii: clamped, unconditional loads
-    constexpr int PER = 128 * 128 / 256, BATCH = 16;
+    constexpr int NT = 64 * W, PER = 128 * 128 / NT, BATCH = PER < 16 ? PER : 16;
 #pragma unroll
     for (int b = 0; b < PER; b += BATCH) {
       float v[BATCH];
 #pragma unroll
       for (int q = 0; q < BATCH; ++q) {
-        const int x = threadIdx.x + 256 * (b + q), i = x >> 7, c = x & 127;
+        const int x = threadIdx.x + NT * (b + q), i = x >> 7, c = x & 127;
         v[q] = u[(long)(i1 + min(i, cnt - 1)) * n + i1 + min(c, cnt - 1)];
       }
 #pragma unroll
       for (int q = 0; q < BATCH; ++q) {
-        const int x = threadIdx.x + 256 * (b + q), i = x >> 7, c = x & 127;
+        const int x = threadIdx.x + NT * (b + q), i = x >> 7, c = x & 127;
         ub[x] = (i < cnt && c < cnt) ? v[q] : 0.0f;
       }
     }
@@ -300,18 +301,26 @@ __global__ __launch_bounds__(256) void k_gptq_rows(int rows, int n, int i1, int 
   }
   const int lane = threadIdx.x & 63;
   const int rr = lane / L, ll = lane % L;
-  const int r = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R + rr;
+  const int r = (blockIdx.x * W + (threadIdx.x >> 6)) * R + rr;
   if (__builtin_amdgcn_readfirstlane(r - rr) >= rows) return;  // the wave's first row
   const bool live = r < rows;
   const float* wr = w + (long)min(r, rows - 1) * n + i1;
-  float x[VPL], mq[VPL], mwq[VPL], me[VPL];
+  // the owned columns' results; with 16 columns per lane the codes are kept one byte each (the
+  // registers then allow four wavefronts per SIMD)
+  constexpr bool PACK = VPL >= 16;
+  float x[VPL], mwq[VPL], me[VPL], mq[PACK ? 1 : VPL];
+  uint32_t mcode[PACK ? VPL / 4 : 1];
 #pragma unroll
   for (int t = 0; t < VPL; ++t) {
     const int c = VPL * ll + t;
     x[t] = (c < cnt) ? wr[c] : 0.0f;
-    mq[t] = 0.0f;
     mwq[t] = 0.0f;
     me[t] = 0.0f;
+    if constexpr (PACK) {
+      if ((t & 3) == 0) mcode[t >> 2] = 0u;
+    } else {
+      mq[t] = 0.0f;
+    }
   }
   float sc = 0.0f, zr = 0.0f, maxq = 0.0f;
   unsigned near_codes = 0, near_zeros = 0;  // counted once per row, by its lane 0
@@ -363,7 +372,10 @@ __global__ __launch_bounds__(256) void k_gptq_rows(int rows, int n, int i1, int 
         if (ll == 0) near_codes += near_midpoint(xv, sc, zr, maxq) ? 1u : 0u;
         const float e = (xv - dq) * di;
         if (ll == oi) {
-          mq[t] = q;
+          if constexpr (PACK)
+            mcode[t >> 2] = (mcode[t >> 2] & ~(0xffu << (8 * (t & 3)))) | ((uint32_t)code_of(q) << (8 * (t & 3)));
+          else
+            mq[t] = q;
           mwq[t] = dq;
           me[t] = e;
         }
@@ -378,7 +390,10 @@ __global__ __launch_bounds__(256) void k_gptq_rows(int rows, int n, int i1, int 
       const int c = VPL * ll + t;
       if (c < cnt) {
         const long o = (long)r * n + i1 + c;
-        codes[o] = code_of(mq[t]);
+        if constexpr (PACK)
+          codes[o] = (uint8_t)(mcode[t >> 2] >> (8 * (t & 3)));
+        else
+          codes[o] = code_of(mq[t]);
         wq[o] = mwq[t];
         err[o] = me[t];
       }
@@ -734,19 +749,19 @@ hipError_t gptq_block(hipStream_t st, int rows, int n, int i1, int cnt, int g, i
                       const float* invd, const uint8_t* gbits, int mse, float* scales, float* zeros, uint8_t* codes,
                       float* wq, float* err, unsigned long long* mid, bool groups_in_block) {
   // Lanes per row: as few as keep about two wavefronts per SIMD busy (1024 SIMDs), at least 8.
+  // Two 64 KB workgroups per CU, every row resident at once up to 32768 rows: 32 lanes per row
+  // and 4 wavefronts per workgroup up to 4096 rows (at most 2 wavefronts per SIMD), 16 lanes and
+  // 8 wavefronts up to 16384 (at most 4 per SIMD), 8 lanes and 8 wavefronts above.
   if (groups_in_block && !mse && cnt <= 128 && i1 % g == 0 && rows >= 2048) {
-    const int lanes = rows >= 16384 ? 8 : (rows >= 8192 ? 16 : 32);
-    const int rpw = 64 / lanes, wg_rows = 4 * rpw;
-    const dim3 grid2((rows + wg_rows - 1) / wg_rows), blk2(256);
-    if (lanes == 8)
-      hipLaunchKernelGGL(k_gptq_rows<8>, grid2, blk2, 0, st, rows, n, i1, cnt, g, ng, w, u, invd, gbits, scales, zeros,
-                         codes, wq, err, mid);
-    else if (lanes == 16)
-      hipLaunchKernelGGL(k_gptq_rows<16>, grid2, blk2, 0, st, rows, n, i1, cnt, g, ng, w, u, invd, gbits, scales,
-                         zeros, codes, wq, err, mid);
+    if (rows > 16384)
+      hipLaunchKernelGGL((k_gptq_rows<8, 8>), dim3((rows + 63) / 64), dim3(512), 0, st, rows, n, i1, cnt, g, ng, w, u,
+                         invd, gbits, scales, zeros, codes, wq, err, mid);
+    else if (rows > 4096)
+      hipLaunchKernelGGL((k_gptq_rows<16, 8>), dim3((rows + 31) / 32), dim3(512), 0, st, rows, n, i1, cnt, g, ng, w,
+                         u, invd, gbits, scales, zeros, codes, wq, err, mid);
     else
-      hipLaunchKernelGGL(k_gptq_rows<32>, grid2, blk2, 0, st, rows, n, i1, cnt, g, ng, w, u, invd, gbits, scales,
-                         zeros, codes, wq, err, mid);
+      hipLaunchKernelGGL((k_gptq_rows<32, 4>), dim3((rows + 7) / 8), dim3(256), 0, st, rows, n, i1, cnt, g, ng, w, u,
+                         invd, gbits, scales, zeros, codes, wq, err, mid);
     return hipGetLastError();
   }
   const dim3 grid((rows + GB_ROWS - 1) / GB_ROWS), blk(64 * GB_ROWS);

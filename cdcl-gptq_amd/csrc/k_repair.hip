@@ -690,10 +690,12 @@ __global__ __launch_bounds__(256) void k_refit(int rows, int n, int ng, int g, i
 // k_refit. hu = U H_CC (U = codes - zero, one row per row of the group) is a K = 1 chain per
 // element in k order (one KC panel), so a K = 1 MFMA computes it as the sgemm does. 64 rows:
 // v_mfma_f32_32x32x1_2b_f32, wave w takes rows 32 (w >> 1) .. +31 and columns 64 (w & 1) .. +63.
-// 16 rows (for matrices with too few rows to give every CU a 64-row workgroup): waves 0 and 1
-// take columns 64 w .. +63 with v_mfma_f32_16x16x1_4b_f32, its four 16 x 16 blocks side by side
-// (lane l supplies A = u of row l % 16 and B = H_CC column 64 w + l; D register r of lane l is
-// row 4 (l >> 4) + (r & 3), column 64 w + 16 (r >> 2) + (l & 15)). A = u is read from the codes
+// 32 and 16 rows (two resident workgroups per CU, for matrices whose rows fit that way in one
+// round): v_mfma_f32_16x16x1_4b_f32, its four 16 x 16 blocks side by side, half the chain latency
+// of the 32 x 32 form; wave w takes rows 16 (w >> 1) .. +15 (32 rows; with 16 rows only waves 0
+// and 1) and columns 64 (w & 1) .. +63 (lane l supplies A = u of row 16 (w >> 1) + l % 16 and
+// B = H_CC column 64 (w & 1) + l; D register r of lane l is row 16 (w >> 1) + 4 (l >> 4) + (r & 3),
+// column 64 (w & 1) + 16 (r >> 2) + (l & 15)). A = u is read from the codes
 // staged in LDS, B = H_CC staged in LDS. The products u_k hu_k and u_k g_k are then formed in
 // parallel into LDS, the sequential sums num = sum u_k g_k and den = sum u_k hu_k run one lane per
 // row, and the accepted rows' e and W_hat are updated by the whole workgroup along the columns.
@@ -773,10 +775,10 @@ __global__ __launch_bounds__(256) void k_refit_mfma(int rows, int n, int ng, int
   __syncthreads();
   // hu chains on the matrix cores
   constexpr bool R64 = RF_ROWS == 64;
-  static_assert(RF_ROWS == 64 || RF_ROWS == 16, "64- or 16-row workgroups");
-  const int wr = R64 ? wv >> 1 : 0, wc = R64 ? wv & 1 : wv;
-  const bool mwave = R64 || wv < 2;
-  const int arow = R64 ? 32 * wr + (lane & 31) : (lane & 15);
+  static_assert(RF_ROWS == 64 || RF_ROWS == 32 || RF_ROWS == 16, "64-, 32- or 16-row workgroups");
+  const int wr = RF_ROWS == 16 ? 0 : wv >> 1, wc = wv & 1;
+  const bool mwave = RF_ROWS != 16 || wv < 2;
+  const int arow = R64 ? 32 * wr + (lane & 31) : 16 * wr + (lane & 15);
   const float za = zrow[arow];
   const uint32_t* crow = CB + arow * (RF_CS / 4);
   const float* hcol = S + 64 * (wc & 1) + lane;
@@ -813,7 +815,8 @@ __global__ __launch_bounds__(256) void k_refit_mfma(int rows, int n, int ng, int
   if (mwave) {
 #pragma unroll
     for (int r = 0; r < (R64 ? 32 : 16); ++r) {  // panel end C = fma(1, chain, 0), then u_k * hu_k
-      const int row = R64 ? 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5) : 4 * (lane >> 4) + (r & 3);
+      const int row = R64 ? 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5)
+                          : 16 * wr + 4 * (lane >> 4) + (r & 3);
       const int col = R64 ? 64 * wc + 32 * (r >> 4) + (lane & 31) : 64 * wc + 16 * (r >> 2) + (lane & 15);
       const float u = (float)cb[row * RF_CS + col] - zrow[row];
       PH[row * RF_PS + col] = u * __builtin_fmaf(1.0f, acc[r], 0.0f);
@@ -1339,15 +1342,19 @@ hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, i
                        const uint8_t* active, double* dlog, uint32_t* dcnt) {
   const int wd = std::min(gi * g + g, n) - gi * g;
   if (wd <= 128) {
-    // 64-row workgroups while they give at least half of the CUs one; 16-row ones below that
+    // the smallest workgroups (shortest chains) whose count still fits two per CU, so that all
+    // rows are resident in one round; 64-row ones beyond that
     int cus = 0;
     const hipError_t err = cu_count(&cus);
     if (err != hipSuccess) return err;
-    if ((rows + 63) / 64 >= cus / 2)
-      hipLaunchKernelGGL(k_refit_mfma<64>, dim3((rows + 63) / 64), dim3(256), 0, st, rows, n, ng, g, gi, rc, G, h32,
+    if ((rows + 15) / 16 <= 2 * cus)
+      hipLaunchKernelGGL(k_refit_mfma<16>, dim3((rows + 15) / 16), dim3(256), 0, st, rows, n, ng, g, gi, rc, G, h32,
+                         codes, scales, zeros, wq, e, active, dlog, dcnt);
+    else if ((rows + 31) / 32 <= 2 * cus)
+      hipLaunchKernelGGL(k_refit_mfma<32>, dim3((rows + 31) / 32), dim3(256), 0, st, rows, n, ng, g, gi, rc, G, h32,
                          codes, scales, zeros, wq, e, active, dlog, dcnt);
     else
-      hipLaunchKernelGGL(k_refit_mfma<16>, dim3((rows + 15) / 16), dim3(256), 0, st, rows, n, ng, g, gi, rc, G, h32,
+      hipLaunchKernelGGL(k_refit_mfma<64>, dim3((rows + 63) / 64), dim3(256), 0, st, rows, n, ng, g, gi, rc, G, h32,
                          codes, scales, zeros, wq, e, active, dlog, dcnt);
     return hipGetLastError();
   }

@@ -303,24 +303,35 @@ def test_quantize_repair_knobs(ctx):
                     label=str(kw))
 
 
-@pytest.mark.parametrize("d_out", [1000, 8256])
+@pytest.mark.parametrize("d_out", [1000, 8256, 16450])
 def test_quantize_refit_row_tilings(ctx, d_out):
-    """The group refit runs 16-row workgroups when 64-row ones would leave more than half of the
-    CUs idle (fewer than 64 x CUs / 2 rows, 8128 on a 256-CU part) and 64-row ones above: 1000 rows
-    take the 16-row form (ragged last workgroup), 8256 the 64-row form (ragged last workgroup)."""
+    """The group refit takes the smallest workgroups (16, 32 or 64 rows) whose count fits two per
+    CU: on a 256-CU part 1000 rows take the 16-row form, 8256 the 32-row form and 16450 the 64-row
+    form, each with a ragged last workgroup."""
     w, x, h, _ = synth_layer(40 + d_out % 7, d_out, 256, 1024)
     assert_same(*run_both(ctx, w, h, bits=4, group=128, block=128, act_order=True, passes=3, row_chunk=64),
                 label=f"refit rows {d_out}")
 
 
-@pytest.mark.parametrize("d_out", [2500, 4500, 8200])
+@pytest.mark.parametrize("d_out", [2500, 4500, 8200, 16450])
 def test_quantize_block_sweep_lane_groups(ctx, d_out):
-    """The phase-1 sweep with several rows per wavefront (32, 16 and 8 lanes per row for 2500, 4500
-    and 8200 rows; ragged last workgroup), group 64 inside the 128-column block (two group grids
-    per block) and a ragged last block (n = 320)."""
+    """The phase-1 sweep with several rows per wavefront (32 lanes per row and 4 wavefronts per
+    workgroup for 2500 rows, 16 lanes and 8 wavefronts for 4500 and 8200, 8 lanes and 8
+    wavefronts for 16450; ragged last workgroup), group 64 inside the 128-column block (two group
+    grids per block) and a ragged last block (n = 320)."""
     w, x, h, _ = synth_layer(50 + d_out % 11, d_out, 320, 1100)
     assert_same(*run_both(ctx, w, h, bits=3, group=64, block=128, act_order=True, passes=2, row_chunk=64),
                 label=f"sweep lanes {d_out}")
+
+
+def test_quantize_descent_many_rows(ctx):
+    """The descent with more rows than the device keeps resident at once (one wavefront per row,
+    8192 on a 256-CU part): 8300 rows, ragged 48-column sub-blocks (n = 256 leaves a 16-column
+    last one), two sweeps, half of the sub-blocks selected per chunk."""
+    w, x, h, _ = synth_layer(61, 8300, 256, 1024)
+    assert_same(*run_both(ctx, w, h, bits=3, group=64, block=128, act_order=True, passes=3, sub_block=48,
+                          cd_sweeps=2, refine_frac=0.5, row_chunk=64),
+                label="descent pairs 8300")
 
 
 def test_quantize_wide_gradient_tiles(ctx):
