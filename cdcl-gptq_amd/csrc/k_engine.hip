@@ -55,11 +55,23 @@ __global__ __launch_bounds__(256) void k_colsq(int d_out, int n, const float* __
   const int j = blockIdx.x * 256 + threadIdx.x;
   if (j >= n) return;
   double s = 0.0;
-  if (!dead[j])
-    for (int r = 0; r < d_out; ++r) {
-      const double v = (double)w[(long)r * n + j];
-      s = s + v * v;
+  if (!dead[j]) {
+    // the sum stays sequential over the rows; the loads go out CS_BATCH rows ahead of the adds
+    constexpr int CS_BATCH = 32;
+    for (int r0 = 0; r0 < d_out; r0 += CS_BATCH) {
+      float v[CS_BATCH];
+#pragma unroll
+      for (int q = 0; q < CS_BATCH; ++q) v[q] = w[(long)min(r0 + q, d_out - 1) * n + j];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int q = 0; q < CS_BATCH; ++q) {
+        if (r0 + q < d_out) {
+          const double x = (double)v[q];
+          s = s + x * x;
+        }
+      }
     }
+  }
   out[j] = s;
 }
 

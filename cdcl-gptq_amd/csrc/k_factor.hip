@@ -63,12 +63,18 @@ __global__ __launch_bounds__(256) void k_build_flipped_f64(int n, const double* 
 // that column to its slots. LDS accesses of one wavefront complete in order, so a read issued
 // after a write sees it. Slot columns left of t's are skipped; the registers of finished columns
 // (and of the upper triangle) that are still updated are never read again.
+// The steps are software-pipelined: step t first updates the slot column that holds column t + 1
+// and publishes it, then runs column t + 1's pivot, square root and divisions while it applies
+// column t to the rest of its slots (no branch between them, so the two interleave), then stores
+// column t + 1 of L and reads it back for step t + 1. Every element still receives the same
+// operations in the same order. A failing pivot is recorded (the first one) and reported at the
+// end; the remaining steps run on with values that are discarded with the error.
 constexpr int DGL = 8;           // lane grid side
 constexpr int DSL = NBC / DGL;   // row / column slots per lane
 __global__ __launch_bounds__(64) void k_chol_diag(int n, double* __restrict__ a, int k, int kb, int* status,
                                                   double* pivot) {
-  __shared__ double pre[NBC];  // column t with all earlier columns applied, before the division
-  __shared__ double col[NBC];  // column t of L (zero above row t)
+  __shared__ double pre[NBC + 64];  // column t with all earlier columns applied; + a discard slot per lane
+  __shared__ double col[NBC];       // column t of L (zero above row t)
   if (*status) return;
   const int lane = threadIdx.x, tr = lane >> 3, tc = lane & 7;
   double v[DSL][DSL];
@@ -79,47 +85,83 @@ __global__ __launch_bounds__(64) void k_chol_diag(int n, double* __restrict__ a,
       const int i = DGL * r + tr, j = DGL * c + tc;
       v[r][c] = a[(long)(k + min(i, kb - 1)) * n + k + min(j, kb - 1)];
     }
-  // A pivot that is not positive and finite records the first failing step; the remaining steps
-  // run on (their values are discarded with the error), so the loops have no early exit.
-  bool failed = false;
+  int fail_t = -1;
+  double fail_d = 0.0;
+  double c0 = 0.0, c1 = 0.0;  // this lane's entries (rows lane, lane + 64) of the latest column of L
+  // column tn (slot column ctn, lanes tc == ltn) to LDS; the other lanes write their discard slot
+  auto publish = [&](int ctn, int ltn) {
+    const bool own = tc == ltn;
+#pragma unroll
+    for (int r = ctn; r < DSL; ++r) pre[own ? DGL * r + tr : NBC + lane] = v[r][ctn];
+  };
+  // pivot of column tn and the divided column of L into LDS (values past kb are computed from
+  // clamped reads and never stored)
+  auto divide = [&](int tn) {
+    const double d = pre[tn];
+    const bool rec = (!(d > 0.0) || !isfinite(d)) && fail_t < 0 && tn < kb;
+    fail_d = rec ? d : fail_d;
+    fail_t = rec ? tn : fail_t;
+    const double ltt = sqrt(d);
+    const double q0 = pre[lane] / ltt, q1 = pre[min(lane + 64, NBC - 1)] / ltt;
+    c0 = (lane == tn) ? ltt : ((lane > tn && lane < kb) ? q0 : 0.0);
+    c1 = (lane + 64 == tn) ? ltt : ((lane + 64 > tn && lane + 64 < kb) ? q1 : 0.0);
+    col[lane] = c0;
+    if (lane + 64 < NBC) col[lane + 64] = c1;
+  };
+  auto store_col = [&](int tn) {
+    if (lane >= tn && lane < kb) a[(long)(k + lane) * n + k + tn] = c0;
+    if (lane + 64 >= tn && lane + 64 < kb) a[(long)(k + lane + 64) * n + k + tn] = c1;
+  };
+  double ci[DSL], cj[DSL];  // column t of L at rows DGL q + tr (ci) and DGL q + tc (cj)
+  publish(0, 0);
+  divide(0);
+  store_col(0);
+#pragma unroll
+  for (int q = 0; q < DSL; ++q) {
+    ci[q] = col[DGL * q + tr];
+    cj[q] = col[DGL * q + tc];
+  }
 #pragma unroll
   for (int ct = 0; ct < DSL; ++ct) {
     const int nlt = min(DGL, kb - DGL * ct);  // uniform; <= 0 past the block
     for (int lt = 0; lt < nlt; ++lt) {
-      const int t = DGL * ct + lt;
-      if (tc == lt) {
+      const int t = DGL * ct + lt;  // ci / cj hold column t of L
+      if (lt + 1 < DGL) {           // column t + 1 lives in slot column ct
 #pragma unroll
-        for (int r = ct; r < DSL; ++r) pre[DGL * r + tr] = v[r][ct];
-      }
-      const double d = pre[t];  // the same pivot in every lane: the branch below is uniform
-      if ((!(d > 0.0) || !isfinite(d)) && !failed) {
-        failed = true;
-        if (lane == 0) {
-          *status = k + t + 1;
-          *pivot = d;
+        for (int r = ct; r < DSL; ++r) v[r][ct] = v[r][ct] - ci[r] * cj[ct];
+        publish(ct, lt + 1);
+        divide(t + 1);
+#pragma unroll
+        for (int r = ct + 1; r < DSL; ++r)
+#pragma unroll
+          for (int c = ct + 1; c <= r; ++c) v[r][c] = v[r][c] - ci[r] * cj[c];
+        if (t + 1 < kb) store_col(t + 1);
+#pragma unroll
+        for (int q = ct; q < DSL; ++q) {
+          ci[q] = col[DGL * q + tr];
+          cj[q] = col[DGL * q + tc];
+        }
+      } else if (ct + 1 < DSL) {  // column t + 1 starts slot column ct + 1; slot column ct is finished
+#pragma unroll
+        for (int r = ct + 1; r < DSL; ++r) v[r][ct + 1] = v[r][ct + 1] - ci[r] * cj[ct + 1];
+        publish(ct + 1, 0);
+        divide(t + 1);
+#pragma unroll
+        for (int r = ct + 2; r < DSL; ++r)
+#pragma unroll
+          for (int c = ct + 2; c <= r; ++c) v[r][c] = v[r][c] - ci[r] * cj[c];
+        if (t + 1 < kb) store_col(t + 1);
+#pragma unroll
+        for (int q = ct + 1; q < DSL; ++q) {
+          ci[q] = col[DGL * q + tr];
+          cj[q] = col[DGL * q + tc];
         }
       }
-      const double ltt = sqrt(d);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int i = lane + 64 * h;
-        if (i < NBC) {
-          const double c = (i == t) ? ltt : ((i > t && i < kb) ? pre[i] / ltt : 0.0);
-          col[i] = c;
-          if (i >= t && i < kb) a[(long)(k + i) * n + k + t] = c;
-        }
-      }
-      double ci[DSL], cj[DSL];
-#pragma unroll
-      for (int q = ct; q < DSL; ++q) {
-        ci[q] = col[DGL * q + tr];
-        cj[q] = col[DGL * q + tc];
-      }
-#pragma unroll
-      for (int r = ct; r < DSL; ++r)
-#pragma unroll
-        for (int c = ct; c <= r; ++c) v[r][c] = v[r][c] - ci[r] * cj[c];
     }
+  }
+  if (lane == 0 && fail_t >= 0) {
+    *status = k + fail_t + 1;
+    *pivot = fail_d;
   }
 }
 
