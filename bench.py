@@ -15,6 +15,7 @@ timed on a bounded sample of the same workload on this host and extrapolated (se
 from __future__ import annotations
 
 import argparse
+import concurrent.futures
 import json
 import os
 import sys
@@ -487,6 +488,9 @@ def main():
                     help="with --workload container: counter-collection run (1 GiB copy + one step)")
     ap.add_argument("--cpu-validate", action="store_true",
                     help="time the CPU baseline's rows x n^2 model against a down_proj-width sample and exit")
+    ap.add_argument("--serial", action="store_true",
+                    help="quantize the layer's matrices one after another on one context (default: the chains "
+                         "of matrices that share an input run concurrently, one context each)")
     ap.add_argument("--floor-rows", type=int, default=0,
                     help="latency-floor run (under a kernel trace): the config's matrices cut to their first "
                          "FLOOR_ROWS rows, same inputs and settings, one untimed step; prints the phase times")
@@ -504,7 +508,7 @@ def main():
         # the same matrices with fewer rows in flight: each sweep launch then runs its rows'
         # dependent chains with no other waves on their SIMDs
         spec = dict(spec, layers=[(name, min(d_out, args.floor_rows), key) for name, d_out, key in spec["layers"]])
-        args.steps, args.warmup, args.no_cpu_baseline = 1, 0, True
+        args.steps, args.warmup, args.no_cpu_baseline, args.serial = 1, 0, True, True
     if args.cpu_validate:
         cpu_validate(spec, min(os.cpu_count() or 1, 16))
         return
@@ -538,6 +542,17 @@ def main():
         outs[name] = (cdclq.DeviceArray(ctx, (d_out, n), np.uint8), cdclq.DeviceArray(ctx, (d_out, ng), np.float32),
                       cdclq.DeviceArray(ctx, (d_out, ng), np.float32))
 
+    # The layer's matrices in chains by input: the matrices of one input share its factorisation
+    # (one context's factor cache, in the reference's order); different inputs are independent, so
+    # after the accumulations their chains run concurrently on their own contexts. Each call is the
+    # same synchronous quantize_layer as in the serial order, with the same results.
+    chains = {}
+    for name, d_out, key in spec["layers"]:
+        chains.setdefault(key, []).append((name, d_out, key))
+    chain_ctx = {k: (ctx if args.serial else cdclq.Context(0)) for k in chains}
+    pool = None if args.serial else concurrent.futures.ThreadPoolExecutor(max_workers=len(chains))
+    all_ctx = [ctx] + ([] if args.serial else list(chain_ctx.values()))
+
     def step():
         stats = {}
         for _, _, h in jobs:
@@ -550,28 +565,46 @@ def main():
             ctx.check(cdclq.lib().cdclq_f64_to_f32_device(ctx.ptr, h64s[key].ptr, n * n, h32s[key].ptr))
             if xts:
                 ctx.check(cdclq.lib().cdclq_f64_to_f32_device(ctx.ptr, m64s[key].ptr, n * n, m32s[key].ptr))
-        for name, d_out, key in spec["layers"]:
-            n = spec["inputs"][key]
-            c, s, z = outs[name]
-            _, _, st = cdclq.quantize_layer_device(ctx, ws[name], d_out, n, h32s[key], m32s.get(key), key, cfg, c, s,
-                                                   z, nthreads=spec["nthreads"])
-            stats[name] = st
+        def run_chain(cctx, names):
+            out = {}
+            for name, d_out, key in names:
+                n = spec["inputs"][key]
+                c, s, z = outs[name]
+                _, _, st = cdclq.quantize_layer_device(cctx, ws[name], d_out, n, h32s[key], m32s.get(key), key, cfg,
+                                                       c, s, z, nthreads=spec["nthreads"])
+                out[name] = st
+            return out
+
+        # this step's H are new: no factorisation carries over from the previous step
+        for c in set(chain_ctx.values()):
+            c.clear_cache()
+        if args.serial:
+            stats.update(run_chain(ctx, spec["layers"]))
+        else:  # the chains run at once, each on its own context (stream, workspace, factor cache)
+            for fut in [pool.submit(run_chain, chain_ctx[k], chains[k]) for k in chains]:
+                stats.update(fut.result())
         return stats
 
     for i in range(args.warmup):
         t0 = time.perf_counter()
         step()
         log(f"[bench] warmup {i} {time.perf_counter() - t0:.3f}s")
-    ctx.set_timing(True)
-    ctx.reset_timing()
+    for c in all_ctx:
+        c.set_timing(True)
+        c.reset_timing()
     times = []
     for i in range(args.steps):
         t0 = time.perf_counter()
         stats = step()
         times.append(time.perf_counter() - t0)
         log(f"[bench] step {i} {times[-1]:.3f}s")
-    ph = ctx.timing()
-    ctx.set_timing(False)
+    ph = {}
+    for c in all_ctx:  # device time per phase, summed over the contexts (concurrent chains overlap)
+        for k, v in c.timing().items():
+            e = ph.setdefault(k, {"ms": 0.0, "launches": 0})
+            e["ms"] += v["ms"]
+            e["launches"] += v["launches"]
+        c.set_timing(False)
     ms_per_step = 1000.0 * sum(times) / len(times)
     for name, st in stats.items():
         log(f"[bench] {name}: loss_gptq {st.loss_gptq:.6e} loss_final {st.loss_final:.6e} "
@@ -585,6 +618,10 @@ def main():
     achieved = flops / (gram_ms * 1e-3) / 1e12 if gram_ms > 0 else 0.0
     phases = {k: round(v["ms"] / args.steps, 3) for k, v in ph.items()}
     log(f"[bench] device ms per step by phase: {phases}")
+    if pool is not None:
+        pool.shutdown()
+        for c in chain_ctx.values():
+            c.close()
     if args.floor_rows > 0:
         print(json.dumps({"profile": "floor-rows", "workload": spec["workload"], "rows": args.floor_rows,
                           "layers": {name: [d_out, spec["inputs"][key]] for name, d_out, key in spec["layers"]},
@@ -607,7 +644,9 @@ def main():
         "data": DATA_DESC[(spec.get("xgen") or {"kind": "outlier"})["kind"]],
         "config": {"workload": spec["workload"], "tokens": T,
                    "layers": {name: [d_out, spec["inputs"][key]] for name, d_out, key in spec["layers"]},
-                   "quant": {**spec["cfg"], "passes": cfg.passes, "tol": cfg.tol}, "parallelism": "1 GPU"},
+                   "quant": {**spec["cfg"], "passes": cfg.passes, "tol": cfg.tol}, "parallelism": "1 GPU",
+                   "schedule": "matrices one after another" if args.serial else
+                   "one chain of matrices per input, chains concurrent (one context and stream each)"},
         "phases_ms_per_step": phases,
         "roofline": {
             "bound": "mfma",
