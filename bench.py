@@ -142,14 +142,14 @@ def make_inputs(ctx, spec: dict, only=None):
 
 
 def gram_jobs(spec: dict, xs: dict, xts: dict, h64s: dict, m64s: dict):
-    """The layer's accumulations as (x, y, h) device triples: H = X^T X per input, or, with the
+    """The layer's accumulations as (x, y, h, input key): H = X^T X per input, or, with the
     asymmetric target, H~ = X~^T X~ and M = X^T X~."""
     jobs = []
     for key in xs:
         if xts:
-            jobs += [(xts[key], xts[key], h64s[key]), (xs[key], xts[key], m64s[key])]
+            jobs += [(xts[key], xts[key], h64s[key], key), (xs[key], xts[key], m64s[key], key)]
         else:
-            jobs.append((xs[key], xs[key], h64s[key]))
+            jobs.append((xs[key], xs[key], h64s[key], key))
     return jobs
 
 
@@ -307,7 +307,7 @@ def profile_gram(ctx, spec, jobs):
     rc = hip.hipMemcpy(dst.ptr, src.ptr, nbytes, 3)  # hipMemcpyDeviceToDevice: one copy kernel
     if rc != 0 or hip.hipDeviceSynchronize() != 0:
         raise RuntimeError(f"calibration copy failed ({rc})")
-    for _, _, h in jobs:
+    for _, _, h, _ in jobs:
         h.zero()
     T = spec["tokens"]
     cdclq.gram_accumulate_batch_device(ctx, [j[0] for j in jobs], [j[1] for j in jobs], [T] * len(jobs),
@@ -553,18 +553,23 @@ def main():
     pool = None if args.serial else concurrent.futures.ThreadPoolExecutor(max_workers=len(chains))
     all_ctx = [ctx] + ([] if args.serial else list(chain_ctx.values()))
 
-    def step():
-        stats = {}
-        for _, _, h in jobs:
-            h.zero()
-        # the layer's Hessians (and cross-covariances) accumulate in one launch; each equals its own
-        # gram_accumulate
-        cdclq.gram_accumulate_batch_device(ctx, [j[0] for j in jobs], [j[1] for j in jobs], [T] * len(jobs),
-                                           [j[0].shape[1] for j in jobs], [j[2] for j in jobs])
-        for key, n in spec["inputs"].items():
+    def gram(keys):
+        """The accumulations of the inputs `keys` in one launch (each equals its own gram_accumulate),
+        then their f32 copies."""
+        js = [j for j in jobs if j[3] in keys]
+        cdclq.gram_accumulate_batch_device(ctx, [j[0] for j in js], [j[1] for j in js], [T] * len(js),
+                                           [j[0].shape[1] for j in js], [j[2] for j in js])
+        for key in keys:
+            n = spec["inputs"][key]
             ctx.check(cdclq.lib().cdclq_f64_to_f32_device(ctx.ptr, h64s[key].ptr, n * n, h32s[key].ptr))
             if xts:
                 ctx.check(cdclq.lib().cdclq_f64_to_f32_device(ctx.ptr, m64s[key].ptr, n * n, m32s[key].ptr))
+
+    def step():
+        stats = {}
+        for _, _, h, _ in jobs:
+            h.zero()
+
         def run_chain(cctx, names):
             out = {}
             for name, d_out, key in names:
@@ -578,9 +583,11 @@ def main():
         # this step's H are new: no factorisation carries over from the previous step
         for c in set(chain_ctx.values()):
             c.clear_cache()
-        if args.serial:
+        if args.serial:  # all accumulations in one launch, then the matrices one after another
+            gram(list(spec["inputs"]))
             stats.update(run_chain(ctx, spec["layers"]))
-        else:  # the chains run at once, each on its own context (stream, workspace, factor cache)
+        else:  # one launch, then the chains at once, each on its own context (stream, workspace, cache)
+            gram(list(spec["inputs"]))
             for fut in [pool.submit(run_chain, chain_ctx[k], chains[k]) for k in chains]:
                 stats.update(fut.result())
         return stats
@@ -650,8 +657,8 @@ def main():
         "phases_ms_per_step": phases,
         "roofline": {
             "bound": "mfma",
-            "kernel": f"k_gram_dma (the step's {len(jobs)} accumulations H += X^T Y in one launch, K=1 f32 MFMA "
-                      "chains, f64 chunks)",
+            "kernel": f"k_gram_dma (the step's {len(jobs)} accumulations H += X^T Y in "
+                      f"{gram_launches // max(args.steps, 1)} launch(es), K=1 f32 MFMA chains, f64 chunks)",
             "achieved": round(achieved, 2),
             "peak": FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",

@@ -50,7 +50,7 @@ def device_hessians(ctx, spec, only=None):
     h64s = {k: cdclq.DeviceArray(ctx, (n, n), np.float64) for k, n in keys.items()}
     m64s = {k: cdclq.DeviceArray(ctx, (n, n), np.float64) for k, n in keys.items()} if xts else {}
     jobs = bench.gram_jobs(spec, xs, xts, h64s, m64s)
-    for _, _, h in jobs:
+    for _, _, h, _ in jobs:
         h.zero()
     cdclq.gram_accumulate_batch_device(ctx, [j[0] for j in jobs], [j[1] for j in jobs], [T] * len(jobs),
                                        [j[0].shape[1] for j in jobs], [j[2] for j in jobs])
