@@ -110,6 +110,7 @@ def lib() -> C.CDLL:
         "cdclq_ctx_clear_cache": ([vp], i32),
         "cdclq_quantize_layer": ([vp, vp, sz, sz, vp, vp, C.c_char_p, cfgp, sz, vp, vp, vp, vp, vp, stp], i32),
         "cdclq_quantize_layer_device": ([vp, vp, sz, sz, vp, vp, C.c_char_p, cfgp, sz, vp, vp, vp, vp, vp, stp], i32),
+        "cdclq_prepare_layer_device": ([vp, vp, sz, sz, vp, C.c_char_p, cfgp], i32),
         "cdclq_gram_accumulate": ([vp, vp, vp, sz, sz, vp], i32),
         "cdclq_gram_accumulate_device": ([vp, vp, vp, sz, sz, vp], i32),
         "cdclq_gram_accumulate_device_noalloc": ([vp, vp, vp, sz, sz, vp], i32),
@@ -173,7 +174,7 @@ def exported_symbols() -> list[str]:
     return [
         "cdclq_abi_version", "cdclq_sizeof_config", "cdclq_sizeof_stats", "cdclq_default_config",
         "cdclq_num_groups", "cdclq_ctx_create", "cdclq_ctx_destroy", "cdclq_last_error", "cdclq_ctx_clear_cache",
-        "cdclq_quantize_layer", "cdclq_quantize_layer_device", "cdclq_gram_accumulate",
+        "cdclq_quantize_layer", "cdclq_quantize_layer_device", "cdclq_prepare_layer_device", "cdclq_gram_accumulate",
         "cdclq_gram_accumulate_device", "cdclq_gram_accumulate_device_noalloc", "cdclq_gram_accumulate_batch_device",
         "cdclq_sgemm_device", "cdclq_dgemm_device", "cdclq_ctx_last_midpoint_counts", "cdclq_upper_chol_of_inverse", "cdclq_upper_chol_of_inverse_device",
         "cdclq_proxy_loss", "cdclq_device_alloc", "cdclq_device_free", "cdclq_memcpy_h2d", "cdclq_memcpy_d2h",
@@ -456,6 +457,13 @@ def quantize_layer_device(ctx: Context, w: DeviceArray, d_out: int, d_in: int, h
                                                 hkey.encode(), C.byref(c), nthreads, codes.ptr, scales.ptr,
                                                 zeros.ptr, perm.ctypes.data, gbits.ctypes.data, C.byref(st)))
     return perm, gbits, LayerStats(**{f: getattr(st, f) for f, _ in _Stats._fields_})
+
+
+def prepare_layer_device(ctx: Context, w: DeviceArray, d_out: int, d_in: int, h: DeviceArray, hkey: str,
+                         cfg: Config):
+    """The factor cache fill of quantize_layer on its own (src/engine.rs:708-723): a following
+    quantize_layer_device on ctx with the same hkey, h and cfg reuses it."""
+    ctx.check(lib().cdclq_prepare_layer_device(ctx.ptr, w.ptr, d_out, d_in, h.ptr, hkey.encode(), C.byref(cfg._c())))
 
 
 def gram_accumulate(x, y, t: int, n: int, h: np.ndarray, ctx: Context) -> np.ndarray:

@@ -200,26 +200,13 @@ int grad_gemm(cdclq_ctx* ctx, int rows, int n, int c0, int wd, const float* e, c
   return err == hipSuccess ? CDCLQ_OK : fail(ctx, CDCLQ_DEVICE, std::string("gradient GEMM: ") + hipGetErrorString(err));
 }
 
-int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, const float* h, const float* m,
-                    const char* hkey, const cdclq_config* cfg, size_t nthreads, uint8_t* codes, float* scales,
-                    float* zeros, uint32_t* perm_out, uint8_t* gbits_out, cdclq_layer_stats* stats) {
-  if (!cfg) return fail(ctx, CDCLQ_INVALID_ARG, "cfg is null");
-  if (!w || !h || !codes || !scales || !zeros || !perm_out || !gbits_out)
-    return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
-  if (d_out_ == 0 || n_ == 0) return fail(ctx, CDCLQ_INVALID_ARG, "empty layer (d_out and d_in must be > 0)");
-  if (n_ > 65535 || d_out_ > (size_t)1 << 20 || d_out_ * n_ > ((size_t)1 << 31) - 1)
-    return fail(ctx, CDCLQ_INVALID_ARG, "layer too large for this build (d_in <= 65535, d_out*d_in < 2^31)");
-  CK(validate(ctx, cfg, n_));
-  ctx->mid_last = cdclq_midpoint_counts{};
-  const int d_out = (int)d_out_, n = (int)n_;
-  const int g = (int)effective_group(cfg, n_);
-  const int ng = (n + g - 1) / g;
-  const int bsz = (int)std::min<uint64_t>(cfg->block, (uint64_t)n);
-  const int sbw = (int)std::min<uint64_t>(cfg->sub_block, (uint64_t)n);
+// Dead columns, column order and the factor cache entry (U, damped permuted h32) for (hkey, perm):
+// src/engine.rs:708-723 with build_prepared (:320-342). A cache entry that matches is reused.
+static int prepare(cdclq_ctx* ctx, const float* w, int d_out, int n, const float* h, const char* hkey,
+                   const cdclq_config* cfg, int g, std::vector<uint32_t>& perm, std::vector<uint8_t>& dead,
+                   size_t& nskel) {
   hipStream_t st = ctx->st;
-  HIPCK(hipSetDevice(ctx->device));
-  const double t0 = now_secs();
-
+  const size_t n_ = (size_t)n;
   // ---- dead columns and column order (src/engine.rs:708-717, :271-304)
   CK(ensure(ctx, ctx->diag_d, (size_t)n * 4));
   HIPCK(diag_extract(st, n, h, P<float>(ctx->diag_d)));
@@ -227,13 +214,13 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
   HIPCK(hipMemcpyAsync(hd32.data(), ctx->diag_d.p, (size_t)n * 4, hipMemcpyDeviceToHost, st));
   HIPCK(hipStreamSynchronize(st));
   std::vector<double> hdiag(n);
-  std::vector<uint8_t> dead(n);
+  dead.assign(n, 0);
   for (int j = 0; j < n; ++j) {
     hdiag[j] = (double)hd32[j];
     dead[j] = hdiag[j] == 0.0;
   }
-  size_t nskel = 0;
-  std::vector<uint32_t> perm;
+  nskel = 0;
+  perm.clear();
   perm.reserve(n);
   std::vector<uint8_t> in_skel(n, 0);
   if (cfg->skeleton_pct > 0.0 && g < n) {
@@ -300,6 +287,33 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
     ctx->cache_n = n_;
     ctx->cache_damp = damp_val;
   }
+  return CDCLQ_OK;
+}
+
+int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, const float* h, const float* m,
+                    const char* hkey, const cdclq_config* cfg, size_t nthreads, uint8_t* codes, float* scales,
+                    float* zeros, uint32_t* perm_out, uint8_t* gbits_out, cdclq_layer_stats* stats) {
+  if (!cfg) return fail(ctx, CDCLQ_INVALID_ARG, "cfg is null");
+  if (!w || !h || !codes || !scales || !zeros || !perm_out || !gbits_out)
+    return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+  if (d_out_ == 0 || n_ == 0) return fail(ctx, CDCLQ_INVALID_ARG, "empty layer (d_out and d_in must be > 0)");
+  if (n_ > 65535 || d_out_ > (size_t)1 << 20 || d_out_ * n_ > ((size_t)1 << 31) - 1)
+    return fail(ctx, CDCLQ_INVALID_ARG, "layer too large for this build (d_in <= 65535, d_out*d_in < 2^31)");
+  CK(validate(ctx, cfg, n_));
+  ctx->mid_last = cdclq_midpoint_counts{};
+  const int d_out = (int)d_out_, n = (int)n_;
+  const int g = (int)effective_group(cfg, n_);
+  const int ng = (n + g - 1) / g;
+  const int bsz = (int)std::min<uint64_t>(cfg->block, (uint64_t)n);
+  const int sbw = (int)std::min<uint64_t>(cfg->sub_block, (uint64_t)n);
+  hipStream_t st = ctx->st;
+  HIPCK(hipSetDevice(ctx->device));
+  const double t0 = now_secs();
+
+  std::vector<uint32_t> perm;
+  std::vector<uint8_t> dead;
+  size_t nskel = 0;
+  CK(prepare(ctx, w, d_out, n, h, hkey, cfg, g, perm, dead, nskel));
   const float* U = P<float>(ctx->cache_u);
   const float* H32 = P<float>(ctx->cache_h32);
 
@@ -880,6 +894,25 @@ int cdclq_quantize_layer_device(cdclq_ctx* ctx, const float* w, size_t d_out, si
   if (!ctx) return CDCLQ_INVALID_ARG;
   ctx->err.clear();
   return quantize_device(ctx, w, d_out, d_in, h, m, hkey, cfg, nthreads, codes, scales, zeros, perm, gbits, stats);
+}
+
+int cdclq_prepare_layer_device(cdclq_ctx* ctx, const float* w, size_t d_out, size_t d_in, const float* h,
+                               const char* hkey, const cdclq_config* cfg) {
+  if (!ctx) return CDCLQ_INVALID_ARG;
+  ctx->err.clear();
+  if (!cfg) return fail(ctx, CDCLQ_INVALID_ARG, "cfg is null");
+  if (!w || !h) return fail(ctx, CDCLQ_INVALID_ARG, "null buffer argument");
+  if (d_out == 0 || d_in == 0) return fail(ctx, CDCLQ_INVALID_ARG, "empty layer (d_out and d_in must be > 0)");
+  if (d_in > 65535 || d_out > (size_t)1 << 20 || d_out * d_in > ((size_t)1 << 31) - 1)
+    return fail(ctx, CDCLQ_INVALID_ARG, "layer too large for this build (d_in <= 65535, d_out*d_in < 2^31)");
+  CK(validate(ctx, cfg, d_in));
+  HIPCK(hipSetDevice(ctx->device));
+  std::vector<uint32_t> perm;
+  std::vector<uint8_t> dead;
+  size_t nskel = 0;
+  CK(prepare(ctx, w, (int)d_out, (int)d_in, h, hkey, cfg, (int)effective_group(cfg, d_in), perm, dead, nskel));
+  HIPCK(hipStreamSynchronize(ctx->st));
+  return CDCLQ_OK;
 }
 
 int cdclq_quantize_layer(cdclq_ctx* ctx, const float* w, size_t d_out, size_t d_in, const float* h, const float* m,

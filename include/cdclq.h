@@ -116,6 +116,16 @@ int cdclq_quantize_layer_device(cdclq_ctx* ctx, const float* w, size_t d_out, si
                                 uint8_t* codes, float* scales, float* zeros, uint32_t* perm, uint8_t* gbits,
                                 cdclq_layer_stats* stats);
 
+/* The factor cache fill that cdclq_quantize_layer[_device] performs first (src/engine.rs:708-723,
+ * build_prepared :320-342), on its own: the column order for (w, h, cfg) and, unless ctx's cache
+ * already holds it, U and the damped permuted H for (hkey, that order). A following
+ * cdclq_quantize_layer[_device] on ctx with the same hkey, h and cfg (and, with the skeleton, the
+ * same w) reuses the entry, exactly as a second reference call through the same PrepCache does.
+ * No reference counterpart: it lets a caller run the factorisations of several contexts ahead of
+ * their other work. w, h: device pointers. Synchronous. */
+int cdclq_prepare_layer_device(cdclq_ctx* ctx, const float* w, size_t d_out, size_t d_in, const float* h,
+                               const char* hkey, const cdclq_config* cfg);
+
 /* Near-midpoint accounting of the last cdclq_quantize_layer[_device] call on ctx (no reference
  * counterpart: the parity contract's record of rounding decisions an implementation with another
  * operation order could legitimately resolve differently). A decision clamp(round(a / b) + z, 0,

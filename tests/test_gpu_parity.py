@@ -476,6 +476,40 @@ def test_device_entry_point_matches_host(ctx):
     assert sd.loss_final == sh.loss_final
 
 
+def test_prepare_entry_point_fills_the_cache(ctx):
+    """cdclq_prepare_layer_device runs the factorisation that the next quantize_layer_device call on
+    the same context (same hkey, H and cfg) reuses: one factorisation for the pair, and results
+    bit-identical to the quantize call on an empty cache."""
+    w, x, h, _ = synth_layer(71, 48, 128, 500)
+    gcfg, _ = cfgs(bits=3, group=32, block=64, act_order=True, row_chunk=16, passes=2)
+    dw, dh = cdclq.DeviceArray.from_host(ctx, w), cdclq.DeviceArray.from_host(ctx, h)
+
+    def run():
+        dc = cdclq.DeviceArray(ctx, (48, 128), np.uint8)
+        ds = cdclq.DeviceArray(ctx, (48, 4), np.float32)
+        dz = cdclq.DeviceArray(ctx, (48, 4), np.float32)
+        perm, gbits, st = cdclq.quantize_layer_device(ctx, dw, 48, 128, dh, None, "pk", gcfg, dc, ds, dz)
+        return perm, gbits, dc.download(), ds.download(), dz.download(), st
+
+    ctx.clear_cache()
+    ref = run()
+    ctx.clear_cache()
+    ctx.set_timing(True)
+    ctx.reset_timing()
+    try:
+        cdclq.prepare_layer_device(ctx, dw, 48, 128, dh, "pk", gcfg)
+        prepared = ctx.timing()["factor"]["launches"]
+        got = run()
+        total = ctx.timing()["factor"]["launches"]
+    finally:
+        ctx.set_timing(False)
+        ctx.clear_cache()
+    assert prepared == 1 and total == 1, (prepared, total)
+    for a, b in zip(ref[:5], got[:5]):
+        assert np.array_equal(a, b)
+    assert got[5].loss_gptq == ref[5].loss_gptq and got[5].loss_final == ref[5].loss_final
+
+
 def test_proxy_loss(ctx):
     w, x, h, _ = synth_layer(80, 40, 96, 400)
     gcfg, ocfg = cfgs(bits=3, group=32, block=32, act_order=False, row_chunk=8)
