@@ -855,6 +855,7 @@ void cdclq_ctx_destroy(cdclq_ctx* ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->st);
+  (void)hipStreamSynchronize(ctx->st2);
   drain_timing(ctx);
   DevBuf* bufs[] = {&ctx->w_in, &ctx->h_in, &ctx->m_in, &ctx->x_in, &ctx->y_in, &ctx->h64_in, &ctx->u_out,
                     &ctx->codes_o, &ctx->scales_o, &ctx->zeros_o, &ctx->wp, &ctx->wwork, &ctx->wq, &ctx->ebuf,
@@ -869,7 +870,6 @@ void cdclq_ctx_destroy(cdclq_ctx* ctx) {
   for (DevBuf& b : ctx->pk_tab) free_buf(b);
   for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
   if (ctx->pin) (void)hipHostFree(ctx->pin);
-  (void)hipStreamSynchronize(ctx->st2);
   (void)hipEventDestroy(ctx->ev_col);
   (void)hipEventDestroy(ctx->ev_panel);
   (void)hipStreamDestroy(ctx->st2);
