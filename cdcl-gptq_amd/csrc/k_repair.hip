@@ -953,15 +953,15 @@ __device__ __forceinline__ void fold_chains(const float* __restrict__ src, long 
 }
 
 template <int NPL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NPL == 1 ? 8 : 1))) void k_cd(int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc,
-                                            int sweeps, const float* __restrict__ G, const float* __restrict__ h32,
-                                            const uint8_t* __restrict__ gbits, const float* __restrict__ scales,
-                                            const float* __restrict__ zeros, uint8_t* __restrict__ codes,
-                                            float* __restrict__ wq, float* __restrict__ e,
-                                            const uint8_t* __restrict__ active, const uint8_t* __restrict__ sel,
-                                            double* __restrict__ dlog, uint32_t* __restrict__ dcnt, int cap,
-                                            unsigned long long* __restrict__ mid, uint32_t* __restrict__ evals,
-                                            const float* __restrict__ P, int np) {
+// The 64-column form asks for 8 wavefronts per SIMD: the unrolled panel addresses of its fold would
+// otherwise take enough scalar registers to cap it at 7.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NPL == 1 ? 8 : 1))) void k_cd(
+    int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc, int sweeps, const float* __restrict__ G,
+    const float* __restrict__ h32, const uint8_t* __restrict__ gbits, const float* __restrict__ scales,
+    const float* __restrict__ zeros, uint8_t* __restrict__ codes, float* __restrict__ wq, float* __restrict__ e,
+    const uint8_t* __restrict__ active, const uint8_t* __restrict__ sel, double* __restrict__ dlog,
+    uint32_t* __restrict__ dcnt, int cap, unsigned long long* __restrict__ mid, uint32_t* __restrict__ evals,
+    const float* __restrict__ P, int np) {
   // Sub-blocks of up to 64 columns keep H_CC (the sub-block's rows and columns of h32, 16 KB) in
   // LDS, shared by the workgroup's rows: the gradient update after a move reads its row from there.
   constexpr int HW = NPL * 64;
