@@ -377,7 +377,11 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
                                                    const float* __restrict__ B, long ldb, float* __restrict__ C,
                                                    long ldc, float alpha, int nunits, float* __restrict__ P,
                                                    const int* __restrict__ rtiles, int kfold) {
-  __shared__ float R[DNB][LSTAGE];
+  // With C a ring of two stages (64 KB), so that a block sweep's workgroup (64 KB) and a narrow
+  // update's (72 KB) fit beside this one on each CU: this kernel runs on a side stream while the
+  // main stream sweeps the next blocks. Without C the ring of three.
+  constexpr int NB = DIRECT ? 2 : DNB;
+  __shared__ float R[NB][LSTAGE];
   const int nct = (wd + LPC - 1) / LPC;
   const int np = k / CDCLQ_KC + (k % CDCLQ_KC != 0);
   const int u0 = (int)((long)blockIdx.x * nunits / gridDim.x);
@@ -426,7 +430,7 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
   unit_offsets();
   auto issue_next = [&]() {
     if (!ivalid) return;
-    const uint32_t buf = lds0 + (uint32_t)((fi % DNB) * LSTAGE * 4);
+    const uint32_t buf = lds0 + (uint32_t)((fi % NB) * LSTAGE * 4);
     const int ks = iu.k0 + is * DSK;
     const float* ea = A + (long)iu.r0 * lda + ks;
     const float* hb = B + (long)ks * ldb;
@@ -447,10 +451,12 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
     }
   };
   issue_next();
-  issue_next();
+  if (NB == 3) issue_next();
   const int er = 32 * wr + (lane & 31);
-  // Ordering as in k_panel_dma: with C the unit's stores precede the deferred load of its last
-  // stage; without C the chains are stored (nontemporal) at the next unit's first stage.
+  // Without C, ordering as in k_panel_dma: the chains are stored (nontemporal) at the next unit's
+  // first stage. With C (ring of two) each stage waits for everything issued before it -- its own
+  // loads, issued one stage ahead, the unit's C loads and the previous unit's C stores -- and the
+  // next stage's loads are issued after the barrier that retires the reads of its slot.
   int fc = 0;
   v32f acc = {};
   Unit pu = iu;
@@ -466,7 +472,7 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
     const Unit cu = unit(cu_idx);
     float cv[32];
     for (int cs = 0; cs < cu.nst; ++cs) {
-      if (fi - fc >= 2)
+      if (!DIRECT && fi - fc >= 2)
         wait_vmcnt<LDPW>();
       else
         wait_vmcnt<0>();
@@ -475,7 +481,7 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
         store_p(pu);
         acc = v32f{};
       }
-      if (DIRECT && cs == 0) {  // before the stage after next, as in k_panel_dma
+      if (DIRECT && cs == 0) {
 #pragma unroll
         for (int r = 0; r < 32; ++r) {
           const int row = min(cu.r0 + 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), m - 1);
@@ -483,8 +489,8 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
           cv[r] = C[(long)row * ldc + col];
         }
       }
-      if (!DIRECT || cs + 1 < cu.nst) issue_next();
-      const float* buf = &R[fc % DNB][0];
+      issue_next();
+      const float* buf = &R[fc % NB][0];
       const float* es = buf + 32 * er;
       const float* hs = buf + DSK * PR + 64 * wc + lane;
 #pragma unroll
@@ -510,7 +516,6 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
         if (row < m && col < wd) C[(long)row * ldc + col] = __builtin_fmaf(alpha, acc[r], cv[r]);
       }
       acc = v32f{};
-      issue_next();
     } else {
       pu = cu;
     }
@@ -1228,8 +1233,8 @@ static hipError_t dma_slots(int* out) {
   return hipSuccess;
 }
 
-// resident k_lazy_wide workgroups on the whole device (both forms use the same resources; cached
-// per process)
+// resident k_lazy_wide<DIRECT> workgroups on the whole device (cached per process)
+template <bool DIRECT>
 static hipError_t wide_slots(int* out) {
   static std::atomic<int> cached{0};
   int v = cached.load(std::memory_order_relaxed);
@@ -1237,7 +1242,7 @@ static hipError_t wide_slots(int* out) {
     int dev = 0, cus = 0, per = 0;
     hipError_t err = hipGetDevice(&dev);
     if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (err == hipSuccess) err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_lazy_wide<true>, 512, 0);
+    if (err == hipSuccess) err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_lazy_wide<DIRECT>, 512, 0);
     if (err != hipSuccess) return err;
     v = std::max(1, cus * std::max(1, per));
     cached.store(v, std::memory_order_relaxed);
@@ -1274,7 +1279,7 @@ hipError_t panel_gemm(hipStream_t st, int m, int wd, int k, const float* A, long
   if (dma) {
     if (wd == LPC) {  // 128-column gradients of tall enough matrices: one E tile read per unit
       int ws = 0;
-      const hipError_t e2 = wide_slots(&ws);
+      const hipError_t e2 = wide_slots<false>(&ws);
       if (e2 != hipSuccess) return e2;
       const long wunits = (long)ntiles * ((k + CDCLQ_KC - 1) / CDCLQ_KC);
       if (wunits >= 4L * ws) {
@@ -1310,7 +1315,7 @@ hipError_t chain_gemm_mfma(hipStream_t st, int m, int n, int k, float alpha, int
   if (!chain_gemm_mfma_ok(m, n, k, A, lda, B, ldb, kfold)) return hipErrorInvalidValue;
   const int kf = kfold > 0 ? kfold : k;
   int ws = 0;
-  const hipError_t e2 = wide_slots(&ws);
+  const hipError_t e2 = wide_slots<true>(&ws);
   if (e2 != hipSuccess) return e2;
   const long wunits = (long)((m + PR - 1) / PR) * ((n + LPC - 1) / LPC);
   if (beta_one && wunits >= ws && wunits <= INT32_MAX) {
