@@ -364,8 +364,8 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
 
 // The lazy trailing update C = fma(alpha, A B, C) (k <= 256, one panel) on 128 x 128 tiles: 8
 // waves, wave w rows 32 (w & 3) .. +31 and columns 64 (w >> 2) .. +63, one E tile read per 128
-// columns; the stage ring, load plan and per-element chain are those of k_panel_dma<true> (B
-// stage [32 k][128 cols], 2 k rows per load). Used when there are enough 128 x 128 tiles to give
+// columns; the stages, load plan and per-element chain are those of k_panel_dma<true> (B stage
+// [32 k][128 cols], 2 k rows per load). Used when there are enough 128 x 128 tiles to give
 // every CU one. Without C (DIRECT false) the same tile computes the repair gradient's 128-column
 // per-panel chains (units (row tile, panel)), stored to P as k_panel_dma<false> stores them, when
 // there are at least four units per workgroup.
@@ -377,9 +377,9 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
                                                    const float* __restrict__ B, long ldb, float* __restrict__ C,
                                                    long ldc, float alpha, int nunits, float* __restrict__ P,
                                                    const int* __restrict__ rtiles, int kfold) {
-  // With C a ring of two stages (64 KB), so that a block sweep's workgroup (64 KB) and a narrow
-  // update's (72 KB) fit beside this one on each CU: this kernel runs on a side stream while the
-  // main stream sweeps the next blocks. Without C the ring of three.
+  // With C a ring of two stages (64 KB), so that a narrow update's workgroup (72 KB) fits beside
+  // this one on each CU: this kernel runs on a side stream while the main stream updates and
+  // sweeps the next blocks. Without C the ring of three.
   constexpr int NB = DIRECT ? 2 : DNB;
   __shared__ float R[NB][LSTAGE];
   const int nct = (wd + LPC - 1) / LPC;
