@@ -695,9 +695,12 @@ int gram_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const f
     else
       gram_mfma_tiles((int)i, jobs[i].n, sym, tiles[0]);
   }
-  // XCD-aware order: workgroup w runs on XCD w % 8, so give each XCD a contiguous run of tiles
-  // (neighbouring tiles share X stripes in that XCD's L2).
-  for (auto& tl : tiles) {
+  // XCD-aware order: workgroup w runs on XCD w % 8. The direct-to-LDS tiles go in gangs of 4 x 8
+  // neighbouring tiles, one gang per XCD at a time (the gang's 32 workgroups share 4 X and 8 Y
+  // stripes in that XCD's L2); the others in a contiguous run per XCD (sharing X stripes).
+  gram_dma_order(tiles[1]);
+  {
+    auto& tl = tiles[0];
     const size_t nx = 8, m = tl.size();
     std::vector<int4> ord(m);
     const size_t per = (m + nx - 1) / nx;
@@ -712,16 +715,19 @@ int gram_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const f
   const size_t ntile = tiles[0].size() + tiles[1].size();
   GramJob* djobs;
   int4* dtiles;
+  int* prog = nullptr;  // gang pacing words, one per tile slot (none on the allocation-free path)
   if (fixed) {
     if (ntile > kGramScratchTiles)
       return fail(ctx, CDCLQ_INVALID_ARG, "gram_accumulate: tile list exceeds the allocation-free scratch");
     djobs = reinterpret_cast<GramJob*>(fixed + 256);
     dtiles = reinterpret_cast<int4*>(fixed + 512);
   } else {
-    CK(ensure(ctx, ctx->tiles_d, ntile * sizeof(int4) + jobs.size() * sizeof(GramJob) + 64));
+    CK(ensure(ctx, ctx->tiles_d, jobs.size() * sizeof(GramJob) + 64 + ntile * (sizeof(int4) + sizeof(int))));
     char* base = P<char>(ctx->tiles_d);
     djobs = reinterpret_cast<GramJob*>(base);
     dtiles = reinterpret_cast<int4*>(base + ((jobs.size() * sizeof(GramJob) + 63) / 64) * 64);
+    prog = reinterpret_cast<int*>(dtiles + ntile);
+    HIPCK(zero_words(st, prog, (int)ntile));
   }
   HIPCK(hipMemcpyAsync(djobs, jobs.data(), jobs.size() * sizeof(GramJob), hipMemcpyHostToDevice, st));
   HIPCK(hipMemcpyAsync(dtiles, tiles[0].data(), tiles[0].size() * sizeof(int4), hipMemcpyHostToDevice, st));
@@ -730,7 +736,7 @@ int gram_batch_device(cdclq_ctx* ctx, int count, const float* const* xs, const f
   {
     PhaseScope ps(ctx, CDCLQ_PHASE_GRAM);
     HIPCK(gram_mfma(st, djobs, dtiles, (int)tiles[0].size(), vec4));
-    HIPCK(gram_dma(st, djobs, dtiles + tiles[0].size(), (int)tiles[1].size()));
+    HIPCK(gram_dma(st, djobs, dtiles + tiles[0].size(), (int)tiles[1].size(), prog));
   }
   HIPCK(hipStreamSynchronize(st));
   return CDCLQ_OK;

@@ -19,6 +19,8 @@
 // 128x128 super-tile triangle are listed and off-diagonal results are also written transposed
 // (exact: fma(a, b, c) == fma(b, a, c)); this requires the incoming H to be symmetric, which the
 // host checks.
+#include <algorithm>
+#include <climits>
 #include <mutex>
 
 #include "cdclq_dev.h"
@@ -217,16 +219,20 @@ constexpr int DKT = 64;                   // tokens per stage
 constexpr int DSTAGE = DKT * (TI + DTJ);  // floats per stage: X [64][128], Y [64][128]
 constexpr int DPW = DSTAGE / 512 / 4;     // 1 KB load instructions per wave and stage (8)
 constexpr int DLA = 2;                    // token pairs read ahead of the matrix core
+constexpr int GANG_LAG = 4;               // stages a gang member may run ahead of its slowest one
+constexpr int GANG_SPIN = 100;            // polls before a member stops pacing (≈ 0.2 ms)
 
 __global__ __launch_bounds__(512, 1) void k_gram_dma(const GramJob* __restrict__ jobs,
-                                                     const int4* __restrict__ tiles) {
+                                                     const int4* __restrict__ tiles, int* __restrict__ prog) {
   __shared__ float R[2][DSTAGE];
   const int4 tl = tiles[blockIdx.x];
+  if (tl.x < 0) return;  // an empty slot of a short gang (gram_dma_order)
   const GramJob jb = jobs[tl.x];
   const int n = jb.n, T = jb.t;
   __attribute__((address_space(1))) double* H = (__attribute__((address_space(1))) double*)jb.h;
   const int i0 = tl.y * TI, j0 = tl.z * DTJ;
-  const bool mirror = tl.w != 0;
+  const bool mirror = (tl.w & 1) != 0;
+  const int gsz = (tl.w >> 1) & 63, gpos = (tl.w >> 7) & 31, gid = tl.w >> 12;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wr = wv >> 2, wc = wv & 3;
   const int rbase = i0 + 64 * wr + 4 * (lane >> 5);
@@ -254,6 +260,15 @@ __global__ __launch_bounds__(512, 1) void k_gram_dma(const GramJob* __restrict__
     for (int q = 0; q < DPW; ++q) dma16(src[q] + t0n, buf + dst[q]);
   };
   issue(0);
+  // Gang pacing (prog != null). The 32 tiles of a gang run on one XCD at the same time and share 4
+  // X and 8 Y stripes in its L2 only while they stay within a few stages of each other. Wave 0
+  // publishes the stage its workgroup has reached in prog[32 gang + position] (INT_MAX once done)
+  // and loads the others' stages; before the next stage's barrier, if any member is more than
+  // GANG_LAG stages behind, it polls until none is, or gives up pacing after GANG_SPIN polls (a
+  // member that is not resident). Pacing only delays; the arithmetic is untouched.
+  int* const gp = (prog != nullptr && gsz > 1) ? prog + 32 * gid : nullptr;
+  bool pace = gp != nullptr && __builtin_amdgcn_readfirstlane(wv) == 0;
+  int seen = INT_MAX;  // lane < gsz: the stage member `lane` had published, loaded a stage earlier
   v32f acc = {};
   float tmp[32];
 #pragma unroll
@@ -262,6 +277,18 @@ __global__ __launch_bounds__(512, 1) void k_gram_dma(const GramJob* __restrict__
     // this wave's part of stage s has landed; the barrier publishes every wave's part and retires
     // all reads of stage s - 1, whose buffer the next stage's loads then fill
     wait_vmcnt<0>();
+    if (pace) {
+      if (__builtin_amdgcn_ballot_w64(lane < gsz && s - seen > GANG_LAG)) {
+        int polls = 0;
+        do {
+          __builtin_amdgcn_s_sleep(8);
+          if (lane < gsz) seen = __hip_atomic_load(gp + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } while (__builtin_amdgcn_ballot_w64(lane < gsz && s - seen > GANG_LAG) && ++polls < GANG_SPIN);
+        pace = polls < GANG_SPIN;
+      }
+      if (lane == 0) __hip_atomic_store(gp + gpos, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane < gsz) seen = __hip_atomic_load(gp + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     __builtin_amdgcn_s_barrier();
     if (s + 1 < nstage) issue(s + 1);
     const float* xs = &R[s & 1][64 * wr + lane];
@@ -303,6 +330,7 @@ __global__ __launch_bounds__(512, 1) void k_gram_dma(const GramJob* __restrict__
       }
     }
   }
+  if (gp != nullptr && tid == 0) __hip_atomic_store(gp + gpos, INT_MAX, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
   for (int r = 0; r < 32; ++r) {
     const int row = rbase + 32 * (r >> 4) + 8 * ((r & 15) >> 2) + (r & 3);
@@ -358,10 +386,41 @@ hipError_t gram_mfma(hipStream_t st, const GramJob* jobs, const int4* tiles, int
   return hipGetLastError();
 }
 
-hipError_t gram_dma(hipStream_t st, const GramJob* jobs, const int4* tiles, int ntiles) {
+hipError_t gram_dma(hipStream_t st, const GramJob* jobs, const int4* tiles, int ntiles, int* prog) {
   if (ntiles <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_gram_dma, dim3(ntiles), dim3(512), 0, st, jobs, tiles);
+  hipLaunchKernelGGL(k_gram_dma, dim3(ntiles), dim3(512), 0, st, jobs, tiles, prog);
   return hipGetLastError();
+}
+
+// Morton index of tile (I, J), the column bit lowest: 32 consecutive indices are a 4 x 8 block
+static uint64_t tile_morton(int I, int J) {
+  uint64_t k = 0;
+  for (int b = 0; b < 24; ++b) k |= (uint64_t)((J >> b) & 1) << (2 * b) | (uint64_t)((I >> b) & 1) << (2 * b + 1);
+  return k;
+}
+
+void gram_dma_order(std::vector<int4>& tl) {
+  // each job's tiles in Morton order, jobs one after another
+  for (size_t i = 0; i < tl.size();) {
+    size_t j = i;
+    while (j < tl.size() && tl[j].x == tl[i].x) ++j;
+    std::stable_sort(tl.begin() + i, tl.begin() + j,
+                     [](const int4& a, const int4& b) { return tile_morton(a.y, a.z) < tile_morton(b.y, b.z); });
+    i = j;
+  }
+  // gangs of 32 consecutive tiles (one may span two jobs), so the launch takes no more rounds of
+  // 256 workgroups than the tiles need; the gang fields stay 0 (no pacing) past 2^19 gangs
+  const size_t m = tl.size(), ng = (m + 31) / 32, rounds = (ng + 7) / 8;
+  const bool fields = ng < (size_t(1) << 19);
+  std::vector<int4> out(rounds * 8 * 32, make_int4(-1, 0, 0, 0));
+  for (size_t t = 0; t < m; ++t) {
+    const size_t g = t / 32, p = t % 32;
+    int4 v = tl[t];
+    const int gs = (int)std::min<size_t>(32, m - 32 * g);
+    v.w = (v.w & 1) | (fields ? (gs << 1) | ((int)p << 7) | ((int)g << 12) : 0);
+    out[(32 * (g / 8) + p) * 8 + g % 8] = v;
+  }
+  tl.swap(out);
 }
 
 void gram_dma_tiles(int job, int n, bool sym, std::vector<int4>& out) {

@@ -46,9 +46,17 @@ struct GramJob {
 // mirror flag). `sym`: Y == X and the incoming H is symmetric.
 void gram_mfma_tiles(int job, int n, bool sym, std::vector<int4>& out);
 // direct-to-LDS gram for jobs that satisfy gram_dma_eligible (all tiles interior, T % 64 == 0), on
-// 128 x 128 tiles (int4: job, row block of 128, col block of 128, mirror flag)
-hipError_t gram_dma(hipStream_t st, const GramJob* jobs, const int4* tiles, int ntiles);
+// 128 x 128 tiles (int4: job, row block of 128, col block of 128, flags: mirror in bit 0, gang
+// size in bits 1-6, position in the gang in bits 7-11, gang in bits 12-30; job -1: an empty slot).
+// prog: one zeroed int per tile slot for the gang pacing, or null (no pacing).
+hipError_t gram_dma(hipStream_t st, const GramJob* jobs, const int4* tiles, int ntiles, int* prog);
 void gram_dma_tiles(int job, int n, bool sym, std::vector<int4>& out);
+// Reorders a gram_dma_tiles list (jobs contiguous) into gangs of 32 neighbouring tiles (each job in
+// Morton order of (row block, col block): an aligned gang is a 4 x 8 block of tiles, 12 stripes of
+// X and Y instead of up to 33 for a run of one row), gang g on XCD g % 8 in round g / 8: slot
+// (32 round + position) * 8 + XCD (workgroup w runs on XCD w % 8), empty slots after the last
+// tile. Sets the gang fields of the flags.
+void gram_dma_order(std::vector<int4>& tiles);
 bool gram_dma_eligible(int n, int t, const void* x, const void* y);
 hipError_t gram_mfma(hipStream_t st, const GramJob* jobs, const int4* tiles, int ntiles, bool vec4);
 hipError_t sym_check(hipStream_t st, int n, const double* h, int* flag);
