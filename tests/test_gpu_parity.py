@@ -163,6 +163,31 @@ def test_gram_batch_matches_single_calls(ctx):
         assert np.array_equal(d.download().view(np.uint64), ho.view(np.uint64)), (t, n)
 
 
+def test_gram_batch_gangs_across_jobs(ctx):
+    """Direct-to-LDS jobs of different widths and token counts in one launch: 132 tiles in gangs of
+    32, two gangs spanning two jobs (members with different token counts pace each other until the
+    shorter ones finish), and a partial last gang. Each H bit-identical to the oracle's."""
+    rng = np.random.default_rng(11)
+    cases = []
+    for (t, n, kind) in ((2048, 1024, "sym0"), (3072, 1152, "asym"), (1024, 640, "symstart")):
+        x = (rng.standard_normal((t, n)) * rng.uniform(0.1, 5, n)).astype(np.float32)
+        y = x if kind != "asym" else (x + 0.1 * rng.standard_normal((t, n))).astype(np.float32)
+        if kind == "symstart":  # bitwise symmetric start: the mirrored path
+            a = rng.standard_normal((n, n))
+            h0 = np.triu(a) + np.triu(a, 1).T
+        else:
+            h0 = np.zeros((n, n)) if kind == "sym0" else rng.standard_normal((n, n))
+        cases.append((t, n, x, y, h0))
+    dx = [cdclq.DeviceArray.from_host(ctx, c[2]) for c in cases]
+    dy = [d if c[3] is c[2] else cdclq.DeviceArray.from_host(ctx, c[3]) for d, c in zip(dx, cases)]
+    dh = [cdclq.DeviceArray.from_host(ctx, c[4]) for c in cases]
+    print("[parity] gram gangs across jobs", [(c[0], c[1]) for c in cases], flush=True)
+    cdclq.gram_accumulate_batch_device(ctx, dx, dy, [c[0] for c in cases], [c[1] for c in cases], dh)
+    for (t, n, x, y, h0), d in zip(cases, dh):
+        ho = O.gram_accumulate(x, None if y is x else y, h0.copy())
+        assert np.array_equal(d.download().view(np.uint64), ho.view(np.uint64)), (t, n)
+
+
 # ---------------------------------------------------------------- sgemm / dgemm
 def _gemm_device(ctx, dt, m, k, n, alpha, a, sa, b, sb, beta, c0, sc):
     """Runs cdclq_{s,d}gemm_device on device copies of a, b, c0 with element strides sa, sb, sc."""
