@@ -498,7 +498,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
         print(f"bench.py: this build measures one GPU only (requested --gpus {args.gpus}, WORLD_SIZE {world}); "
-              "the multi-GPU sharding is described in DESIGN.md and not run.", flush=True)
+              "sharding the path over several GPUs is a design only, not run here.", flush=True)
         sys.exit(2)
 
     import cdclq
