@@ -8,6 +8,7 @@
  */
 #include "cdclq_oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <omp.h>
 #include <stdio.h>
@@ -228,13 +229,74 @@ static void find_params_lo(const float* vals, size_t len, uint32_t bits, int mse
  * order, acc = chain of fma(a_ik, b_kj, acc) from 0 in k order; C = fma(alpha, acc, C') where C' is
  * beta*C for the first panel (0 when beta == 0; C is not read) and C afterwards. The split of C
  * across threads (pgemm_*) never changes this per-element order. */
-#define MB 16
+#define MB 128
 #define NBF 256
 
-#define DEFINE_GEMM(NAME, T, FMA)                                                                                     \
+/* Register-blocked chains: 4 rows x 2 vectors of C, each element's chain kept in one vector lane.
+ * Every lane runs exactly the scalar sequence above (acc = fma(a_ik, b_kj, acc) from +0 in k
+ * order, then C = fma(alpha, acc, C)); only the loop nest differs, so results are identical. */
+#define DEFINE_MK(NAME, T, V, W, SET1, ZERO, LOAD, STORE, VFMA)                                                     \
+  static void NAME##_mk4(const T* ap, const T* bp, size_t kc, T alpha, T* cv) {                                   \
+    V c00 = ZERO(), c01 = ZERO(), c10 = ZERO(), c11 = ZERO();                                                        \
+    V c20 = ZERO(), c21 = ZERO(), c30 = ZERO(), c31 = ZERO();                                                        \
+    for (size_t kk = 0; kk < kc; ++kk) {                                                                            \
+      const T* bk = bp + kk * NBF;                                                                                  \
+      const T* ak = ap + kk * 4;                                                                                    \
+      const V b0 = LOAD(bk), b1 = LOAD(bk + W);                                                                     \
+      V x = SET1(ak[0]);                                                                                            \
+      c00 = VFMA(x, b0, c00);                                                                                       \
+      c01 = VFMA(x, b1, c01);                                                                                       \
+      x = SET1(ak[1]);                                                                                              \
+      c10 = VFMA(x, b0, c10);                                                                                       \
+      c11 = VFMA(x, b1, c11);                                                                                       \
+      x = SET1(ak[2]);                                                                                              \
+      c20 = VFMA(x, b0, c20);                                                                                       \
+      c21 = VFMA(x, b1, c21);                                                                                       \
+      x = SET1(ak[3]);                                                                                              \
+      c30 = VFMA(x, b0, c30);                                                                                       \
+      c31 = VFMA(x, b1, c31);                                                                                       \
+    }                                                                                                               \
+    const V al = SET1(alpha);                                                                                       \
+    STORE(cv, VFMA(al, c00, LOAD(cv)));                                                                             \
+    STORE(cv + W, VFMA(al, c01, LOAD(cv + W)));                                                                     \
+    STORE(cv + NBF, VFMA(al, c10, LOAD(cv + NBF)));                                                                 \
+    STORE(cv + NBF + W, VFMA(al, c11, LOAD(cv + NBF + W)));                                                         \
+    STORE(cv + 2 * NBF, VFMA(al, c20, LOAD(cv + 2 * NBF)));                                                         \
+    STORE(cv + 2 * NBF + W, VFMA(al, c21, LOAD(cv + 2 * NBF + W)));                                                 \
+    STORE(cv + 3 * NBF, VFMA(al, c30, LOAD(cv + 3 * NBF)));                                                         \
+    STORE(cv + 3 * NBF + W, VFMA(al, c31, LOAD(cv + 3 * NBF + W)));                                                 \
+  }
+
+DEFINE_MK(sg, float, __m256, 8, _mm256_set1_ps, _mm256_setzero_ps, _mm256_loadu_ps, _mm256_storeu_ps, _mm256_fmadd_ps)
+DEFINE_MK(dg, double, __m256d, 4, _mm256_set1_pd, _mm256_setzero_pd, _mm256_loadu_pd, _mm256_storeu_pd,
+          _mm256_fmadd_pd)
+
+#define DEFINE_GEMM(NAME, T, FMA, W)                                                                                  \
+  /* scalar chains of row i (tile-relative) over columns [j0c, j1c) */                                              \
+  static void NAME##_rows1(const T* arow, ptrdiff_t csa, const T* bp, size_t kc, size_t j0c, size_t j1c, T alpha,    \
+                           T* cr, T* acc) {                                                                         \
+    for (size_t j = j0c; j < j1c; ++j) acc[j] = (T)0;                                                               \
+    if (g_mut == 11) { /* planted mutation 11: every product rounded before it is added */                         \
+      for (size_t kk = 0; kk < kc; ++kk) {                                                                          \
+        const T av = arow[(ptrdiff_t)kk * csa];                                                                     \
+        const T* bk = bp + kk * NBF;                                                                                \
+        for (size_t j = j0c; j < j1c; ++j) {                                                                        \
+          const T p = av * bk[j];                                                                                   \
+          acc[j] = acc[j] + p;                                                                                      \
+        }                                                                                                           \
+      }                                                                                                             \
+    } else {                                                                                                        \
+      for (size_t kk = 0; kk < kc; ++kk) {                                                                          \
+        const T av = arow[(ptrdiff_t)kk * csa];                                                                     \
+        const T* bk = bp + kk * NBF;                                                                                \
+        for (size_t j = j0c; j < j1c; ++j) acc[j] = FMA(av, bk[j], acc[j]);                                         \
+      }                                                                                                             \
+    }                                                                                                               \
+    for (size_t j = j0c; j < j1c; ++j) cr[j] = FMA(alpha, acc[j], cr[j]);                                          \
+  }                                                                                                                 \
   static void NAME##_tile(size_t i0, size_t mb, size_t j0, size_t nb, size_t k, T alpha, const T* a, ptrdiff_t rsa,  \
                           ptrdiff_t csa, const T* b, ptrdiff_t rsb, ptrdiff_t csb, T beta, T* c, ptrdiff_t rsc,       \
-                          ptrdiff_t csc, T* bp, T* cv, T* acc) {                                                      \
+                          ptrdiff_t csc, T* bp, T* ap, T* cv, T* acc) {                                               \
     for (size_t i = 0; i < mb; ++i)                                                                                   \
       for (size_t j = 0; j < nb; ++j)                                                                                 \
         cv[i * NBF + j] = (beta == (T)0) ? (T)0 : beta * c[(ptrdiff_t)(i0 + i) * rsc + (ptrdiff_t)(j0 + j) * csc];    \
@@ -250,28 +312,24 @@ static void find_params_lo(const float* vals, size_t len, uint32_t bits, int mse
         else                                                                                                          \
           for (size_t j = 0; j < nb; ++j) dst[j] = brow[(ptrdiff_t)j * csb];                                          \
       }                                                                                                               \
-      for (size_t i = 0; i < mb; ++i) {                                                                               \
-        const T* arow = a + (ptrdiff_t)(i0 + i) * rsa + (ptrdiff_t)k0 * csa;                                          \
-        for (size_t j = 0; j < nb; ++j) acc[j] = (T)0;                                                                \
-        if (g_mut == 11) { /* planted mutation 11: every product rounded before it is added */                       \
-          for (size_t kk = 0; kk < kc; ++kk) {                                                                        \
-            const T av = arow[(ptrdiff_t)kk * csa];                                                                   \
-            const T* bk = bp + kk * NBF;                                                                              \
-            for (size_t j = 0; j < nb; ++j) {                                                                         \
-              const T p = av * bk[j];                                                                                 \
-              acc[j] = acc[j] + p;                                                                                    \
-            }                                                                                                         \
-          }                                                                                                           \
-        } else {                                                                                                      \
-          for (size_t kk = 0; kk < kc; ++kk) {                                                                        \
-            const T av = arow[(ptrdiff_t)kk * csa];                                                                   \
-            const T* bk = bp + kk * NBF;                                                                              \
-            for (size_t j = 0; j < nb; ++j) acc[j] = FMA(av, bk[j], acc[j]);                                         \
-          }                                                                                                           \
-        }                                                                                                             \
-        T* cr = cv + i * NBF;                                                                                         \
-        for (size_t j = 0; j < nb; ++j) cr[j] = FMA(alpha, acc[j], cr[j]);                                           \
-      }                                                                                                               \
+      const size_t nbv = (g_mut == 11) ? 0 : nb - nb % (2 * W); /* columns taken by the vector chains */             \
+      const size_t mbv = nbv ? mb - mb % 4 : 0; /* rows taken by the vector chains */                               \
+      /* A rows packed k-major in groups of 4 (ap[i*KC + kk*4 + r]), read along A's contiguous direction */         \
+      if (rsa == 1)                                                                                                   \
+        for (size_t kk = 0; kk < kc; ++kk)                                                                            \
+          for (size_t i = 0; i < mbv; ++i) ap[(i & ~(size_t)3) * KC + kk * 4 + (i & 3)] = a[(ptrdiff_t)(i0 + i) + (ptrdiff_t)(k0 + kk) * csa]; \
+      else                                                                                                            \
+        for (size_t i = 0; i < mbv; ++i)                                                                              \
+          for (size_t kk = 0; kk < kc; ++kk)                                                                          \
+            ap[(i & ~(size_t)3) * KC + kk * 4 + (i & 3)] = a[(ptrdiff_t)(i0 + i) * rsa + (ptrdiff_t)(k0 + kk) * csa]; \
+      for (size_t j = 0; j < nbv; j += 2 * W)                                                                         \
+        for (size_t i = 0; i < mbv; i += 4) NAME##_mk4(ap + i * KC, bp + j, kc, alpha, cv + i * NBF + j);             \
+      for (size_t i = 0; i < mbv; ++i)                                                                                \
+        NAME##_rows1(a + (ptrdiff_t)(i0 + i) * rsa + (ptrdiff_t)k0 * csa, csa, bp, kc, nbv, nb, alpha, cv + i * NBF,  \
+                     acc);                                                                                            \
+      for (size_t i = mbv; i < mb; ++i)                                                                               \
+        NAME##_rows1(a + (ptrdiff_t)(i0 + i) * rsa + (ptrdiff_t)k0 * csa, csa, bp, kc, 0, nb, alpha, cv + i * NBF,    \
+                     acc);                                                                                            \
     }                                                                                                                 \
     for (size_t i = 0; i < mb; ++i)                                                                                   \
       for (size_t j = 0; j < nb; ++j) c[(ptrdiff_t)(i0 + i) * rsc + (ptrdiff_t)(j0 + j) * csc] = cv[i * NBF + j];    \
@@ -295,21 +353,23 @@ static void find_params_lo(const float* vals, size_t len, uint32_t bits, int mse
       T* bp = (T*)xcalloc((size_t)KC * NBF, sizeof(T));                                                               \
       T* cv = (T*)xcalloc((size_t)MB * NBF, sizeof(T));                                                               \
       T* acc = (T*)xcalloc(NBF, sizeof(T));                                                                           \
+      T* ap = (T*)xcalloc((size_t)MB * KC, sizeof(T));                                                                \
       _Pragma("omp for schedule(dynamic)") for (size_t t = 0; t < ntiles; ++t) {                                      \
         size_t ti = t / ntj, tj = t % ntj;                                                                            \
         size_t i0 = ti * MB, j0 = tj * NBF;                                                                           \
         size_t mb = (m - i0 < MB) ? m - i0 : MB;                                                                      \
         size_t nb = (n - j0 < NBF) ? n - j0 : NBF;                                                                    \
-        NAME##_tile(i0, mb, j0, nb, k, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc, bp, cv, acc);              \
+        NAME##_tile(i0, mb, j0, nb, k, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc, bp, ap, cv, acc);          \
       }                                                                                                               \
       free(bp);                                                                                                       \
       free(cv);                                                                                                       \
       free(acc);                                                                                                      \
+      free(ap);                                                                                                       \
     }                                                                                                                 \
   }
 
-DEFINE_GEMM(sg, float, fmaf)
-DEFINE_GEMM(dg, double, fma)
+DEFINE_GEMM(sg, float, fmaf, 8)
+DEFINE_GEMM(dg, double, fma, 4)
 
 /* single-thread wrappers = src/linalg.rs:98-99; parallel = pgemm_f32/f64 (src/linalg.rs:183-184) */
 static void sgemm1(size_t m, size_t k, size_t n, float alpha, const float* a, ptrdiff_t rsa, ptrdiff_t csa,
