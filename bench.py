@@ -153,6 +153,131 @@ def gram_jobs(spec: dict, xs: dict, xts: dict, h64s: dict, m64s: dict):
     return jobs
 
 
+class LayerStep:
+    """One decoder layer of a config, resident in HBM, and its step.
+
+    Holds the calibration inputs (generated on the device), the f64 accumulators and their f32
+    copies (H, and M with the asymmetric target), the weights and the output buffers. A step runs
+    every accumulation in one batched launch, then one quantize_layer call per matrix. The matrices
+    form one chain per input: the matrices of an input share its factorisation through one
+    context's factor cache, in the reference's order (src/pipeline.rs:109-130); different inputs
+    are independent, so with serial=False their chains run concurrently, each on its own context
+    (stream, workspace, cache) from its own host thread. Each call is the same synchronous
+    quantize_layer as in the serial order, with the same results. Every cache is cleared at the
+    start of a step (each step's H are new)."""
+
+    def __init__(self, ctx, spec: dict, serial: bool = False, weights: bool = True):
+        import cdclq
+
+        self.ctx, self.spec, self.serial = ctx, spec, serial
+        self.T = spec["tokens"]
+        self.xs, self.xts = make_inputs(ctx, spec)
+        self.h64s, self.h32s, self.m64s, self.m32s = {}, {}, {}, {}
+        for key, n in spec["inputs"].items():
+            self.h64s[key] = cdclq.DeviceArray(ctx, (n, n), np.float64)
+            self.h32s[key] = cdclq.DeviceArray(ctx, (n, n), np.float32)
+            if self.xts:
+                self.m64s[key] = cdclq.DeviceArray(ctx, (n, n), np.float64)
+                self.m32s[key] = cdclq.DeviceArray(ctx, (n, n), np.float32)
+        self.jobs = gram_jobs(spec, self.xs, self.xts, self.h64s, self.m64s)
+        self.cfg = cdclq.Config(**spec["cfg"])
+        self.ws, self.outs, self.perm_gbits = {}, {}, {}
+        self.chains, self.chain_ctx, self.pool = {}, {}, None
+        if not weights:
+            return
+        for li, (name, d_out, key) in enumerate(spec["layers"]):
+            n = spec["inputs"][key]
+            self.ws[name] = cdclq.DeviceArray(ctx, (d_out, n), np.float32)
+            ctx.check(cdclq.lib().cdclq_synth_normal_device(ctx.ptr, weight_seed(li), 0, d_out * n, spec["wsigma"],
+                                                             self.ws[name].ptr))
+            ng = (n + self.cfg.group - 1) // self.cfg.group
+            self.outs[name] = (cdclq.DeviceArray(ctx, (d_out, n), np.uint8),
+                               cdclq.DeviceArray(ctx, (d_out, ng), np.float32),
+                               cdclq.DeviceArray(ctx, (d_out, ng), np.float32))
+        for name, d_out, key in spec["layers"]:
+            self.chains.setdefault(key, []).append((name, d_out, key))
+        self.chain_ctx = {k: (ctx if serial else cdclq.Context(0)) for k in self.chains}
+        if not serial:
+            self.pool = concurrent.futures.ThreadPoolExecutor(max_workers=len(self.chains))
+
+    def contexts(self) -> list:
+        return [self.ctx] + ([] if self.serial else list(self.chain_ctx.values()))
+
+    def gram(self, keys):
+        """The accumulations of the inputs `keys` in one launch (each equals its own
+        gram_accumulate), then their f32 copies."""
+        import cdclq
+
+        ctx, T = self.ctx, self.T
+        js = [j for j in self.jobs if j[3] in keys]
+        for _, _, h, _ in js:
+            h.zero()
+        cdclq.gram_accumulate_batch_device(ctx, [j[0] for j in js], [j[1] for j in js], [T] * len(js),
+                                           [j[0].shape[1] for j in js], [j[2] for j in js])
+        for key in keys:
+            n = self.spec["inputs"][key]
+            ctx.check(cdclq.lib().cdclq_f64_to_f32_device(ctx.ptr, self.h64s[key].ptr, n * n, self.h32s[key].ptr))
+            if self.xts:
+                ctx.check(cdclq.lib().cdclq_f64_to_f32_device(ctx.ptr, self.m64s[key].ptr, n * n,
+                                                               self.m32s[key].ptr))
+
+    def run_chain(self, cctx, names):
+        """The chain's quantize_layer calls in order on one context; returns ({name: (LayerStats,
+        near-midpoint counts)}, seconds)."""
+        import cdclq
+
+        out = {}
+        t0 = time.perf_counter()
+        for name, d_out, key in names:
+            n = self.spec["inputs"][key]
+            c, s, z = self.outs[name]
+            perm, gbits, st = cdclq.quantize_layer_device(cctx, self.ws[name], d_out, n, self.h32s[key],
+                                                          self.m32s.get(key), key, self.cfg, c, s, z,
+                                                          nthreads=self.spec["nthreads"])
+            out[name] = (st, cctx.last_midpoint_counts())
+            self.perm_gbits[name] = (perm, gbits)
+        return out, time.perf_counter() - t0
+
+    def step(self):
+        """One layer: returns ({name: (LayerStats, near-midpoint counts)}, host wall split)."""
+        stats = {}
+        for c in set(self.chain_ctx.values()):
+            c.clear_cache()
+        t0 = time.perf_counter()
+        self.gram(list(self.spec["inputs"]))  # all accumulations in one launch (synchronous)
+        t1 = time.perf_counter()
+        chain_s = {}
+        if self.serial:  # the matrices one after another
+            res, _ = self.run_chain(self.ctx, self.spec["layers"])
+            stats.update(res)
+        else:  # the chains at once, each on its own context
+            futs = {k: self.pool.submit(self.run_chain, self.chain_ctx[k], self.chains[k]) for k in self.chains}
+            for k, fut in futs.items():
+                res, chain_s[k] = fut.result()
+                stats.update(res)
+        return stats, {"gram": t1 - t0, "quantize": time.perf_counter() - t1, "chains": chain_s}
+
+    def free_inputs(self):
+        for d in list(self.xs.values()) + list(self.xts.values()):
+            d.free()
+        self.xs, self.xts = {}, {}
+
+    def close_chains(self):
+        if self.pool is not None:
+            self.pool.shutdown()
+            self.pool = None
+            for c in self.chain_ctx.values():
+                c.close()
+            self.chain_ctx = {k: self.ctx for k in self.chain_ctx}
+
+    def free(self):
+        self.close_chains()
+        self.free_inputs()
+        for d in (list(self.h64s.values()) + list(self.h32s.values()) + list(self.m64s.values())
+                  + list(self.m32s.values()) + list(self.ws.values()) + [a for o in self.outs.values() for a in o]):
+            d.free()
+
+
 def gram_flops(n: int, t: int) -> float:
     """Algorithmic work of one symmetric H accumulation: n(n+1) t flops (one triangle)."""
     return float(n) * (n + 1) * t
@@ -180,103 +305,102 @@ def factorisations(spec: dict) -> list:
     return list(spec["inputs"].values())
 
 
-def cpu_sample(spec: dict, cores: int, n0: int, rows: int, rc: int, with_factor: bool = True):
-    """Times the oracle's quantize_layer on `rows` x n0 (chunks of rc) with a synthetic H; returns
-    (seconds of phase 1+2, seconds of the factorisation or 0, seconds of the target GEMMs or 0)."""
-    import oracle as O
-
-    cs = O.synth_outlier_scales(101, n0, 0.01, 20.0)
-    x = O.synth_tokens(102, 2048, n0, cs)
-    h = O.gram_accumulate(x).astype(np.float32)
-    w = O.synth_normal(103, rows * n0, spec["wsigma"]).reshape(rows, n0)
-    t_fac = 0.0
-    if with_factor:
-        hd = h.astype(np.float64)
-        hd[np.arange(n0), np.arange(n0)] += 0.01 * np.mean(np.diag(hd))
-        t0 = time.perf_counter()
-        O.upper_chol_of_inverse(hd)
-        t_fac = time.perf_counter() - t0
-    cfg = O.config(**{**spec["cfg"], "row_chunk": rc})
-    m = h if spec.get("asym_noise") else None
-    q = O.quantize_layer(w, h, cfg, m=m, nthreads=cores)
-    # secs_prepare holds the factorisation and (with M) the target GEMMs; the factor is timed above
-    t_target = max(0.0, q.stats["secs_prepare"] - t_fac) if m is not None else 0.0
-    return q.stats["secs_quant"], t_fac, t_target
+def rows_per_chunk(spec: dict, d_out: int) -> int:
+    """The reference's row chunk (src/engine.rs:768-770) at the config's thread count."""
+    rc = spec["cfg"].get("row_chunk", 0)
+    if rc <= 0:
+        rc = min(max(-(-d_out // spec["nthreads"]), 32), 256)
+    return max(min(rc, d_out), 1)
 
 
-def cpu_baseline(spec: dict, cores: int) -> dict:
-    """Time the oracle (C restatement of the reference's rayon path) on a bounded sample of the
-    workload and extrapolate to one full step with the work scaling of each phase: the Gram by
-    n^2 T per accumulation (the reference computes every entry, also of a symmetric H), the
-    factorisation by n^3, phase 1 + 2 (and the asymmetric target) by rows x n^2."""
+FACTOR_SAMPLE_MAX_N = 16384  # wider factorisations are extrapolated by n^3 (minutes on the host)
+
+
+def cpu_baseline(spec: dict, cores: int, fetch) -> dict:
+    """The oracle (C restatement of the reference's rayon path) timed on bounded samples of the
+    step's own work, on this host, then scaled to one step.
+
+    `fetch(kind, key_or_name, rows)` returns the workload's own host arrays after the timed region:
+    ("h", key) the f32 H, ("m", key) the f32 M, ("w", name, rows) the first rows of a matrix.
+    * Gram: each distinct width accumulates a slab of the config's synthetic tokens; scaled by
+      T / slab (2048-token chunks in sequence, each the same work) per accumulation.
+    * Factorisation + phase 1 + 2: for each distinct width, the widest-row matrix of that width is
+      quantized on one wave of row chunks (one chunk per thread, the reference's chunk size, with
+      the step's real H and W rows): secs_prepare is the factorisation, secs_quant the wave of
+      chunks. Each matrix is then ceil(chunks / threads) waves of its own chunk size (per-chunk time
+      taken linear in its rows), which is how chunks map to the reference's thread pool.
+    * Widths above FACTOR_SAMPLE_MAX_N (config 5's 28672) take the sample of the widest width at
+      or below it, scaled by n^3 (factor) and n^2 x rows (chunks, target GEMMs)."""
     import oracle as O
 
     O.set_threads(cores)
-    n0 = min(4096, min(spec["inputs"].values()))
-    ts = 16384  # eight 2048-token chunks
-    x = O.synth_tokens(102, ts, n0, None)
-    t0 = time.perf_counter()
-    O.gram_accumulate(x)
-    t_gram = time.perf_counter() - t0
     T = spec["tokens"]
-    njobs = 2 if spec.get("asym_noise") else 1  # H~ and M per input with the asymmetric target
-    gram_full = t_gram * njobs * sum(n * n * T for n in spec["inputs"].values()) / (n0 * n0 * ts)
-    rc = 171 if n0 == 4096 else 64
-    rows = min(2 * rc * cores, 8192)  # two row chunks per thread
-    t_q, t_fac, t_tgt = cpu_sample(spec, cores, n0, rows, rc)
-    fac_full = t_fac * sum((n / n0) ** 3 for n in factorisations(spec))
-    quant_full = target_full = 0.0
-    for (_, d_out, key) in spec["layers"]:
+    asym = bool(spec.get("asym_noise"))
+    njobs = 2 if asym else 1  # H~ and M per input with the asymmetric target
+    widths = sorted(set(spec["inputs"].values()))
+    notes = []
+    gram_full = 0.0
+    for n in widths:
+        slab = min(T, 8192 if n <= 4096 else 2048 if n <= 16384 else 1024)
+        x = O.synth_tokens(102, slab, n, None)
+        t0 = time.perf_counter()
+        O.gram_accumulate(x)
+        t = time.perf_counter() - t0
+        del x
+        cnt = sum(1 for v in spec["inputs"].values() if v == n)
+        gram_full += t * njobs * cnt * T / slab
+        notes.append(f"gram {slab} tokens at n={n} {t:.2f}s")
+    cfg = O.config(**spec["cfg"])
+    samples = {}  # width -> (factor s, per-row chunk s, target s per row)
+    for n in [v for v in widths if v <= FACTOR_SAMPLE_MAX_N]:
+        key = next(k for k, v in spec["inputs"].items() if v == n)
+        name, d_out, _ = max((l for l in spec["layers"] if spec["inputs"][l[2]] == n), key=lambda l: l[1])
+        rc = rows_per_chunk(spec, d_out)
+        chunks = min(cores, -(-d_out // rc))
+        rows = min(d_out, chunks * rc)
+        h = fetch("h", key)
+        m = fetch("m", key) if asym else None
+        w = fetch("w", name, rows)
+        c = O.config(**{**spec["cfg"], "row_chunk": rc})
+        if asym:  # the target GEMMs are inside secs_prepare: time the factor on its own
+            hd = h.astype(np.float64)
+            t0 = time.perf_counter()
+            q = O.quantize_layer(w, h, c, m=m, hkey=key, nthreads=cores)
+            wall = time.perf_counter() - t0
+            hd[np.arange(n), np.arange(n)] += cfg.damp * np.mean(np.diag(hd))
+            t0 = time.perf_counter()
+            O.upper_chol_of_inverse(hd)
+            t_fac = time.perf_counter() - t0
+            t_tgt = max(0.0, q.stats["secs_prepare"] - t_fac) / rows
+        else:
+            q = O.quantize_layer(w, h, c, hkey=key, nthreads=cores)
+            t_fac, t_tgt = q.stats["secs_prepare"], 0.0
+        samples[n] = (t_fac, q.stats["secs_quant"] / rc, t_tgt)
+        notes.append(f"{name} n={n}: factor {t_fac:.2f}s, one wave of {chunks} chunks x {rc} rows "
+                     f"{q.stats['secs_quant']:.2f}s")
+        del h, m, w
+    fac_full = quant_full = target_full = 0.0
+    fac_widths = spec["inputs"].values() if spec["cfg"].get("skeleton_pct", 0.0) <= 0.0 else \
+        [spec["inputs"][key] for _, _, key in spec["layers"]]
+    for n in fac_widths:
+        n0 = max(v for v in samples if v <= n) if any(v <= n for v in samples) else max(samples)
+        fac_full += samples[n0][0] * (n / n0) ** 3
+    for name, d_out, key in spec["layers"]:
         n = spec["inputs"][key]
-        quant_full += t_q * (d_out / rows) * (n / n0) ** 2
-        target_full += t_tgt * (d_out / rows) * (n / n0) ** 2
+        n0 = n if n in samples else max(samples)
+        rc = rows_per_chunk(spec, d_out)
+        waves = -(-(-(-d_out // rc)) // cores)
+        quant_full += samples[n0][1] * rc * waves * (n / n0) ** 2
+        target_full += samples[n0][2] * d_out * (n / n0) ** 2
     total = gram_full + fac_full + quant_full + target_full
-    val = recorded_cpu_validation()
-    sample = (f"oracle on {cores} threads of {cpu_model()}: gram {ts} tokens x n={n0} ({t_gram:.2f}s, scaled by "
-              f"n^2*T per accumulation), factor n={n0} ({t_fac:.2f}s, scaled by n^3), phase1+2 of {rows} rows x "
-              f"n={n0} in chunks of {rc} ({t_q:.2f}s, scaled by rows and n^2; the number of repair passes is "
-              f"data-dependent, so this is a model, not a measurement)")
-    if t_tgt:
-        sample += f", asymmetric target GEMMs ({t_tgt:.2f}s, scaled by rows and n^2)"
-    if val:
-        sample += f"; {val}"
+    sample = (f"oracle on {cores} threads of {cpu_model()}, timed in this run on the step's own H and W rows: "
+              + "; ".join(notes) + ". Scaled to the step: Gram by tokens, each matrix by its waves of row chunks "
+              "(chunk time linear in rows); factorisations measured at their width"
+              + (" (wider ones by n^3)" if any(v > FACTOR_SAMPLE_MAX_N for v in widths) else "")
+              + ". Repair passes are data-dependent per chunk, so the waves are a model of the full step.")
     return {"value": round(total, 2), "unit": "s/layer", "cores": cores, "kind": "port", "cpu": cpu_model(),
             "sample": sample, "phases_s": {"gram": round(gram_full, 2), "factor": round(fac_full, 2),
                                            "quant": round(quant_full, 2), "target": round(target_full, 2)}}
-
-
-def recorded_cpu_validation():
-    """The check of the rows x n^2 model against a timed down_proj-width sample, as recorded in
-    profiles/cpu_baseline_c4.md by `bench.py --cpu-validate` (None if not recorded)."""
-    try:
-        with open(os.path.join(ROOT, "profiles", "cpu_baseline_c4.md")) as f:
-            for line in f:
-                if line.startswith("validation:"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return None
-
-
-def cpu_validate(spec: dict, cores: int):
-    """Times phase 1 + 2 of the down_proj width (n = 14336, one row chunk of 171 per thread) and
-    compares it with the rows x n^2 extrapolation from the n = 4096 sample cpu_baseline uses."""
-    import oracle as O
-
-    O.set_threads(cores)
-    n0, rc = 4096, 171
-    rows0 = min(2 * rc * cores, 8192)
-    t_q0, _, _ = cpu_sample(spec, cores, n0, rows0, rc, with_factor=False)
-    n1 = max(spec["inputs"].values())
-    rows1 = rc * cores
-    t0 = time.perf_counter()
-    t_q1, _, _ = cpu_sample(spec, cores, n1, rows1, rc, with_factor=False)
-    wall = time.perf_counter() - t0
-    predicted = t_q0 * (rows1 / rows0) * (n1 / n0) ** 2
-    line = (f"measured phase1+2 of {rows1} rows x n={n1} (chunks of {rc}) = {t_q1:.1f}s vs {predicted:.1f}s "
-            f"predicted from {rows0} rows x n={n0} ({t_q0:.1f}s): measured/predicted = {t_q1 / predicted:.2f} "
-            f"({cores} threads of {cpu_model()})")
-    print(json.dumps({"cpu_validate": line, "wall_s": round(wall, 1)}), flush=True)
 
 
 def recorded_traffic(summary: str):
@@ -471,6 +595,43 @@ def container_bench(args, spec):
     ctx.close()
 
 
+def step_wall_ms(walls: list) -> dict:
+    """Host wall-clock split of the timed steps (means): the accumulations, then the quantize calls
+    (with the chains concurrent: from the first chain's start to the last one's end, and each
+    chain's own span). gram + quantize is the step; the per-phase device times overlap instead."""
+    k = len(walls)
+    out = {"gram": round(1e3 * sum(w["gram"] for w in walls) / k, 2),
+           "quantize": round(1e3 * sum(w["quantize"] for w in walls) / k, 2)}
+    if walls[0]["chains"]:
+        out["chains"] = {c: round(1e3 * sum(w["chains"][c] for w in walls) / k, 2) for c in walls[0]["chains"]}
+    return out
+
+
+def midpoint_report(stats: dict) -> dict:
+    """Near-midpoint rounding decisions of the step (cdclq_ctx_last_midpoint_counts after each
+    call): per matrix and summed over the layer. A decision is near when the f64 quotient of its
+    f32 operands lies within 1e-9 of k + 1/2 and the two candidates differ after clamping."""
+    per = {name: mid for name, (_, mid) in stats.items()}
+    tot = {}
+    for mid in per.values():
+        for f, v in mid.items():
+            tot[f] = tot.get(f, 0) + v
+    return {"layer": tot, "per_matrix": per}
+
+
+def bpw_report(spec: dict, stats: dict) -> dict:
+    """Effective bits per weight (LayerStats.bits_total: codes plus the f16 scale and 8-bit zero
+    point of each group, src/quant.rs:248-250) per matrix and weighted by element count over the
+    layer."""
+    per, num, den = {}, 0.0, 0
+    for name, d_out, key in spec["layers"]:
+        st = stats[name][0]
+        per[name] = {"bits_codes": st.bits_codes, "bits_total": st.bits_total}
+        num += st.bits_total * d_out * spec["inputs"][key]
+        den += d_out * spec["inputs"][key]
+    return {"layer_bits_total": round(num / den, 6), "per_matrix": per}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -486,8 +647,6 @@ def main():
                          "layer's quantized matrices (cdclq-v1)")
     ap.add_argument("--profile", action="store_true",
                     help="with --workload container: counter-collection run (1 GiB copy + one step)")
-    ap.add_argument("--cpu-validate", action="store_true",
-                    help="time the CPU baseline's rows x n^2 model against a down_proj-width sample and exit")
     ap.add_argument("--serial", action="store_true",
                     help="quantize the layer's matrices one after another on one context (default: the chains "
                          "of matrices that share an input run concurrently, one context each)")
@@ -509,89 +668,20 @@ def main():
         # dependent chains with no other waves on their SIMDs
         spec = dict(spec, layers=[(name, min(d_out, args.floor_rows), key) for name, d_out, key in spec["layers"]])
         args.steps, args.warmup, args.no_cpu_baseline, args.serial = 1, 0, True, True
-    if args.cpu_validate:
-        cpu_validate(spec, min(os.cpu_count() or 1, 16))
-        return
     if args.workload == "container":
         container_bench(args, spec)
         return
     T = spec["tokens"]
     ctx = cdclq.Context(0)
     log(f"[bench] {spec['workload']}: generating inputs in HBM")
-    xs, xts = make_inputs(ctx, spec)
-    h64s, h32s, m64s, m32s = {}, {}, {}, {}
-    for key, n in spec["inputs"].items():
-        h64s[key] = cdclq.DeviceArray(ctx, (n, n), np.float64)
-        h32s[key] = cdclq.DeviceArray(ctx, (n, n), np.float32)
-        if xts:
-            m64s[key] = cdclq.DeviceArray(ctx, (n, n), np.float64)
-            m32s[key] = cdclq.DeviceArray(ctx, (n, n), np.float32)
-    jobs = gram_jobs(spec, xs, xts, h64s, m64s)
     if args.profile_gram:
-        profile_gram(ctx, spec, jobs)
+        L = LayerStep(ctx, spec, serial=True, weights=False)
+        profile_gram(ctx, spec, L.jobs)
         ctx.close()
         return
-    ws, outs = {}, {}
-    cfg = cdclq.Config(**spec["cfg"])
-    for li, (name, d_out, key) in enumerate(spec["layers"]):
-        n = spec["inputs"][key]
-        ws[name] = cdclq.DeviceArray(ctx, (d_out, n), np.float32)
-        ctx.check(cdclq.lib().cdclq_synth_normal_device(ctx.ptr, weight_seed(li), 0, d_out * n, spec["wsigma"],
-                                                         ws[name].ptr))
-        ng = (n + cfg.group - 1) // cfg.group
-        outs[name] = (cdclq.DeviceArray(ctx, (d_out, n), np.uint8), cdclq.DeviceArray(ctx, (d_out, ng), np.float32),
-                      cdclq.DeviceArray(ctx, (d_out, ng), np.float32))
-
-    # The layer's matrices in chains by input: the matrices of one input share its factorisation
-    # (one context's factor cache, in the reference's order); different inputs are independent, so
-    # after the accumulations their chains run concurrently on their own contexts. Each call is the
-    # same synchronous quantize_layer as in the serial order, with the same results.
-    chains = {}
-    for name, d_out, key in spec["layers"]:
-        chains.setdefault(key, []).append((name, d_out, key))
-    chain_ctx = {k: (ctx if args.serial else cdclq.Context(0)) for k in chains}
-    pool = None if args.serial else concurrent.futures.ThreadPoolExecutor(max_workers=len(chains))
-    all_ctx = [ctx] + ([] if args.serial else list(chain_ctx.values()))
-
-    def gram(keys):
-        """The accumulations of the inputs `keys` in one launch (each equals its own gram_accumulate),
-        then their f32 copies."""
-        js = [j for j in jobs if j[3] in keys]
-        cdclq.gram_accumulate_batch_device(ctx, [j[0] for j in js], [j[1] for j in js], [T] * len(js),
-                                           [j[0].shape[1] for j in js], [j[2] for j in js])
-        for key in keys:
-            n = spec["inputs"][key]
-            ctx.check(cdclq.lib().cdclq_f64_to_f32_device(ctx.ptr, h64s[key].ptr, n * n, h32s[key].ptr))
-            if xts:
-                ctx.check(cdclq.lib().cdclq_f64_to_f32_device(ctx.ptr, m64s[key].ptr, n * n, m32s[key].ptr))
-
-    def step():
-        stats = {}
-        for _, _, h, _ in jobs:
-            h.zero()
-
-        def run_chain(cctx, names):
-            out = {}
-            for name, d_out, key in names:
-                n = spec["inputs"][key]
-                c, s, z = outs[name]
-                _, _, st = cdclq.quantize_layer_device(cctx, ws[name], d_out, n, h32s[key], m32s.get(key), key, cfg,
-                                                       c, s, z, nthreads=spec["nthreads"])
-                out[name] = st
-            return out
-
-        # this step's H are new: no factorisation carries over from the previous step
-        for c in set(chain_ctx.values()):
-            c.clear_cache()
-        if args.serial:  # all accumulations in one launch, then the matrices one after another
-            gram(list(spec["inputs"]))
-            stats.update(run_chain(ctx, spec["layers"]))
-        else:  # one launch, then the chains at once, each on its own context (stream, workspace, cache)
-            gram(list(spec["inputs"]))
-            for fut in [pool.submit(run_chain, chain_ctx[k], chains[k]) for k in chains]:
-                stats.update(fut.result())
-        return stats
-
+    L = LayerStep(ctx, spec, serial=args.serial)
+    jobs, all_ctx, cfg = L.jobs, L.contexts(), L.cfg
+    step = L.step
     for i in range(args.warmup):
         t0 = time.perf_counter()
         step()
@@ -599,12 +689,13 @@ def main():
     for c in all_ctx:
         c.set_timing(True)
         c.reset_timing()
-    times = []
+    times, walls = [], []
     for i in range(args.steps):
         t0 = time.perf_counter()
-        stats = step()
+        stats, wall = step()
         times.append(time.perf_counter() - t0)
-        log(f"[bench] step {i} {times[-1]:.3f}s")
+        walls.append(wall)
+        log(f"[bench] step {i} {times[-1]:.3f}s (gram {wall['gram']:.3f}s, quantize {wall['quantize']:.3f}s)")
     ph = {}
     for c in all_ctx:  # device time per phase, summed over the contexts (concurrent chains overlap)
         for k, v in c.timing().items():
@@ -613,9 +704,9 @@ def main():
             e["launches"] += v["launches"]
         c.set_timing(False)
     ms_per_step = 1000.0 * sum(times) / len(times)
-    for name, st in stats.items():
+    for name, (st, mid) in stats.items():
         log(f"[bench] {name}: loss_gptq {st.loss_gptq:.6e} loss_final {st.loss_final:.6e} "
-            f"updates {st.code_updates} prepare {st.secs_prepare:.3f}s quant {st.secs_quant:.3f}s")
+            f"updates {st.code_updates} prepare {st.secs_prepare:.3f}s quant {st.secs_quant:.3f}s near-midpoint {mid}")
     gram_ms = ph["gram"]["ms"]
     gram_launches = ph["gram"]["launches"]
     # algorithmic work, one launch for all of the step's accumulations: n(n+1)T per symmetric H (one
@@ -625,10 +716,7 @@ def main():
     achieved = flops / (gram_ms * 1e-3) / 1e12 if gram_ms > 0 else 0.0
     phases = {k: round(v["ms"] / args.steps, 3) for k, v in ph.items()}
     log(f"[bench] device ms per step by phase: {phases}")
-    if pool is not None:
-        pool.shutdown()
-        for c in chain_ctx.values():
-            c.close()
+    L.close_chains()
     if args.floor_rows > 0:
         print(json.dumps({"profile": "floor-rows", "workload": spec["workload"], "rows": args.floor_rows,
                           "layers": {name: [d_out, spec["inputs"][key]] for name, d_out, key in spec["layers"]},
@@ -654,7 +742,12 @@ def main():
                    "quant": {**spec["cfg"], "passes": cfg.passes, "tol": cfg.tol}, "parallelism": "1 GPU",
                    "schedule": "matrices one after another" if args.serial else
                    "one chain of matrices per input, chains concurrent (one context and stream each)"},
-        "phases_ms_per_step": phases,
+        "step_wall_ms": step_wall_ms(walls),
+        ("phases_ms_per_step" if args.serial else "device_ms_per_step_summed_over_contexts"): phases,
+        "near_midpoint": midpoint_report(stats),
+        "bits_per_weight": bpw_report(spec, stats),
+        "matrices": {name: {"loss_gptq": st.loss_gptq, "loss_final": st.loss_final, "code_updates": st.code_updates}
+                     for name, (st, _) in stats.items()},
         "roofline": {
             "bound": "mfma",
             "kernel": f"k_gram_dma (the step's {len(jobs)} accumulations H += X^T Y in "
@@ -672,7 +765,14 @@ def main():
     if not args.no_cpu_baseline:
         cores = min(os.cpu_count() or 1, 16)
         log(f"[bench] timing the CPU baseline sample on {cores} threads")
-        result["cpu_baseline"] = cpu_baseline(spec, cores)
+
+        def fetch(kind, what, rows=None):
+            if kind == "w":
+                return L.ws[what].download()[:rows]
+            return (L.h32s if kind == "h" else L.m32s)[what].download()
+
+        L.free_inputs()
+        result["cpu_baseline"] = cpu_baseline(spec, cores, fetch)
     print(json.dumps(result), flush=True)
     ctx.close()
 

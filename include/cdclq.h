@@ -149,12 +149,15 @@ int cdclq_ctx_last_midpoint_counts(const cdclq_ctx* ctx, cdclq_midpoint_counts* 
 int cdclq_gram_accumulate(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h);
 int cdclq_gram_accumulate_device(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n, double* h);
 /* Allocation-free variant of cdclq_gram_accumulate_device, with no counterpart in the reference:
- * for callers that cannot allocate device memory (code under HIP graph capture, calibration hooks
- * in a tight forward loop, harnesses that forbid hipMalloc). Same arguments, same result bit for
- * bit. It calls no hipMalloc / hipFree: its status words and tile list live in a fixed array of
- * about 2 MiB per GPU, held until the process ends. Limit: n <= 32768 (larger n returns
- * CDCLQ_INVALID_ARG before any device work). Every call on a GPU shares that GPU's array, so calls
- * that overlap on one GPU (several contexts or threads at once) race; calls in sequence do not. */
+ * for callers that cannot allocate device memory (calibration hooks in a tight forward loop,
+ * harnesses that forbid hipMalloc). Same arguments, same result bit for bit. It calls no hipMalloc
+ * / hipFree: its status words and tile list live in a fixed array of about 2 MiB per GPU, held
+ * until the process ends. Like the other entry points it is synchronous: it reads the symmetry
+ * check's flag back to the host to choose the tile list, copies that list from host memory and
+ * waits for its stream, so it cannot be recorded into a HIP graph. Limit: n <= 32768 (larger n
+ * returns CDCLQ_INVALID_ARG before any device work). Every call on a GPU shares that GPU's array,
+ * so calls that overlap on one GPU (several contexts or threads at once) race; calls in sequence
+ * do not. */
 int cdclq_gram_accumulate_device_noalloc(cdclq_ctx* ctx, const float* x, const float* y, size_t t, size_t n,
                                         double* h);
 /* `count` independent accumulations in one launch (device pointers): hs[i] += xs[i]^T ys[i] with

@@ -162,7 +162,8 @@ def classify_mismatches(got_codes, want_codes, midmap, rc: int) -> dict:
     k + 1/2. Other mismatches in a row chunk of `rc` rows that holds an exempt one are cascaded: a
     different code changes that row's later errors and gradients, and the chunk's shared
     convergence decisions reach its other rows. The rest are non-exempt, i.e. real differences.
-    Returns counts: mismatches, exempt, cascaded, non_exempt, rows (with a mismatch), exempt_chunks."""
+    Returns counts: mismatches, exempt, cascaded, non_exempt, rows (with a mismatch), exempt_chunks,
+    and `chunk_ids`, the sorted indices of the row chunks holding an exempt mismatch."""
     bad = np.asarray(got_codes) != np.asarray(want_codes)
     rows = np.nonzero(bad.any(axis=1))[0]
     ex = bad & (np.asarray(midmap) != 0)
@@ -170,7 +171,13 @@ def classify_mismatches(got_codes, want_codes, midmap, rc: int) -> dict:
     total, n_ex = int(bad.sum()), int(ex.sum())
     casc = sum(int(bad[r].sum() - ex[r].sum()) for r in rows if r // rc in ex_chunks)
     return dict(mismatches=total, exempt=n_ex, cascaded=casc, non_exempt=total - n_ex - casc, rows=int(len(rows)),
-                exempt_chunks=len(ex_chunks))
+                exempt_chunks=len(ex_chunks), chunk_ids=sorted(ex_chunks))
+
+
+# Near-midpoint report of the session's parity comparisons: one record per comparison (label, the
+# oracle's counts, the GPU's counts, the mismatch classification or None when the codes are equal).
+# tests/conftest.py prints the totals at the end of the run.
+MIDPOINT_LOG: list = []
 
 
 def tie_problem(d_out: int = 48, n: int = 256, g: int = 64, seed: int = 5):

@@ -163,6 +163,47 @@ def test_tinyllama_configs_match_the_oracle(ctx, cname):
         d.free()
 
 
+def compare_with_digests(cname, gold, name, codes, scales, zeros, perm, gbits, st, mid=None):
+    got = dict(codes=codes, scales=scales, zeros=zeros, perm=perm, gbits=gbits)
+    g = gold["layers"][name]
+    diff = [f for f in ("codes", "scales", "zeros", "perm", "gbits") if sha(got[f]) != g[f]]
+    assert not diff, f"{cname} {name}: {diff} differ from the oracle's digests"
+    for f in ("loss_gptq", "loss_final"):
+        a, b = getattr(st, f), g["stats"][f]
+        assert abs(a - b) <= 1e-6 * abs(b), f"{cname} {name}: {f} {a!r} vs oracle {b!r}"
+    for f in ("subblocks_total", "subblocks_refined", "code_updates", "skeleton_groups", "bits_codes", "bits_total"):
+        assert getattr(st, f) == g["stats"][f], f"{cname} {name}: {f} {getattr(st, f)} vs {g['stats'][f]}"
+    if mid is not None and "midpoint" in g:
+        assert mid == g["midpoint"], f"{cname} {name}: near-midpoint counts {mid} vs oracle {g['midpoint']}"
+
+
+def test_concurrent_chains_match_the_oracle(ctx):
+    """The schedule behind the headline number (bench.py's LayerStep, serial=False): config 2's
+    layer with one chain per input (q->k->v, o, gate->up, down), the four chains concurrent on their
+    own contexts from their own host threads after one batched accumulation launch. Two steps in a
+    row (each clears the factor caches); every matrix equals the oracle's digests."""
+    spec = bench.CONFIGS["c2"]
+    with open(GOLDEN) as f:
+        gold = json.load(f)["configs"]["c2"]
+    L = bench.LayerStep(ctx, spec, serial=False)
+    try:
+        for rep in range(2):
+            print(f"[configs] c2 concurrent chains, step {rep}", flush=True)
+            stats, wall = L.step()
+            print(f"[configs] step {rep}: gram {wall['gram']:.3f}s quantize {wall['quantize']:.3f}s "
+                  f"chains {wall['chains']}", flush=True)
+            for key in spec["inputs"]:
+                assert sha(L.h32s[key].download()) == gold["inputs"][key]["h32_sha256"], f"c2 {key}: H differs"
+            for name, _, _ in spec["layers"]:
+                c, s, z = L.outs[name]
+                perm, gbits = L.perm_gbits[name]
+                st, mid = stats[name]
+                compare_with_digests("c2", gold, name, c.download(), s.download(), z.download(), perm, gbits, st,
+                                     mid)
+    finally:
+        L.free()
+
+
 # ---------------------------------------------------------------- config 5 at full size
 def test_config5_full_size_properties(ctx):
     """Llama-3-70B MLP: gate_proj 28672 x 8192 and down_proj 8192 x 28672, INT3 g128, passes 6, with

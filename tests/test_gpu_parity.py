@@ -10,8 +10,8 @@ import pytest
 
 import cdclq
 import oracle as O
-from problems import (classify_mismatches, damped, fixture_hessians, rand_spd, ref_problem, row_chunk, synth_layer,
-                      tie_problem)
+from problems import (MIDPOINT_LOG, classify_mismatches, damped, fixture_hessians, rand_spd, ref_problem, row_chunk,
+                      synth_layer, tie_problem)
 
 pytestmark = pytest.mark.gpu
 
@@ -45,34 +45,52 @@ def run_both(ctx, w, h, m=None, nthreads=8, hkey="layer", **kw):
     return qg, sg, qo
 
 
-def assert_same(qg, sg, qo, label=""):
-    """The parity bar: perm, gbits, codes, zeros and scales bit-exact, except code mismatches the
-    near-midpoint exemption covers (counted and reported; rows of such chunks may then differ in
-    scales and zeros as a cascade); losses within 1e-6; the GPU's near-midpoint accounting equal to
-    the oracle's."""
+def assert_same(qg, sg, qo, label="", allow_exempt=True):
+    """The parity bar: perm, gbits, codes, zeros and scales bit-exact; losses within 1e-6; the GPU's
+    near-midpoint accounting equal to the oracle's. The one exemption (north star): a code mismatch
+    where the oracle's own rounding input lay within 1e-9 of a midpoint (counted and reported). A
+    row chunk holding such a mismatch may then differ elsewhere too (its rows' later errors, its
+    shared selection and convergence decisions), so its rows' scales and zeros are not compared and
+    the layer-wide sums get a looser bound; every other row is still compared bit for bit.
+    `allow_exempt=False` fails on any mismatch (layers built to have none)."""
     so = qo.stats
     assert np.array_equal(qg.perm, qo.perm), f"{label}: perm differs"
     assert np.array_equal(qg.gbits, qo.gbits), f"{label}: gbits differ"
+    rc = getattr(qo, "rc", qg.codes.shape[0])
+    keep = np.ones(qg.codes.shape[0], bool)  # rows compared bit for bit
+    cls = None
     bad = np.argwhere(qg.codes != qo.codes)
     if bad.size:
         r, c = bad[0]
-        cls = classify_mismatches(qg.codes, qo.codes, qo.midmap, getattr(qo, "rc", qg.codes.shape[0])) \
-            if getattr(qo, "midmap", None) is not None else None
+        if getattr(qo, "midmap", None) is not None:
+            cls = classify_mismatches(qg.codes, qo.codes, qo.midmap, rc)
         print(f"[parity] {label}: near-midpoint classification {cls}", flush=True)
-        if cls is None or cls["non_exempt"]:
+        if cls is None or cls["non_exempt"] or not allow_exempt:
             raise AssertionError(f"{label}: {len(bad)} code mismatches; first at row {r} col {c}: "
                                  f"gpu {qg.codes[r, c]} oracle {qo.codes[r, c]}; rows affected "
                                  f"{len(np.unique(bad[:, 0]))}; classification {cls}")
-        return  # every mismatch is exempt or cascaded: the bar holds, with the counts reported above
-    sbad = np.argwhere(qg.scales.view(np.uint32) != qo.scales.view(np.uint32))
-    assert sbad.size == 0, f"{label}: {len(sbad)} scale mismatches, first {sbad[0]}"
-    assert np.array_equal(qg.zeros, qo.zeros), f"{label}: zero points differ"
+        for ch in cls["chunk_ids"]:
+            keep[ch * rc:(ch + 1) * rc] = False
+    MIDPOINT_LOG.append(dict(label=label, oracle=getattr(qo, "midpoint", None), gpu=getattr(qg, "midpoint", None),
+                             classification=cls))
+    sbad = np.argwhere(qg.scales[keep].view(np.uint32) != qo.scales[keep].view(np.uint32))
+    assert sbad.size == 0, f"{label}: {len(sbad)} scale mismatches outside exempt chunks, first {sbad[0]}"
+    zbad = np.argwhere(qg.zeros[keep] != qo.zeros[keep])
+    assert zbad.size == 0, f"{label}: {len(zbad)} zero-point mismatches outside exempt chunks, first {zbad[0]}"
+    assert np.array_equal(qg.codes[keep], qo.codes[keep]), f"{label}: codes differ outside exempt chunks"
     if getattr(qg, "midpoint", None) is not None and getattr(qo, "midpoint", None) is not None:
-        assert qg.midpoint == qo.midpoint, f"{label}: near-midpoint accounting gpu {qg.midpoint} oracle {qo.midpoint}"
+        if cls is None:
+            assert qg.midpoint == qo.midpoint, f"{label}: near-midpoint accounting gpu {qg.midpoint} oracle {qo.midpoint}"
+        else:  # a tie broken the other way changes that chunk's later decisions; the ties themselves are seen
+            assert qg.midpoint["code_near"] + qg.midpoint["zero_near"] + qg.midpoint["cd_near"] > 0, \
+                f"{label}: exempt mismatches but no near-midpoint decision counted on the GPU {qg.midpoint}"
+    rel = REL if cls is None else 1e-3  # cascaded chunks move the layer-wide sums a little
     for f in ("loss_gptq", "loss_final"):
         a, b = getattr(sg, f), so[f]
-        assert abs(a - b) <= REL * max(abs(b), 1e-300), f"{label}: {f} gpu {a!r} oracle {b!r}"
-    for f in ("subblocks_total", "subblocks_refined", "code_updates", "skeleton_groups"):
+        assert abs(a - b) <= rel * max(abs(b), 1e-300), f"{label}: {f} gpu {a!r} oracle {b!r}"
+    fields = ("subblocks_total", "skeleton_groups") if cls else \
+        ("subblocks_total", "subblocks_refined", "code_updates", "skeleton_groups")
+    for f in fields:
         assert getattr(sg, f) == so[f], f"{label}: {f} gpu {getattr(sg, f)} oracle {so[f]}"
     assert sg.bits_codes == so["bits_codes"] and sg.bits_total == so["bits_total"]
 
@@ -307,17 +325,28 @@ def test_quantize_variants(ctx, bits, group, block, act, mse):
                           passes=3), label=f"b{bits} g{group} B{block}")
 
 
+# (d_out, n, block, sub_block, row_chunk): the one-wavefront block sweep and descent (48 rows);
+# the lane-group sweep k_gptq_rows at 32, 16 and 8 lanes per row (2560, 4160 and 16448 rows);
+# blocks and sub-blocks wider than 1024 columns (k_gptq_block_mem, k_cd_mem).
+TIE_SHAPES = [(48, 256, 64, 64, 16), (2560, 256, 128, 64, 64), (4160, 256, 128, 64, 64), (16448, 128, 128, 64, 256),
+              (40, 3072, 2048, 1280, 16)]
+
+
+@pytest.mark.parametrize("shape", TIE_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}B{s[2]}sb{s[3]}")
 @pytest.mark.parametrize("method", ["gptq", "cdcl"])
-def test_quantize_tie_layer_midpoint_accounting(ctx, method):
+def test_quantize_tie_layer_midpoint_accounting(ctx, method, shape):
     """A layer whose codes, zero points and descent targets are exact f32 ties (every decision is
-    near a midpoint): bit-exact outputs and the same near-midpoint counts on the GPU as in the
-    oracle (assert_same compares them), which pins the device accounting."""
-    w, h = tie_problem()
-    qg, sg, qo = run_both(ctx, w, h, bits=4, group=64, block=64, act_order=False, row_chunk=16, passes=2,
-                          method=method, refit_scales=False)
+    near a midpoint): bit-exact outputs with no exemption used, and the same non-zero near-midpoint
+    counts on the GPU as in the oracle (assert_same compares them), which pins the device
+    accounting of every sweep kernel that counts."""
+    d_out, n, block, sub_block, rc = shape
+    w, h = tie_problem(d_out=d_out, n=n)
+    qg, sg, qo = run_both(ctx, w, h, bits=4, group=64, block=block, sub_block=sub_block, act_order=False,
+                          row_chunk=rc, passes=2, method=method, refit_scales=False)
     assert qo.midpoint["code_near"] > 0 and qo.midpoint["zero_near"] > 0
     assert method == "gptq" or qo.midpoint["cd_near"] > 0
-    assert_same(qg, sg, qo, label=f"ties {method}")
+    assert_same(qg, sg, qo, label=f"ties {method} {shape}", allow_exempt=False)
+    assert qg.midpoint == qo.midpoint
 
 
 def test_quantize_repair_knobs(ctx):

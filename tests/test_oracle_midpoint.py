@@ -62,7 +62,7 @@ def test_classifier_exempts_ties_and_catches_real_differences():
     r, c = near[0]
     got[r, c] ^= 1
     assert classify_mismatches(got, q.codes, mm, rc) == dict(mismatches=1, exempt=1, cascaded=0, non_exempt=0, rows=1,
-                                                            exempt_chunks=1)
+                                                            exempt_chunks=1, chunk_ids=[int(r) // rc])
     # a difference where the oracle's decision was not near a midpoint: non-exempt
     got = q.codes.copy()
     r2, c2 = far[0]

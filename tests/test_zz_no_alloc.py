@@ -70,3 +70,36 @@ def test_noalloc_gram_rejects_n_above_the_limit(ctx):
     assert rc == cdclq.INVALID_ARG
     assert "exceeds the allocation-free limit of 32768" in cdclq.lib().cdclq_last_error(ctx.ptr).decode()
     d.free()
+
+
+def _free_bytes():
+    hip = C.CDLL("libamdhip64.so")
+    free, total = C.c_size_t(0), C.c_size_t(0)
+    assert hip.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
+    return free.value
+
+
+def test_noalloc_gram_leaves_device_memory_unchanged():
+    """On a context that has never grown its workspace, the allocation-free call leaves the
+    device's free memory exactly as it was (inputs allocated beforehand, output read after the
+    second probe); the allocating call on another fresh context is printed as the contrast."""
+    rng = np.random.default_rng(23)
+    t, n = 4096, 512
+    x = rng.standard_normal((t, n)).astype(np.float32)
+    warm = cdclq.Context(0)
+    _pair(warm, x, x, np.zeros((n, n)), noalloc=True)  # code objects and the fixed array in place
+    warm.close()
+    for noalloc in (True, False):
+        c = cdclq.Context(0)
+        dx = cdclq.DeviceArray.from_host(c, x)
+        dh = cdclq.DeviceArray.from_host(c, np.zeros((n, n)))
+        fn = cdclq.lib().cdclq_gram_accumulate_device_noalloc if noalloc else cdclq.lib().cdclq_gram_accumulate_device
+        before = _free_bytes()
+        c.check(fn(c.ptr, dx.ptr, dx.ptr, t, n, dh.ptr))
+        after = _free_bytes()
+        print(f"[noalloc] noalloc={noalloc}: free device memory {before} -> {after}", flush=True)
+        if noalloc:
+            assert after == before, f"the allocation-free call changed free device memory by {after - before}"
+        for d in (dx, dh):
+            d.free()
+        c.close()
