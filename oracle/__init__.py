@@ -138,6 +138,7 @@ def lib():
         L.orc_synth_normal_at.restype = C.c_float
         L.orc_synth_normal.argtypes = [C.c_uint64, C.c_uint64, sz, C.c_float, f32p]
         L.orc_synth_outlier_scales.argtypes = [C.c_uint64, sz, C.c_double, C.c_float, f32p]
+        L.orc_synth_lognormal_scales.argtypes = [C.c_uint64, sz, C.c_float, f32p]
         L.orc_synth_tokens.argtypes = [C.c_uint64, C.c_uint64, sz, sz, C.c_void_p, f32p]
         L.orc_synth_tokens_heavy.argtypes = [C.c_uint64, C.c_uint64, sz, sz, C.c_void_p, C.c_void_p, f32p]
         L.orc_last_midpoint_counts.argtypes = [C.c_void_p]
@@ -471,6 +472,12 @@ def synth_normal(seed: int, n: int, sigma: float = 1.0, offset: int = 0) -> np.n
 def synth_outlier_scales(seed: int, n: int, frac: float, factor: float) -> np.ndarray:
     out = np.empty(n, np.float32)
     lib().orc_synth_outlier_scales(seed, n, frac, factor, out)
+    return out
+
+
+def synth_lognormal_scales(seed: int, n: int, sigma: float) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_synth_lognormal_scales(seed, n, sigma, out)
     return out
 
 

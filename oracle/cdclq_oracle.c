@@ -1291,6 +1291,12 @@ void orc_synth_normal(uint64_t seed, uint64_t offset, size_t n, float sigma, flo
   for (size_t i = 0; i < n; ++i) out[i] = orc_synth_normal_at(seed, offset + i) * sigma;
 }
 
+/* Log-normal channel scales exp(sigma * normal(seed, j)), the exponential in f64 (libm) rounded
+ * once to f32: the host generator of the benchmark's config 5 inputs. */
+void orc_synth_lognormal_scales(uint64_t seed, size_t n, float sigma, float* scales) {
+  for (size_t j = 0; j < n; ++j) scales[j] = (float)exp((double)sigma * (double)orc_synth_normal_at(seed, j));
+}
+
 void orc_synth_outlier_scales(uint64_t seed, size_t n, double frac, float factor, float* scales) {
   size_t k = (size_t)round(frac * (double)n);
   if (k > n) k = n;

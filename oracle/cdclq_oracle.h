@@ -171,6 +171,7 @@ float orc_synth_normal_at(uint64_t seed, uint64_t i);
 void orc_synth_normal(uint64_t seed, uint64_t offset, size_t n, float sigma, float* out);
 /* Per-channel scale vector: exactly round(frac*n) channels (seeded Fisher-Yates) get `factor`. */
 void orc_synth_outlier_scales(uint64_t seed, size_t n, double frac, float factor, float* scales);
+void orc_synth_lognormal_scales(uint64_t seed, size_t n, float sigma, float* scales);
 /* X (t x n, token-major): x[r][j] = normal_at(seed, (row0 + r)*n + j) * ch_scale[j]. */
 void orc_synth_tokens(uint64_t seed, uint64_t row0, size_t t, size_t n, const float* ch_scale, float* x);
 float orc_synth_student3_at(uint64_t seed, uint64_t i);

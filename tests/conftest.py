@@ -25,14 +25,16 @@ def pytest_terminal_summary(terminalreporter):
     if not MIDPOINT_LOG:
         return
     tot = {}
-    for rec in MIDPOINT_LOG:
+    both = [r for r in MIDPOINT_LOG if r["oracle"] and r["gpu"]]
+    for rec in both:
         for side in ("oracle", "gpu"):
-            for k, v in (rec[side] or {}).items():
+            for k, v in rec[side].items():
                 tot[(side, k)] = tot.get((side, k), 0) + v
     fired = [r for r in MIDPOINT_LOG if r["classification"]]
     tr = terminalreporter
     tr.section("near-midpoint report")
-    tr.write_line(f"{len(MIDPOINT_LOG)} parity comparisons; comparisons with an exempt code mismatch: {len(fired)}")
+    tr.write_line(f"{len(MIDPOINT_LOG)} parity comparisons, {len(both)} with counts from both sides (totalled "
+                  f"below); comparisons with an exempt code mismatch: {len(fired)}")
     for side in ("oracle", "gpu"):
         tr.write_line(f"{side}: " + ", ".join(f"{k} {v}" for (s, k), v in sorted(tot.items()) if s == side))
     for r in fired:

@@ -1,7 +1,7 @@
 """Writes tests/golden/config_digests.json: the oracle's results for BASELINE configs 2, 3 and 4
 at their real shapes, as SHA-256 digests.
 
-    python tests/golden/make_config_digests.py [c2c3] [c4]    (default: both)
+    python tests/golden/make_config_digests.py [c2c3] [c4] [c5]    (default: c2c3 c4)
 
 Configs 2 and 3 are the TinyLlama-1.1B-shaped decoder layer (262,144 tokens, 0.5% Student-t(3)
 channels); config 4 is the Llama-3-8B-shaped decoder layer (524,288 tokens, 1% outlier channels
@@ -17,6 +17,11 @@ of codes, scales, zeros (f32 bytes), perm (u32) and gbits, plus the LayerStats f
 also records each input's f64 H, the oracle's near-midpoint counts per matrix, and the SHA-256 of
 U = upper_chol_of_inverse(H + 0.01 mean(diag H) I) (f32, the public linalg entry point,
 src/linalg.rs:362-375) of its n = 14336 input.
+
+Config 5 (Llama-3-70B MLP, n = 8192 and 28672, H~ = X~^T X~ and M = X^T X~ over 524,288 tokens,
+asymmetric target) records the f32 and f64 digests of both inputs' H~ and M (about 3 hours of the
+oracle's Gram on 8 cores) and, per matrix, the digests of its first C5_CHUNKS row chunks (default
+7, the chunk size of the full run), with those rows' own stats and near-midpoint counts.
 """
 from __future__ import annotations
 
@@ -49,24 +54,37 @@ def channel_args(spec: dict, i: int, n: int):
     xg = spec.get("xgen")
     if xg is None:
         return O.synth_outlier_scales(cseed, n, spec["outlier_frac"], spec["outlier_factor"]), None
+    if xg["kind"] == "lognormal":
+        return O.synth_lognormal_scales(cseed, n, xg["sigma"]), None
     assert xg["kind"] == "heavy"
     return None, (O.synth_outlier_scales(cseed, n, xg["frac"], 2.0) != 1.0).astype(np.uint8)
 
 
-def hessian64(spec: dict, i: int, n: int) -> np.ndarray:
-    """f64 Gram of input i over the config's tokens, generated and accumulated slab by slab."""
-    tseed = bench.input_seeds(i)[1]
+def hessian64(spec: dict, i: int, n: int):
+    """f64 Gram of input i over the config's tokens, generated and accumulated slab by slab. With
+    the asymmetric target (X~ = X + sigma N(0, 1), the perturbation stream indexed by element):
+    (H~ = X~^T X~, M = X^T X~); otherwise H = X^T X."""
+    _, tseed, pseed = bench.input_seeds(i)
     cs, heavy = channel_args(spec, i, n)
     T = spec["tokens"]
+    asym = spec.get("asym_noise", 0.0)
     h = np.zeros((n, n), np.float64)
+    m = np.zeros((n, n), np.float64) if asym else None
     t0 = time.time()
     for r0 in range(0, T, SLAB):
-        x = O.synth_tokens(tseed, min(SLAB, T - r0), n, cs, row0=r0, heavy=heavy)
-        O.gram_accumulate(x, h=h)
+        t = min(SLAB, T - r0)
+        x = O.synth_tokens(tseed, t, n, cs, row0=r0, heavy=heavy)
+        if asym:
+            xt = x + O.synth_normal(pseed, t * n, asym, offset=r0 * n).reshape(t, n)
+            O.gram_accumulate(xt, h=h)
+            O.gram_accumulate(x, xt, h=m)
+            del xt
+        else:
+            O.gram_accumulate(x, h=h)
         del x
         if (r0 // SLAB) % 8 == 7:
             print(f"  n={n}: {r0 + SLAB}/{T} tokens, {time.time() - t0:.0f}s", flush=True)
-    return h
+    return (h, m) if asym else h
 
 
 def hessians(spec: dict) -> dict:
@@ -125,6 +143,43 @@ def factor_digest(h64: np.ndarray) -> str:
     return sha(u)
 
 
+def run_config5(chunks: int) -> dict:
+    """Config 5 (Llama-3-70B MLP, asymmetric target): the full-size H~ and M of both inputs, then
+    the first `chunks` row chunks of every matrix (the chunk size of the full run, passed
+    explicitly): rows are quantized in independent chunks, and the permutation and the target
+    W* = ((W M') U^T) U act row by row, so these rows equal the same rows of the full run."""
+    name = "c5"
+    spec = bench.CONFIGS[name]
+    out = {"workload": spec["workload"], "tokens": spec["tokens"], "cfg": spec["cfg"], "nthreads": spec["nthreads"],
+           "inputs": {}, "layers": {}}
+    hs = {}
+    for i, (key, n) in enumerate(spec["inputs"].items()):
+        t0 = time.time()
+        h64, m64 = hessian64(spec, i, n)
+        hs[key] = (h64.astype(np.float32), m64.astype(np.float32))
+        out["inputs"][key] = {"n": n, "h32_sha256": sha(hs[key][0]), "m32_sha256": sha(hs[key][1]),
+                              "h64_sha256": sha(h64), "m64_sha256": sha(m64)}
+        del h64, m64
+        print(f"{key}: H~ and M {n}x{n} in {time.time() - t0:.1f}s", flush=True)
+    cache = O.Cache()
+    for li, (lname, d_out, key) in enumerate(spec["layers"]):
+        n = spec["inputs"][key]
+        rc = bench.rows_per_chunk(spec, d_out)
+        rows = min(d_out, chunks * rc)
+        w = O.synth_normal(bench.weight_seed(li), rows * n, spec["wsigma"]).reshape(rows, n)
+        cfg = O.config(**{**spec["cfg"], "row_chunk": rc})
+        t0 = time.time()
+        q = O.quantize_layer(w, hs[key][0], cfg, m=hs[key][1], hkey=key, cache=cache, nthreads=spec["nthreads"])
+        out["layers"][lname] = {
+            "d_out": d_out, "n": n, "input": key, "rows": rows, "row_chunk": rc,
+            "codes": sha(q.codes), "scales": sha(q.scales), "zeros": sha(q.zeros), "perm": sha(q.perm),
+            "gbits": sha(q.gbits), "rows_stats": {f: q.stats[f] for f in STAT_FIELDS}, "rows_midpoint": q.midpoint,
+        }
+        print(f"{name} {lname} first {rows} of {d_out} rows x {n}: {time.time() - t0:.1f}s "
+              f"loss_final {q.stats['loss_final']:.6e} updates {q.stats['code_updates']}", flush=True)
+    return out
+
+
 def load() -> dict:
     if os.path.exists(OUT):
         with open(OUT) as f:
@@ -154,6 +209,11 @@ def main(argv):
         rec = run_config("c4", hs, midpoints=True)
         rec["inputs"]["mlp_act"]["u32_sha256"] = factor_digest(hs["mlp_act"][0])
         res["configs"]["c4"] = rec
+        save(res)
+    if "c5" in which:
+        rec = run_config5(chunks=int(os.environ.get("C5_CHUNKS", "7")))
+        res = load()  # another run may have written meanwhile
+        res["configs"]["c5"] = rec
         save(res)
 
 

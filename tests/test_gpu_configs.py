@@ -9,10 +9,15 @@ full-size Gram), and compares every matrix's codes, scales, zeros, perm and grou
 digests and its LayerStats with the oracle's (losses within 1e-6 relative, counts exact). A
 mismatching matrix is re-run through the oracle here, which names the first differing element.
 
-Config 5 (Llama-3-70B MLP: n = 28672 H~ and M over 524,288 tokens, asymmetric target) and config
-4's down_proj are checked through size-independent properties: two runs bit-identical, codes on
-the grid, f16-exact positive scales, integer zero points, a permutation, repair never raising the
-loss, and the factor: U upper triangular with a positive diagonal and U^T U H x = x.
+Config 4 (Llama-3-8B layer, 524,288 tokens, n = 4096 and 14336), the headline benchmark, runs
+through bench.LayerStep with its chains concurrent, as bench.py times it, and is compared with the
+oracle's digests in the same way, including each matrix's near-midpoint counts and U of the
+n = 14336 input. The concurrent schedule is also checked on config 2's layer over two steps.
+
+Config 5 (Llama-3-70B MLP: n = 28672 H~ and M over 524,288 tokens, asymmetric target) is checked
+through size-independent properties: two runs bit-identical, codes on the grid, f16-exact positive
+scales, integer zero points, a permutation, repair never raising the loss, and the factor: U upper
+triangular with a positive diagonal and U^T U H x = x.
 """
 import hashlib
 import json
@@ -234,19 +239,37 @@ def test_config5_full_size_properties(ctx):
         h64s[key].free()
 
 
-def test_config4_down_proj_properties(ctx):
-    """Config 4's down_proj (4096 x 14336, INT4 g128, act-order) on its n = 14336 input over
-    524,288 tokens: the largest factorisation of the headline benchmark, checked by properties."""
+def test_config4_layer_matches_the_oracle(ctx):
+    """Config 4 at full size, the headline benchmark's own layer and schedule (bench.LayerStep with
+    the chains concurrent): every input's H (f32 and f64) and every matrix's codes, scales, zeros,
+    perm, gbits, LayerStats and near-midpoint counts equal the oracle's digests, and U of the
+    n = 14336 input through the public upper_chol_of_inverse equals the oracle's U."""
     spec = bench.CONFIGS["c4"]
-    key, li = "mlp_act", 6
-    n = spec["inputs"][key]
-    print(f"[configs] c4 down_proj: H at n={n}, T={spec['tokens']}", flush=True)
-    h32s, _, h64s, _ = device_hessians(ctx, spec, only=[key])
-    runs = []
-    for rep in range(2):
-        ctx.clear_cache()
-        runs.append(quantize(ctx, spec, li, h32s[key], key=key))
-    assert_same_run(runs[0], runs[1], "c4 down_proj")
-    assert_properties(runs[0], spec["cfg"]["bits"], "c4 down_proj")
-    h32s[key].free()
-    h64s[key].free()
+    with open(GOLDEN) as f:
+        gold = json.load(f)["configs"].get("c4")
+    if gold is None:
+        pytest.skip("no config 4 digests recorded (tests/golden/make_config_digests.py c4)")
+    print(f"[configs] c4: {spec['workload']}, T={spec['tokens']}, chains concurrent", flush=True)
+    L = bench.LayerStep(ctx, spec, serial=False)
+    try:
+        stats, wall = L.step()
+        print(f"[configs] c4 step: gram {wall['gram']:.3f}s quantize {wall['quantize']:.3f}s", flush=True)
+        L.free_inputs()
+        for key in spec["inputs"]:
+            g = gold["inputs"][key]
+            assert sha(L.h32s[key].download()) == g["h32_sha256"], f"c4 {key}: H (f32) differs from the oracle's"
+            assert sha(L.h64s[key].download()) == g["h64_sha256"], f"c4 {key}: H (f64) differs from the oracle's"
+        for name, _, _ in spec["layers"]:
+            c, s, z = L.outs[name]
+            perm, gbits = L.perm_gbits[name]
+            st, mid = stats[name]
+            print(f"[configs] c4 {name}: loss_final {st.loss_final:.6e} updates {st.code_updates} near {mid}",
+                  flush=True)
+            compare_with_digests("c4", gold, name, c.download(), s.download(), z.download(), perm, gbits, st, mid)
+        n = spec["inputs"]["mlp_act"]
+        h = L.h64s["mlp_act"].download()
+        h[np.arange(n), np.arange(n)] += 0.01 * np.mean(np.diag(h))
+        u = cdclq.upper_chol_of_inverse(h, n, ctx)
+        assert sha(u) == gold["inputs"]["mlp_act"]["u32_sha256"], "c4 n=14336: U differs from the oracle's"
+    finally:
+        L.free()
