@@ -14,7 +14,9 @@ through bench.LayerStep with its chains concurrent, as bench.py times it, and is
 oracle's digests in the same way, including each matrix's near-midpoint counts and U of the
 n = 14336 input. The concurrent schedule is also checked on config 2's layer over two steps.
 
-Config 5 (Llama-3-70B MLP: n = 28672 H~ and M over 524,288 tokens, asymmetric target) is checked
+Config 5 (Llama-3-70B MLP: n = 28672 H~ and M over 524,288 tokens, asymmetric target): the full-size
+H~ and M and the first row chunks of every matrix against the oracle's digests (the oracle cannot
+run every row of this layer here in reasonable time; chunks are independent), and the whole layer
 through size-independent properties: two runs bit-identical, codes on the grid, f16-exact positive
 scales, integer zero points, a permutation, repair never raising the loss, and the factor: U upper
 triangular with a positive diagonal and U^T U H x = x.
@@ -210,6 +212,45 @@ def test_concurrent_chains_match_the_oracle(ctx):
 
 
 # ---------------------------------------------------------------- config 5 at full size
+def test_config5_first_chunks_match_the_oracle(ctx):
+    """Config 5 (Llama-3-70B MLP, asymmetric target) through bench.LayerStep with its chains
+    concurrent: both inputs' H~ and M (f32 and f64, n = 8192 and 28672, 524,288 tokens) equal the
+    oracle's, and so do the permutation, group widths and the codes, scales and zeros of each
+    matrix's first row chunks (the oracle ran those rows only, with the full run's chunk size: row
+    chunks are independent and the target W* = ((W M') U^T) U is row-wise)."""
+    spec = bench.CONFIGS["c5"]
+    with open(GOLDEN) as f:
+        gold = json.load(f)["configs"].get("c5")
+    if gold is None:
+        pytest.skip("no config 5 digests recorded (tests/golden/make_config_digests.py c5)")
+    print(f"[configs] c5: {spec['workload']}, T={spec['tokens']}, chains concurrent", flush=True)
+    L = bench.LayerStep(ctx, spec, serial=False)
+    try:
+        stats, wall = L.step()
+        print(f"[configs] c5 step: gram {wall['gram']:.3f}s quantize {wall['quantize']:.3f}s", flush=True)
+        L.free_inputs()
+        for key in spec["inputs"]:
+            g = gold["inputs"][key]
+            for label, dev in (("h32", L.h32s[key]), ("m32", L.m32s[key]), ("h64", L.h64s[key]), ("m64", L.m64s[key])):
+                assert sha(dev.download()) == g[f"{label}_sha256"], f"c5 {key}: {label} differs from the oracle's"
+        for name, d_out, key in spec["layers"]:
+            g = gold["layers"][name]
+            rows = g["rows"]
+            assert g["row_chunk"] == bench.rows_per_chunk(spec, d_out)
+            c, s, z = L.outs[name]
+            perm, gbits = L.perm_gbits[name]
+            got = dict(codes=c.download()[:rows], scales=s.download()[:rows], zeros=z.download()[:rows], perm=perm,
+                       gbits=gbits)
+            diff = [f for f in ("codes", "scales", "zeros", "perm", "gbits") if sha(got[f]) != g[f]]
+            st = stats[name][0]
+            print(f"[configs] c5 {name}: first {rows} of {d_out} rows, loss_final {st.loss_final:.6e} "
+                  f"updates {st.code_updates}", flush=True)
+            assert not diff, f"c5 {name}: {diff} of the first {rows} rows differ from the oracle's digests"
+    finally:
+        L.free()
+
+
+
 def test_config5_full_size_properties(ctx):
     """Llama-3-70B MLP: gate_proj 28672 x 8192 and down_proj 8192 x 28672, INT3 g128, passes 6, with
     the asymmetric target from H~ and M accumulated on the device over 524,288 tokens (X with
