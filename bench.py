@@ -322,8 +322,9 @@ def cpu_baseline(spec: dict, cores: int, fetch) -> dict:
 
     `fetch(kind, key_or_name, rows)` returns the workload's own host arrays after the timed region:
     ("h", key) the f32 H, ("m", key) the f32 M, ("w", name, rows) the first rows of a matrix.
-    * Gram: each distinct width accumulates a slab of the config's synthetic tokens; scaled by
-      T / slab (2048-token chunks in sequence, each the same work) per accumulation.
+    * Gram: each distinct width accumulates a slab of synthetic tokens of that width (the work
+      does not depend on the values); scaled by T / slab (2048-token chunks in sequence, each the
+      same work) per accumulation.
     * Factorisation + phase 1 + 2: for each distinct width, the widest-row matrix of that width is
       quantized on one wave of row chunks (one chunk per thread, the reference's chunk size, with
       the step's real H and W rows): secs_prepare is the factorisation, secs_quant the wave of
@@ -363,10 +364,8 @@ def cpu_baseline(spec: dict, cores: int, fetch) -> dict:
         w = fetch("w", name, rows)
         c = O.config(**{**spec["cfg"], "row_chunk": rc})
         if asym:  # the target GEMMs are inside secs_prepare: time the factor on its own
-            hd = h.astype(np.float64)
-            t0 = time.perf_counter()
             q = O.quantize_layer(w, h, c, m=m, hkey=key, nthreads=cores)
-            wall = time.perf_counter() - t0
+            hd = h.astype(np.float64)
             hd[np.arange(n), np.arange(n)] += cfg.damp * np.mean(np.diag(hd))
             t0 = time.perf_counter()
             O.upper_chol_of_inverse(hd)
@@ -380,9 +379,7 @@ def cpu_baseline(spec: dict, cores: int, fetch) -> dict:
                      f"{q.stats['secs_quant']:.2f}s")
         del h, m, w
     fac_full = quant_full = target_full = 0.0
-    fac_widths = spec["inputs"].values() if spec["cfg"].get("skeleton_pct", 0.0) <= 0.0 else \
-        [spec["inputs"][key] for _, _, key in spec["layers"]]
-    for n in fac_widths:
+    for n in factorisations(spec):
         n0 = max(v for v in samples if v <= n) if any(v <= n for v in samples) else max(samples)
         fac_full += samples[n0][0] * (n / n0) ** 3
     for name, d_out, key in spec["layers"]:
@@ -393,7 +390,8 @@ def cpu_baseline(spec: dict, cores: int, fetch) -> dict:
         quant_full += samples[n0][1] * rc * waves * (n / n0) ** 2
         target_full += samples[n0][2] * d_out * (n / n0) ** 2
     total = gram_full + fac_full + quant_full + target_full
-    sample = (f"oracle on {cores} threads of {cpu_model()}, timed in this run on the step's own H and W rows: "
+    sample = (f"oracle on {cores} threads of {cpu_model()}, timed in this run (Gram on synthetic tokens of each "
+              "width; factorisation and row chunks on the step's own H and W rows): "
               + "; ".join(notes) + ". Scaled to the step: Gram by tokens, each matrix by its waves of row chunks "
               "(chunk time linear in rows); factorisations measured at their width"
               + (" (wider ones by n^3)" if any(v > FACTOR_SAMPLE_MAX_N for v in widths) else "")
