@@ -7,10 +7,11 @@ inputs of q/k/v, o, gate/up and down) and 7 quantize_layer calls (INT4, g128, B1
 damp 0.01, repair on with the reference defaults), with the factor cache shared by q/k/v and by
 gate/up as in the reference pipeline. Inputs (X, W) are generated in HBM before the timed region.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4|c1] [--no-cpu-baseline] [--profile-gram]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1|c2|c3|c4|c5] [--serial]
+                    [--no-cpu-baseline] [--profile-gram] [--workload layer|container] [--floor-rows R]
 
 Prints one JSON line (rank 0). The CPU baseline is the C restatement of the reference (oracle/)
-timed on a bounded sample of the same workload on this host and extrapolated (see `sample`).
+timed on bounded samples of the same step on this host and scaled to the step (see `sample`).
 """
 from __future__ import annotations
 
