@@ -549,9 +549,17 @@ int quantize_device(cdclq_ctx* ctx, const float* w, size_t d_out_, size_t n_, co
       HIPCK(hipMemsetAsync(rcnt, 0, (size_t)ng * d_out * 4, st));
       for (int gi = 0; gi < ng; ++gi) {
         const int c0 = gi * g, wd = std::min(c0 + g, n) - c0;
-        CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32, all_tiles ? nullptr : rtiles, all_tiles ? ntile : tcnt[0]));
+        const int* tl0 = all_tiles ? nullptr : rtiles;
+        const int nt0 = all_tiles ? ntile : tcnt[0];
+        // the refit kernel folds the per-panel chains itself where it can (one launch less)
+        const bool fused = refit_folds_chains(wd);
+        if (fused)
+          HIPCK(panel_gemm(st, d_out, wd, n, eb, n, H32 + c0, n, P<float>(ctx->part), tl0, nt0));
+        else
+          CK(grad_gemm(ctx, d_out, n, c0, wd, eb, H32, tl0, nt0));
         HIPCK(refit_group(st, d_out, n, ng, g, gi, rc, P<float>(ctx->G), H32, codes, scales, zeros, wq, eb,
-                          active, rlog + (size_t)gi * d_out, rcnt + (size_t)gi * d_out));
+                          active, rlog + (size_t)gi * d_out, rcnt + (size_t)gi * d_out,
+                          fused ? P<float>(ctx->part) : nullptr, fused ? (n + 255) / 256 : 0));
       }
       return CDCLQ_OK;
     };

@@ -717,7 +717,8 @@ __global__ __launch_bounds__(256) void k_refit_mfma(int rows, int n, int ng, int
                                                     const uint8_t* __restrict__ codes, float* __restrict__ scales,
                                                     const float* __restrict__ zeros, float* __restrict__ wq,
                                                     float* __restrict__ e, const uint8_t* __restrict__ active,
-                                                    double* __restrict__ dlog, uint32_t* __restrict__ dcnt) {
+                                                    double* __restrict__ dlog, uint32_t* __restrict__ dcnt,
+                                                    const float* __restrict__ P, int np) {
   // H_CC (zero outside wd x wd), then the products: PH = S[0 ..], PG = S[RF_ROWS * RF_PS ..]
   __shared__ float S[2 * RF_ROWS * RF_PS > 128 * 128 ? 2 * RF_ROWS * RF_PS : 128 * 128];
   __shared__ uint32_t CB[RF_ROWS * RF_CS / 4];
@@ -830,10 +831,41 @@ __global__ __launch_bounds__(256) void k_refit_mfma(int rows, int n, int ng, int
   {  // u_k * g_k: all of a thread's G loads in flight at once (clamped addresses)
     constexpr int PER = RF_ROWS * 128 / 256;
     float gv[PER];
+    if (P) {
+      // G folded here from the gradient GEMM's per-panel chains (P[p][row][col], rows x wd per
+      // panel), in panel order from 0 as k_fold does: C = fma(1, P_p, C). FB panels of every
+      // element are loaded at once; the last batch is predicated. Rows of tiles the GEMM skipped
+      // (no active chunk) read stale chains that only reach their own, unused, products.
+      constexpr int FB = PER <= 8 ? 8 : (PER <= 16 ? 4 : 2);
+      const long pstride = (long)rows * wd;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int x = tid + 256 * i, rl = x >> 7, k = x & 127;
-      gv[i] = G[(long)min(r0 + rl, rows - 1) * wd + min(k, wd - 1)];
+      for (int i = 0; i < PER; ++i) gv[i] = 0.0f;
+      for (int p = 0; p < np; p += FB) {
+        float v[FB][PER];
+#pragma unroll
+        for (int u = 0; u < FB; ++u) {
+          const long po = (long)min(p + u, np - 1) * pstride;
+#pragma unroll
+          for (int i = 0; i < PER; ++i) {
+            const int x = tid + 256 * i, rl = x >> 7, k = x & 127;
+            v[u][i] = __builtin_nontemporal_load(P + po + (long)min(r0 + rl, rows - 1) * wd + min(k, wd - 1));
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before the first add
+#pragma unroll
+        for (int u = 0; u < FB; ++u) {
+          if (p + u < np) {  // uniform
+#pragma unroll
+            for (int i = 0; i < PER; ++i) gv[i] = __builtin_fmaf(1.0f, v[u][i], gv[i]);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int x = tid + 256 * i, rl = x >> 7, k = x & 127;
+        gv[i] = G[(long)min(r0 + rl, rows - 1) * wd + min(k, wd - 1)];
+      }
     }
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -1342,10 +1374,13 @@ hipError_t fold_panels(hipStream_t st, int m, int wd, int np, const float* P, fl
   return hipGetLastError();
 }
 
+bool refit_folds_chains(int wd) { return wd > 0 && wd <= 128; }  // the matrix-core k_refit_mfma
+
 hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, int rc, const float* G,
                        const float* h32, const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
-                       const uint8_t* active, double* dlog, uint32_t* dcnt) {
+                       const uint8_t* active, double* dlog, uint32_t* dcnt, const float* P, int np) {
   const int wd = std::min(gi * g + g, n) - gi * g;
+  if (P && !refit_folds_chains(wd)) return hipErrorInvalidValue;
   if (wd <= 128) {
     // the smallest workgroups (shortest chains) whose count still fits two per CU, so that all
     // rows are resident in one round; 64-row ones beyond that
@@ -1354,13 +1389,13 @@ hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, i
     if (err != hipSuccess) return err;
     if ((rows + 15) / 16 <= 2 * cus)
       hipLaunchKernelGGL(k_refit_mfma<16>, dim3((rows + 15) / 16), dim3(256), 0, st, rows, n, ng, g, gi, rc, G, h32,
-                         codes, scales, zeros, wq, e, active, dlog, dcnt);
+                         codes, scales, zeros, wq, e, active, dlog, dcnt, P, np);
     else if ((rows + 31) / 32 <= 2 * cus)
       hipLaunchKernelGGL(k_refit_mfma<32>, dim3((rows + 31) / 32), dim3(256), 0, st, rows, n, ng, g, gi, rc, G, h32,
-                         codes, scales, zeros, wq, e, active, dlog, dcnt);
+                         codes, scales, zeros, wq, e, active, dlog, dcnt, P, np);
     else
       hipLaunchKernelGGL(k_refit_mfma<64>, dim3((rows + 63) / 64), dim3(256), 0, st, rows, n, ng, g, gi, rc, G, h32,
-                         codes, scales, zeros, wq, e, active, dlog, dcnt);
+                         codes, scales, zeros, wq, e, active, dlog, dcnt, P, np);
     return hipGetLastError();
   }
 #define REFIT_CASE(N)                                                                                                  \

@@ -123,9 +123,13 @@ bool chain_gemm_tiles_ok(int m, int n, int k, const float* A, long lda, const fl
 hipError_t chain_gemm_tiles(hipStream_t st, int m, int n, int k, const float* A, long lda, const float* B, long ldb,
                             float* C, long ldc, int tri);
 hipError_t transpose_f32(hipStream_t st, int n, const float* src, float* dst);
+// Scale refit of group gi from its gradient: G (rows x wd), or, with P, the np per-panel chains of
+// panel_gemm (P[p][rows][wd]) folded in panel order by the kernel itself (no separate fold
+// launch); refit_folds_chains(wd) says whether that form is available.
 hipError_t refit_group(hipStream_t st, int rows, int n, int ng, int g, int gi, int rc, const float* G,
                        const float* h32, const uint8_t* codes, float* scales, const float* zeros, float* wq, float* e,
-                       const uint8_t* active, double* dlog, uint32_t* dcnt);
+                       const uint8_t* active, double* dlog, uint32_t* dcnt, const float* P = nullptr, int np = 0);
+bool refit_folds_chains(int wd);
 // Coordinate descent over one sub-block. The gradient comes from G, or, when P is non-null, from
 // the np per-panel chains of panel_gemm (P[p][rows][wd]), folded in panel order by the kernel
 // itself (no separate fold launch); cd_folds_chains(wd) says whether that form is available.
