@@ -834,8 +834,8 @@ __global__ __launch_bounds__(256) void k_refit_mfma(int rows, int n, int ng, int
     if (P) {
       // G folded here from the gradient GEMM's per-panel chains (P[p][row][col], rows x wd per
       // panel), in panel order from 0 as k_fold does: C = fma(1, P_p, C). FB panels of every
-      // element are loaded at once; the last batch is predicated. Rows of tiles the GEMM skipped
-      // (no active chunk) read stale chains that only reach their own, unused, products.
+      // element are loaded at once; the last batch is predicated. A workgroup that got here holds
+      // a live row, and its 16-64 rows lie in one 128-row tile, which the GEMM therefore computed.
       constexpr int FB = PER <= 8 ? 8 : (PER <= 16 ? 4 : 2);
       const long pstride = (long)rows * wd;
 #pragma unroll
