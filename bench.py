@@ -383,12 +383,14 @@ def cpu_baseline(spec: dict, cores: int, fetch) -> dict:
     for n in factorisations(spec):
         n0 = max(v for v in samples if v <= n) if any(v <= n for v in samples) else max(samples)
         fac_full += samples[n0][0] * (n / n0) ** 3
+    per_matrix = {}
     for name, d_out, key in spec["layers"]:
         n = spec["inputs"][key]
         n0 = n if n in samples else max(samples)
         rc = rows_per_chunk(spec, d_out)
         waves = -(-(-(-d_out // rc)) // cores)
-        quant_full += samples[n0][1] * rc * waves * (n / n0) ** 2
+        per_matrix[name] = samples[n0][1] * rc * waves * (n / n0) ** 2
+        quant_full += per_matrix[name]
         target_full += samples[n0][2] * d_out * (n / n0) ** 2
     total = gram_full + fac_full + quant_full + target_full
     sample = (f"oracle on {cores} threads of {cpu_model()}, timed in this run (Gram on synthetic tokens of each "
@@ -397,9 +399,49 @@ def cpu_baseline(spec: dict, cores: int, fetch) -> dict:
               "(chunk time linear in rows); factorisations measured at their width"
               + (" (wider ones by n^3)" if any(v > FACTOR_SAMPLE_MAX_N for v in widths) else "")
               + ". Repair passes are data-dependent per chunk, so the waves are a model of the full step.")
-    return {"value": round(total, 2), "unit": "s/layer", "cores": cores, "kind": "port", "cpu": cpu_model(),
-            "sample": sample, "phases_s": {"gram": round(gram_full, 2), "factor": round(fac_full, 2),
-                                           "quant": round(quant_full, 2), "target": round(target_full, 2)}}
+    out = {"value": round(total, 2), "unit": "s/layer", "cores": cores, "kind": "port", "cpu": cpu_model(),
+           "sample": sample}
+    chk = recorded_quant_check(spec)
+    if chk is not None:
+        out["value_with_quant_check"] = round(total - quant_full * (1.0 - chk), 2)
+        out["quant_check"] = (f"whole matrices measured {chk} of the chunk-wave model for phase 1 + 2 "
+                              f"(profiles/cpu_baseline_{spec.get('name', '')}.md)")
+    return {**out, "phases_s": {"gram": round(gram_full, 2), "factor": round(fac_full, 2),
+                                           "quant": round(quant_full, 2), "target": round(target_full, 2)},
+            "quant_s_per_matrix": {k: round(v, 2) for k, v in per_matrix.items()}}
+
+
+def recorded_quant_check(spec: dict):
+    """The measured / modelled phase 1 + 2 ratio recorded by `bench.py --cpu-validate` runs in
+    profiles/cpu_baseline_<config>.md (None if not recorded)."""
+    path = os.path.join(ROOT, "profiles", f"cpu_baseline_{spec.get('name', '')}.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("quant_measured_over_model:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def cpu_validate(spec: dict, cores: int, fetch, name: str) -> dict:
+    """Checks the CPU baseline's chunk-wave model on one whole matrix: the oracle quantizes every
+    row of `name` (its own H and W from the step, the config's row chunks) and its measured phase
+    1 + 2 time is set beside the model's prediction for that matrix."""
+    import oracle as O
+
+    model = cpu_baseline(spec, cores, fetch)
+    _, d_out, key = next(l for l in spec["layers"] if l[0] == name)
+    h = fetch("h", key)
+    w = fetch("w", name, d_out)
+    cfg = O.config(**{**spec["cfg"], "row_chunk": rows_per_chunk(spec, d_out)})
+    q = O.quantize_layer(w, h, cfg, hkey=key, nthreads=cores)
+    pred = model["quant_s_per_matrix"][name]
+    return {"cpu_validate": name, "threads": cores, "cpu": cpu_model(), "rows": d_out, "n": spec["inputs"][key],
+            "measured_quant_s": round(q.stats["secs_quant"], 2), "predicted_quant_s": round(pred, 2),
+            "measured_over_predicted": round(q.stats["secs_quant"] / pred, 3),
+            "measured_factor_s": round(q.stats["secs_prepare"], 2), "model": model}
 
 
 def recorded_traffic(summary: str):
@@ -649,6 +691,9 @@ def main():
     ap.add_argument("--serial", action="store_true",
                     help="quantize the layer's matrices one after another on one context (default: the chains "
                          "of matrices that share an input run concurrently, one context each)")
+    ap.add_argument("--cpu-validate", default="",
+                    help="after the timed steps, quantize every row of this matrix on the CPU oracle and print "
+                         "its time beside the CPU baseline model's prediction (instead of the bench line)")
     ap.add_argument("--floor-rows", type=int, default=0,
                     help="latency-floor run (under a kernel trace): the config's matrices cut to their first "
                          "FLOOR_ROWS rows, same inputs and settings, one untimed step; prints the phase times")
@@ -661,7 +706,7 @@ def main():
 
     import cdclq
 
-    spec = CONFIGS[args.config]
+    spec = dict(CONFIGS[args.config], name=args.config)
     if args.floor_rows > 0:
         # the same matrices with fewer rows in flight: each sweep launch then runs its rows'
         # dependent chains with no other waves on their SIMDs
@@ -771,6 +816,10 @@ def main():
             return (L.h32s if kind == "h" else L.m32s)[what].download()
 
         L.free_inputs()
+        if args.cpu_validate:
+            print(json.dumps(cpu_validate(spec, cores, fetch, args.cpu_validate)), flush=True)
+            ctx.close()
+            return
         result["cpu_baseline"] = cpu_baseline(spec, cores, fetch)
     print(json.dumps(result), flush=True)
     ctx.close()
