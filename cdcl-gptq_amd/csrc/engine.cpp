@@ -151,25 +151,49 @@ int factor(cdclq_ctx* ctx, int n, double* a, double* y, float* u) {
   }
   HIPCK(fill_zero_f64(st, y, (size_t)n * n));
   HIPCK(trinv_diag(st, n, a, y, status));
-  if (n > NB) {
+  if (n > NB && n % 2 == 0) {
+    // Triangular inverse, right-looking (src/linalg.rs:284-346 with the same per-element
+    // operations): block row s needs t_s = L[s:e, 0:s] Y[0:s, 0:s], i.e. per element the chains of
+    // the KC panels [0, 256), [256, 512), ... of k < s folded in order, then Y[s:e, 0:s] =
+    // -Y_ss t_s. All block rows' t live in T (zeroed: the fold's first C' is 0), and as soon as
+    // Y's rows [256 p, 256 p + 256) are final, one GEMM folds panel p's chains into every block
+    // row that has the whole panel (block start >= 256 (p + 1)); a block row then folds only its
+    // last, partial panel [256 floor(s / 256), s) itself. Every element of t receives its panels'
+    // chains in panel order, as in the reference's pgemm_f64. Y[k][j] = 0 for k < j, so the
+    // columns past a panel's last row add +0 chains to a +0 accumulator and are skipped.
+    CK(ensure(ctx, ctx->tbuf, (size_t)n * n * sizeof(double)));
+    double* T = P<double>(ctx->tbuf);
+    HIPCK(fill_zero_f64(st, T + (size_t)NB * n, (size_t)(n - NB) * n));
+    int done = 0;  // panels folded into every block row that has them
+    for (int s = NB; s < n; s += NB) {
+      const int e = std::min(s + NB, n), w = e - s, full = s / CDCLQ_KC, kp = full * CDCLQ_KC;
+      for (; done < full; ++done) {
+        const int k0 = done * CDCLQ_KC, c1 = k0 + CDCLQ_KC;
+        const int r0 = (c1 + NB - 1) / NB * NB;  // first block row holding the whole panel
+        HIPCK(inv_acc(st, n - r0, c1, CDCLQ_KC, a + (long)r0 * n + k0, n, y + (long)k0 * n, n, T + (long)r0 * n, n));
+      }
+      if (s > kp)  // the last, partial panel [kp, s)
+        HIPCK(inv_acc(st, w, s, s - kp, a + (long)s * n + kp, n, y + (long)kp * n, n, T + (long)s * n, n));
+      if (inv_gemm_eligible(w, s, w, y + (long)s * n + s, n, T + (long)s * n, n))
+        HIPCK(inv_gemm(st, w, s, w, -1.0, y + (long)s * n + s, n, T + (long)s * n, n, y + (long)s * n, n, nullptr,
+                       false));
+      else
+        HIPCK(gemm_chain<double>(st, w, s, w, -1.0, 0, y + (long)s * n + s, n, 1, T + (long)s * n, n, 1,
+                                 y + (long)s * n, n, 1, false, (double*)nullptr));
+    }
+  } else if (n > NB) {  // odd n (rows not 16-byte aligned): per block row, panels split and folded
     CK(ensure(ctx, ctx->tbuf, (size_t)NB * n * sizeof(double)));
     CK(ensure(ctx, ctx->tpart, gemm_partials_elems(NB, n, n) * sizeof(double)));
-  }
-  for (int s = NB; s < n; s += NB) {
-    const int e = std::min(s + NB, n), w = e - s;
-    double* t = P<double>(ctx->tbuf);
-    // t = L[s:e, 0:s] Y[0:s, 0:s]; Y[s:e, 0:s] = -Y_ss t  (src/linalg.rs:307-343)
-    double* tp = s > 256 ? P<double>(ctx->tpart) : nullptr;
-    if (inv_gemm_eligible(w, s, s, a + (long)s * n, n, y, n))
-      HIPCK(inv_gemm(st, w, s, s, 1.0, a + (long)s * n, n, y, n, t, s, tp, /*b_lower_tri=*/true));
-    else
+    for (int s = NB; s < n; s += NB) {
+      const int e = std::min(s + NB, n), w = e - s;
+      double* t = P<double>(ctx->tbuf);
+      // t = L[s:e, 0:s] Y[0:s, 0:s]; Y[s:e, 0:s] = -Y_ss t  (src/linalg.rs:307-343)
+      double* tp = s > 256 ? P<double>(ctx->tpart) : nullptr;
       HIPCK(gemm_chain<double>(st, w, s, s, 1.0, 0, a + (long)s * n, n, 1, y, n, 1, t, s, 1, false, tp,
                                /*b_lower_tri=*/true));
-    if (inv_gemm_eligible(w, s, w, y + (long)s * n + s, n, t, s))
-      HIPCK(inv_gemm(st, w, s, w, -1.0, y + (long)s * n + s, n, t, s, y + (long)s * n, n, nullptr, false));
-    else
       HIPCK(gemm_chain<double>(st, w, s, w, -1.0, 0, y + (long)s * n + s, n, 1, t, s, 1, y + (long)s * n, n, 1, false,
                                (double*)nullptr));
+    }
   }
   HIPCK(scatter_u(st, n, y, u));
   return CDCLQ_OK;
@@ -853,9 +877,10 @@ int cdclq_ctx_create(int device, cdclq_ctx** out) {
       hipStreamCreateWithFlags(&ctx->st2, hipStreamNonBlocking) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->ev_col, hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->ev_panel, hipEventDisableTiming) != hipSuccess) {
-    if (ctx->ev_col) (void)hipEventDestroy(ctx->ev_col);
-    if (ctx->st2) (void)hipStreamDestroy(ctx->st2);
-    if (ctx->st) (void)hipStreamDestroy(ctx->st);
+    for (hipEvent_t e : {ctx->ev_col, ctx->ev_panel})
+      if (e) (void)hipEventDestroy(e);
+    for (hipStream_t q : {ctx->st2, ctx->st})
+      if (q) (void)hipStreamDestroy(q);
     delete ctx;
     return CDCLQ_DEVICE;
   }

@@ -7,7 +7,7 @@
 //   * trailing update: a_ij = fma(-1, chain_t(p_it p_jt), a_ij) per block (k_gemm.hip, lower tiles);
 //   * inverse of every diagonal block by columns (mul/add roundings), then per block row two
 //     chained GEMMs (k_gemm.hip).
-// The panel solve runs one wave per row with the block's columns spread over lanes: column t is
+// The panel solve gives a row four lanes (its columns interleaved over them): column t is
 // finalised at step t and immediately subtracted from every later column, which performs the
 // reference's per-element subtraction sequence in the same order.
 #include "cdclq_dev.h"
@@ -17,13 +17,6 @@ namespace cdclq {
 namespace {
 
 constexpr int NBC = 96;  // src/linalg.rs:202, :285
-
-__device__ __forceinline__ double readlane_f64(double v, int lane) {
-  const long long b = __double_as_longlong(v);
-  const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffLL), lane);
-  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
-  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
-}
 
 // hp = perm(H) in f64, dead diagonal -> 1, + damp on the diagonal; h32 = (f32)hp; a = flip(hp).
 __global__ __launch_bounds__(256) void k_build_flipped(int n, const float* __restrict__ h,
@@ -165,78 +158,100 @@ __global__ __launch_bounds__(64) void k_chol_diag(int n, double* __restrict__ a,
   }
 }
 
-// Panel solve X L_kk^T = A_panel for all rows below the block (src/linalg.rs:233-241). One wave
-// advances PANEL_RPW rows together (columns over lanes), so the LDS reads of L and the long
-// divisions of the rows overlap. The strict lower part of L is staged transposed with zeros on
-// and above the diagonal (the diagonal separately), so step t applies x_t to every lane without
-// predication: lanes at or before t, already final, take -x_t * 0 into a copy that is no longer
-// read; each final value is kept in f0 / f1 when its step comes. Columns 0..63 (held in s0) and
-// 64.. (s1) run as two loops, so the lane holding column t is known without a select.
-constexpr int PANEL_RPW = 4;  // rows per wave
+// Panel solve X L_kk^T = A_panel for all rows below the block (src/linalg.rs:233-241): for each
+// row, x_j = (a_j - sum_{t<j} x_t l_jt) / l_jj, every product and difference rounded separately,
+// t ascending. Four lanes per row, 16 rows per wavefront: lane 4 r + g holds columns
+// j = 4 q + g (q < 24) of row r, so the columns still open at any step are spread evenly over the
+// row's lanes. Step t: the lane holding column t divides it by l_tt (all lanes run the division;
+// the others' quotients are discarded), a quad permutation hands the quotient to the row's four
+// lanes, and each lane subtracts x_t l_jt from its columns j > t. Column j thus receives the
+// reference's subtractions in the reference's order (right-looking instead of a dot product per
+// column), and finished columns are never touched again. The lower part of L_kk is staged in LDS
+// as LP[t][g][q] = l_{4q+g, t} (zero on and above the diagonal and past the block), so a lane reads
+// the factors of its columns for step t as consecutive pairs; the diagonal is staged separately.
+constexpr int PQ = NBC / 4;  // columns per lane
+
+template <int C>
+__device__ __forceinline__ double quad_bcast(double v) {  // lane 4 r + C's value to lanes 4 r .. 4 r + 3
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_mov_dpp((int)(b & 0xffffffffLL), C * 85, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_mov_dpp((int)(b >> 32), C * 85, 0xf, 0xf, false);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// Step T of the panel solve for one lane (see k_chol_panel); templated on T so that every index
+// into the lane's columns is a constant. On entry `xo` is column T divided by its pivot (valid in
+// the lanes holding column T), `cur` this step's factors l_{4q+g, T} (q >= T / 4) and `dn` the
+// next pivot l_{T+1, T+1}, read from LDS a step ahead so that their latency hides behind the
+// previous step. The step finalises column T, updates column T + 1 first and starts its division,
+// so that the division's latency overlaps the step's other updates (a division started for a
+// column past the block, T + 1 = kb, divides by the pivot 1 staged there and is never used).
+template <int T>
+__device__ __forceinline__ void chol_panel_step(double (&s)[PQ], const double (&cur)[PQ], double xo, double dn,
+                                                int g, int kb, const double* lp0, const double* dg) {
+  constexpr int qt = T >> 2, gt = T & 3, T1 = T + 1, q1 = T1 >> 2;
+  if (T >= kb) return;  // uniform; a real branch, which also bounds the scheduler's reach
+  double nxt[PQ], dn2 = 1.0;
+  if constexpr (T1 < NBC) {
+    const double* lp = lp0 + (T1 * 4 + g) * PQ;  // LP[T + 1][g][.]
+#pragma unroll
+    for (int q = q1; q < PQ; ++q) nxt[q] = lp[q];
+    if constexpr (T1 + 1 < NBC) dn2 = dg[T1 + 1];
+  }
+  const double x = quad_bcast<gt>(xo);
+  double up = s[qt] - x * cur[qt];
+  asm volatile("" : "+v"(up));  // computed in every lane, so that the select below is no branch
+  const double keep = s[qt];
+  const double upd = g > gt ? up : keep;
+  s[qt] = g == gt ? xo : upd;
+  if constexpr (T1 < NBC) {
+    if constexpr (q1 != qt) s[q1] = s[q1] - x * cur[q1];
+    double xo1 = s[q1] / dn;
+    asm volatile("" : "+v"(xo1));  // the division starts here, before the step's other updates
+#pragma unroll
+    for (int q = q1 + 1; q < PQ; ++q) s[q] = s[q] - x * cur[q];
+    chol_panel_step<T1>(s, nxt, xo1, dn2, g, kb, lp0, dg);
+  }
+}
+
 __global__ __launch_bounds__(256) void k_chol_panel(int n, double* __restrict__ a, int k, int kb,
                                                     const int* status) {
-  __shared__ double LT[NBC][NBC + 1];  // LT[t][j] = L[j][t] for t < j < kb, else 0
-  __shared__ double dg[NBC];           // L[t][t]
+  __shared__ double LP[NBC][4][PQ];
+  __shared__ double dg[NBC];
   if (*status) return;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  {  // stage the block with all of a thread's loads in flight at once
+  {  // stage the block with all of a thread's loads in flight at once (clamped addresses)
     constexpr int PER = NBC * NBC / 256;
     double v[PER];
 #pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int e = tid + 256 * q, j = e / NBC, t = e % NBC;
-      v[q] = a[(long)(k + min(j, kb - 1)) * n + k + min(t, kb - 1)];
+    for (int e = 0; e < PER; ++e) {
+      const int x = tid + 256 * e, j = x / NBC, t = x % NBC;
+      v[e] = a[(long)(k + min(j, kb - 1)) * n + k + min(t, kb - 1)];
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int e = tid + 256 * q, j = e / NBC, t = e % NBC;
-      LT[t][j] = (t < j && j < kb) ? v[q] : 0.0;
-      if (t == j) dg[t] = v[q];
+    for (int e = 0; e < PER; ++e) {
+      const int x = tid + 256 * e, j = x / NBC, t = x % NBC;
+      LP[t][j & 3][j >> 2] = (t < j && j < kb) ? v[e] : 0.0;
+      if (t == j) dg[t] = t < kb ? v[e] : 1.0;
     }
   }
   __syncthreads();
-  const int kend = k + kb;
-  const int i0 = kend + (blockIdx.x * 4 + wv) * PANEL_RPW;
-  double s0[PANEL_RPW], s1[PANEL_RPW], f0[PANEL_RPW], f1[PANEL_RPW];
+  const int g = lane & 3;
+  const int row = k + kb + (blockIdx.x * 4 + wv) * 16 + (lane >> 2);
+  const double* src = a + (long)min(row, n - 1) * n + k;  // rows past the end: computed, never stored
+  double s[PQ];
 #pragma unroll
-  for (int q = 0; q < PANEL_RPW; ++q) {
-    const int i = min(i0 + q, n - 1);  // rows past the end are computed but never stored
-    const double* row = a + (long)i * n + k;
-    s0[q] = (lane < kb) ? row[lane] : 0.0;
-    s1[q] = (lane + 64 < kb) ? row[lane + 64] : 0.0;
-    f0[q] = 0.0;
-    f1[q] = 0.0;
-  }
-  const int kb0 = min(kb, 64);
-  for (int t = 0; t < kb0; ++t) {  // column t in s0 (lane t)
-    const double ltt = dg[t];
-    const double l0 = LT[t][lane], l1 = (lane + 64 < NBC) ? LT[t][lane + 64] : 0.0;
+  for (int q = 0; q < PQ; ++q) s[q] = src[min(4 * q + g, kb - 1)];
+  double f0[PQ];
 #pragma unroll
-    for (int q = 0; q < PANEL_RPW; ++q) {
-      const double xt = readlane_f64(s0[q], t) / ltt;
-      f0[q] = (lane == t) ? xt : f0[q];
-      s0[q] = s0[q] - xt * l0;
-      s1[q] = s1[q] - xt * l1;
-    }
-  }
-  for (int t = 64; t < kb; ++t) {  // column t in s1 (lane t - 64); columns 0..63 are final
-    const double ltt = dg[t];
-    const double l1 = (lane + 64 < NBC) ? LT[t][lane + 64] : 0.0;
+  for (int q = 0; q < PQ; ++q) f0[q] = LP[0][g][q];
+  chol_panel_step<0>(s, f0, s[0] / dg[0], dg[1], g, kb, &LP[0][0][0], dg);
+  if (row < n) {
+    double* dst = a + (long)row * n + k;
 #pragma unroll
-    for (int q = 0; q < PANEL_RPW; ++q) {
-      const double xt = readlane_f64(s1[q], t - 64) / ltt;
-      f1[q] = (lane + 64 == t) ? xt : f1[q];
-      s1[q] = s1[q] - xt * l1;
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < PANEL_RPW; ++q) {
-    const int i = i0 + q;
-    if (i >= n) break;
-    double* row = a + (long)i * n + k;
-    if (lane < kb) row[lane] = f0[q];
-    if (lane + 64 < kb) row[lane + 64] = f1[q];
+    for (int q = 0; q < PQ; ++q)
+      if (4 * q + g < kb) dst[4 * q + g] = s[q];
   }
 }
 
@@ -301,7 +316,7 @@ hipError_t chol_diag(hipStream_t st, int n, double* a, int k, int kb, int* statu
 hipError_t chol_panel(hipStream_t st, int n, double* a, int k, int kb, const int* status) {
   const int rows = n - (k + kb);
   if (rows <= 0) return hipSuccess;
-  const int per_wg = 4 * PANEL_RPW;
+  const int per_wg = 64;  // 4 wavefronts of 16 rows
   hipLaunchKernelGGL(k_chol_panel, dim3((rows + per_wg - 1) / per_wg), dim3(256), 0, st, n, a, k, kb, status);
   return hipGetLastError();
 }

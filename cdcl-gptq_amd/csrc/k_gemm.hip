@@ -644,6 +644,27 @@ hipError_t inv_gemm(hipStream_t st, int m, int n, int k, double alpha, const dou
   return hipGetLastError();
 }
 
+bool inv_acc_eligible(int m, int n, int k, const double* A, long lda, const double* B, long ldb) {
+  return m > 0 && n >= 2 && n % 2 == 0 && k > 0 && k <= CDCLQ_KC && k % DMK == 0 && aligned16(A) && lda % 2 == 0 &&
+         aligned16(B) && ldb % 2 == 0;
+}
+
+hipError_t inv_acc(hipStream_t st, int m, int n, int k, const double* A, long lda, const double* B, long ldb,
+                   double* C, long ldc) {
+  if (m <= 0 || n <= 0 || k <= 0) return hipSuccess;
+  if (!inv_acc_eligible(m, n, k, A, lda, B, ldb)) return hipErrorInvalidValue;
+  if (m > 96) {  // the rows below a panel: 128-row tiles
+    const dim3 grid((n + DMN - 1) / DMN, (m + 127) / 128, 1);
+    hipLaunchKernelGGL((k_dmm<128, false, false>), grid, dim3(512), 0, st, m, n, k, 1.0, 1.0, A, lda, B, ldb, C, ldc,
+                       (double*)nullptr, CDCLQ_KC, 0, 0);
+  } else {  // one block row
+    const dim3 grid((n + DMN - 1) / DMN, 1, 1);
+    hipLaunchKernelGGL((k_dmm<96, false, false>), grid, dim3(384), 0, st, m, n, k, 1.0, 1.0, A, lda, B, ldb, C, ldc,
+                       (double*)nullptr, CDCLQ_KC, 0, 0);
+  }
+  return hipGetLastError();
+}
+
 template hipError_t gemm_chain<float>(hipStream_t, int, int, int, float, float, const float*, long, long, const float*,
                                       long, long, float*, long, long, bool, float*, bool);
 template hipError_t gemm_chain<double>(hipStream_t, int, int, int, double, double, const double*, long, long,

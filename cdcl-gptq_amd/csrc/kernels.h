@@ -34,6 +34,14 @@ bool inv_gemm_eligible(int m, int n, int k, const double* A, long lda, const dou
 hipError_t inv_gemm(hipStream_t st, int m, int n, int k, double alpha, const double* A, long lda, const double* B,
                     long ldb, double* C, long ldc, double* partials, bool b_lower_tri);
 
+// C = fma(1, chain, C) for one k range of at most one KC panel (A along k, B along j): a panel's
+// contribution to the triangular inverse's block-row products, applied right-looking to every
+// block row below it, or a block row's last, partial panel (src/linalg.rs:307-321).
+// inv_acc_eligible lists the requirements.
+bool inv_acc_eligible(int m, int n, int k, const double* A, long lda, const double* B, long ldb);
+hipError_t inv_acc(hipStream_t st, int m, int n, int k, const double* A, long lda, const double* B, long ldb,
+                   double* C, long ldc);
+
 // ---- k_gram.hip: H (n x n, f64) += X^T Y over 2048-token chunks on the matrix cores.
 struct GramJob {
   const float* x;  // t x n, token-major

@@ -248,10 +248,12 @@ def test_gemm_bitexact(ctx, dt, m, k, n, alpha, beta, ta, tb):
 
 
 # ---------------------------------------------------------------- U
-@pytest.mark.parametrize("n", [1, 5, 96, 150, 200, 400, 700, 2700])
+@pytest.mark.parametrize("n", [1, 5, 96, 150, 151, 200, 400, 700, 777, 2700])
 def test_upper_chol_bitexact(ctx, n):
-    """n = 2700 puts 9 to 11 KC = 256 panels into the inverse's chain GEMMs (k up to n), so the
-    ordered panel fold runs both its 8-panel loop and its remainder."""
+    """Even n runs the right-looking inverse (a panel's chains folded into every later block row
+    once its rows of Y are final, each block row's partial last panel on its own); n = 2700 gives
+    10 full panels and a 12-row last block. Odd n (151, 777: rows not 16-byte aligned) runs the
+    per-block-row chain GEMMs with their panels split and folded in order."""
     h = rand_spd(n, n + 2) if n <= 700 else _spd_fast(n, n + 2)
     ug = cdclq.upper_chol_of_inverse(h, n, ctx)
     uo = O.upper_chol_of_inverse(h)
