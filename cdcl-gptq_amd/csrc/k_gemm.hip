@@ -605,7 +605,7 @@ bool aligned16(const void* p) { return (uintptr_t)p % 16 == 0; }
 
 hipError_t chol_update(hipStream_t st, int m, int n, int k, const double* P, long ldp, double* C, long ldc) {
   if (m <= 0 || n <= 0 || k <= 0) return hipSuccess;
-  if (n >= 512 && m >= 2 && k % DMK == 0 && aligned16(P) && ldp % 2 == 0) {  // the bulk passes
+  if (n >= 64 && m >= 2 && k % DMK == 0 && aligned16(P) && ldp % 2 == 0) {  // the pipelined 128 x 128 tiles
     const dim3 grid((n + DMN - 1) / DMN, (m + 127) / 128, 1);
     hipLaunchKernelGGL((k_dmm<128, true, false>), grid, dim3(512), 0, st, m, n, k, -1.0, 1.0, P, ldp, P, ldp, C,
                        ldc, (double*)nullptr, 96, 1, 0);
