@@ -989,10 +989,11 @@ __device__ __forceinline__ void fold_chains(const float* __restrict__ src, long 
   for (int s = 0; s < NPL; ++s) gg[s] = s * 64 + lane < wd ? acc[s] : 0.0f;
 }
 
-template <int NPL>
+template <int NPL, int FBW = 0>
 // The 64-column form asks for 8 wavefronts per SIMD: the unrolled panel addresses of its fold would
-// otherwise take enough scalar registers to cap it at 7.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NPL == 1 ? 8 : 1))) void k_cd(
+// otherwise take enough scalar registers to cap it at 7. FBW (64-column form only) widens the
+// fold's batches to FBW panels for gradients of many panels, at 6 wavefronts per SIMD.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NPL == 1 ? (FBW ? 6 : 8) : 1))) void k_cd(
     int rows, int n, int ng, int g, int c0, int wd, int sb, int nsb, int rc, int sweeps, const float* __restrict__ G,
     const float* __restrict__ h32, const uint8_t* __restrict__ gbits, const float* __restrict__ scales,
     const float* __restrict__ zeros, uint8_t* __restrict__ codes, float* __restrict__ wq, float* __restrict__ e,
@@ -1041,7 +1042,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NPL == 1 ? 
       gb[s] = gbits[gi];
     }
     if (P) {
-      fold_chains<NPL, (NPL <= 2 ? 16 / NPL : 2)>(P + (long)r * wd, (long)rows * wd, np, wd, lane, gg);
+      fold_chains<NPL, (FBW ? FBW : (NPL <= 2 ? 16 / NPL : 2))>(P + (long)r * wd, (long)rows * wd, np, wd, lane, gg);
     } else {
 #pragma unroll
       for (int s = 0; s < NPL; ++s) gg[s] = s * 64 + lane < wd ? G[(long)r * wd + s * 64 + lane] : 0.0f;
@@ -1424,7 +1425,13 @@ hipError_t cd_subblock(hipStream_t st, int rows, int n, int ng, int g, int c0, i
   hipLaunchKernelGGL((k_cd<N>), grid, blk, 0, st, rows, n, ng, g, c0, wd, sb, nsb, rc, sweeps, G, h32, gbits, scales,  \
                      zeros, codes, wq, e, active, sel, dlog, dcnt, cap, mid, evals, P, np)
   switch (npl_for(wd)) {
-    case 1: CD_CASE(1); break;
+    case 1:
+      if (P && np > 16)  // many panels: fewer, wider fold batches
+        hipLaunchKernelGGL((k_cd<1, 32>), grid, blk, 0, st, rows, n, ng, g, c0, wd, sb, nsb, rc, sweeps, G, h32, gbits,
+                           scales, zeros, codes, wq, e, active, sel, dlog, dcnt, cap, mid, evals, P, np);
+      else
+        CD_CASE(1);
+      break;
     case 2: CD_CASE(2); break;
     case 4: CD_CASE(4); break;
     case 8: CD_CASE(8); break;
