@@ -319,7 +319,8 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
 // Requirements (checked by the host): A rows run along k (A[i][k], k contiguous); B either along
 // k (BT: B[k][j] = Bt[j][k]) or along j (B[k][j]); every row start 16-byte aligned; k, the k range
 // of every tile and kfold multiples of DMK; n even when B runs along j. Workgroup tile BM x 128
-// (BM = 128: the Cholesky's trailing updates; 96: the inverse's block rows), BM / 32 x 2 waves,
+// (BM = 128: the Cholesky's trailing updates; 64: its left-looking block-column updates; 96: the
+// inverse's block rows), BM / 32 x 2 waves,
 // wave (wr, wc) owning rows 32 wr .. +31 and columns 64 wc .. +63 as 2 x 4 blocks of 16 x 16.
 // Stages of DMK = 16 k are filled with global_load_lds_dwordx4 into a ring of DMS, DMS - 1 stages
 // in flight, one bare barrier per stage. A k-contiguous operand is staged as [row][8 slots of 16 B]
@@ -605,10 +606,16 @@ bool aligned16(const void* p) { return (uintptr_t)p % 16 == 0; }
 
 hipError_t chol_update(hipStream_t st, int m, int n, int k, const double* P, long ldp, double* C, long ldc) {
   if (m <= 0 || n <= 0 || k <= 0) return hipSuccess;
-  if (n >= 64 && m >= 2 && k % DMK == 0 && aligned16(P) && ldp % 2 == 0) {  // the pipelined 128 x 128 tiles
-    const dim3 grid((n + DMN - 1) / DMN, (m + 127) / 128, 1);
-    hipLaunchKernelGGL((k_dmm<128, true, false>), grid, dim3(512), 0, st, m, n, k, -1.0, 1.0, P, ldp, P, ldp, C,
-                       ldc, (double*)nullptr, 96, 1, 0);
+  if (n >= 64 && m >= 2 && k % DMK == 0 && aligned16(P) && ldp % 2 == 0) {  // the pipelined tiles
+    if (n <= DMN) {  // one block column (the left-looking updates): 64-row tiles, twice the workgroups
+      const dim3 grid(1, (m + 63) / 64, 1);
+      hipLaunchKernelGGL((k_dmm<64, true, false>), grid, dim3(256), 0, st, m, n, k, -1.0, 1.0, P, ldp, P, ldp, C,
+                         ldc, (double*)nullptr, 96, 1, 0);
+    } else {
+      const dim3 grid((n + DMN - 1) / DMN, (m + 127) / 128, 1);
+      hipLaunchKernelGGL((k_dmm<128, true, false>), grid, dim3(512), 0, st, m, n, k, -1.0, 1.0, P, ldp, P, ldp, C,
+                         ldc, (double*)nullptr, 96, 1, 0);
+    }
     return hipGetLastError();
   }
   const dim3 grid((n + DBN - 1) / DBN, (m + DBM - 1) / DBM, 1);
