@@ -175,8 +175,7 @@ int factor(cdclq_ctx* ctx, int n, double* a, double* y, float* u) {
       if (s > kp)  // the last, partial panel [kp, s)
         HIPCK(inv_acc(st, w, s, s - kp, a + (long)s * n + kp, n, y + (long)kp * n, n, T + (long)s * n, n));
       if (inv_gemm_eligible(w, s, w, y + (long)s * n + s, n, T + (long)s * n, n))
-        HIPCK(inv_gemm(st, w, s, w, -1.0, y + (long)s * n + s, n, T + (long)s * n, n, y + (long)s * n, n, nullptr,
-                       false));
+        HIPCK(inv_gemm(st, w, s, w, -1.0, y + (long)s * n + s, n, T + (long)s * n, n, y + (long)s * n, n));
       else
         HIPCK(gemm_chain<double>(st, w, s, w, -1.0, 0, y + (long)s * n + s, n, 1, T + (long)s * n, n, 1,
                                  y + (long)s * n, n, 1, false, (double*)nullptr));

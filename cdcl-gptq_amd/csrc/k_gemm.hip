@@ -631,23 +631,12 @@ bool inv_gemm_eligible(int m, int n, int k, const double* A, long lda, const dou
 }
 
 hipError_t inv_gemm(hipStream_t st, int m, int n, int k, double alpha, const double* A, long lda, const double* B,
-                    long ldb, double* C, long ldc, double* partials, bool b_lower_tri) {
+                    long ldb, double* C, long ldc) {
   if (m <= 0 || n <= 0 || k <= 0) return hipSuccess;
-  const int np = (k + CDCLQ_KC - 1) / CDCLQ_KC;
-  const int bt = b_lower_tri ? 1 : 0;
-  dim3 grid((n + DMN - 1) / DMN, 1, 1);
-  if (np > 1 && partials) {
-    grid.z = np;
-    hipLaunchKernelGGL((k_dmm<96, false, true>), grid, dim3(384), 0, st, m, n, k, alpha, 0.0, A, lda, B, ldb, C, ldc,
-                       partials, CDCLQ_KC, 0, bt);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_combine<double>), dim3((unsigned)(((long)m * n + 255) / 256)), dim3(256), 0, st, m, n, np,
-                       alpha, 0.0, (const double*)partials, C, ldc, 1L);
-    return hipGetLastError();
-  }
+  if (!inv_gemm_eligible(m, n, k, A, lda, B, ldb) || k > CDCLQ_KC) return hipErrorInvalidValue;
+  const dim3 grid((n + DMN - 1) / DMN, 1, 1);
   hipLaunchKernelGGL((k_dmm<96, false, false>), grid, dim3(384), 0, st, m, n, k, alpha, 0.0, A, lda, B, ldb, C, ldc,
-                     (double*)nullptr, CDCLQ_KC, 0, bt);
+                     (double*)nullptr, CDCLQ_KC, 0, 0);
   return hipGetLastError();
 }
 

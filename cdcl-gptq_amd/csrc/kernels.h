@@ -26,13 +26,12 @@ size_t gemm_partials_elems(int m, int n, int k);
 // for each block b in order, C = fma(-1, chain_b, C) with chain_b the 96-step FMA chain of
 // P[:, b] P[0:n, b]^T (src/linalg.rs:243-270, one dgemm per block).
 hipError_t chol_update(hipStream_t st, int m, int n, int k, const double* P, long ldp, double* C, long ldc);
-// The triangular inverse's block-row products C = alpha * A B (beta = 0, m <= 96 rows, A along k,
-// B along n; src/linalg.rs:307-343) on the pipelined kernel, panels in parallel into `partials`
-// and folded in order when k spans several KC panels. inv_gemm_eligible lists the requirements
-// (else use gemm_chain).
+// The triangular inverse's product Y[s:e, 0:s] = alpha Y_ss t (beta = 0, m <= 96 rows, k <= KC: one
+// panel; A along k, B along n; src/linalg.rs:330-343) on the pipelined kernel. inv_gemm_eligible
+// lists the requirements (else use gemm_chain).
 bool inv_gemm_eligible(int m, int n, int k, const double* A, long lda, const double* B, long ldb);
 hipError_t inv_gemm(hipStream_t st, int m, int n, int k, double alpha, const double* A, long lda, const double* B,
-                    long ldb, double* C, long ldc, double* partials, bool b_lower_tri);
+                    long ldb, double* C, long ldc);
 
 // C = fma(1, chain, C) for one k range of at most one KC panel (A along k, B along j): a panel's
 // contribution to the triangular inverse's block-row products, applied right-looking to every
