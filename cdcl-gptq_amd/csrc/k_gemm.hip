@@ -329,6 +329,7 @@ __global__ __launch_bounds__(256) void k_dgemm_mfma(int m, int n, int k, double 
 // matrix are read from clamped addresses and only reach outputs that are never stored. b_tri
 // (B lower triangular, beta == 0) starts each tile's k loop at its first column, as in k_dgemm_mfma.
 constexpr int DMK = 16, DMS = 4, DMN = 128;
+constexpr long kDmmWide = 512;  // 128-row tiles from two full rounds of one workgroup per CU (256 CUs)
 template <int BM, bool BT, bool SPLIT>
 __global__ __launch_bounds__(BM * 4) void k_dmm(int m, int n, int k, double alpha, double beta,
                                                const double* __restrict__ A, long lda, const double* __restrict__ B,
@@ -607,8 +608,10 @@ bool aligned16(const void* p) { return (uintptr_t)p % 16 == 0; }
 hipError_t chol_update(hipStream_t st, int m, int n, int k, const double* P, long ldp, double* C, long ldc) {
   if (m <= 0 || n <= 0 || k <= 0) return hipSuccess;
   if (n >= 64 && m >= 2 && k % DMK == 0 && aligned16(P) && ldp % 2 == 0) {  // the pipelined tiles
-    if (n <= DMN) {  // one block column (the left-looking updates): 64-row tiles, twice the workgroups
-      const dim3 grid(1, (m + 63) / 64, 1);
+    // 64-row tiles (twice the workgroups) where 128-row ones would fill the device less than twice:
+    // the left-looking updates and a period's main-stream pass
+    if ((long)((n + DMN - 1) / DMN) * ((m + 127) / 128) < kDmmWide) {
+      const dim3 grid((n + DMN - 1) / DMN, (m + 63) / 64, 1);
       hipLaunchKernelGGL((k_dmm<64, true, false>), grid, dim3(256), 0, st, m, n, k, -1.0, 1.0, P, ldp, P, ldp, C,
                          ldc, (double*)nullptr, 96, 1, 0);
     } else {
@@ -649,9 +652,13 @@ hipError_t inv_acc(hipStream_t st, int m, int n, int k, const double* A, long ld
                    double* C, long ldc) {
   if (m <= 0 || n <= 0 || k <= 0) return hipSuccess;
   if (!inv_acc_eligible(m, n, k, A, lda, B, ldb)) return hipErrorInvalidValue;
-  if (m > 96) {  // the rows below a panel: 128-row tiles
+  if (m > 96 && (long)((n + DMN - 1) / DMN) * ((m + 127) / 128) >= kDmmWide) {  // the rows below a panel
     const dim3 grid((n + DMN - 1) / DMN, (m + 127) / 128, 1);
     hipLaunchKernelGGL((k_dmm<128, false, false>), grid, dim3(512), 0, st, m, n, k, 1.0, 1.0, A, lda, B, ldb, C, ldc,
+                       (double*)nullptr, CDCLQ_KC, 0, 0);
+  } else if (m > 96) {  // a panel whose 128-row tiles would fill the device less than twice
+    const dim3 grid((n + DMN - 1) / DMN, (m + 63) / 64, 1);
+    hipLaunchKernelGGL((k_dmm<64, false, false>), grid, dim3(256), 0, st, m, n, k, 1.0, 1.0, A, lda, B, ldb, C, ldc,
                        (double*)nullptr, CDCLQ_KC, 0, 0);
   } else {  // one block row
     const dim3 grid((n + DMN - 1) / DMN, 1, 1);
