@@ -400,6 +400,14 @@ def test_quantize_wide_gradient_tiles(ctx):
                 label="wide gradient tiles")
 
 
+def test_quantize_descent_fold_of_many_panels(ctx):
+    """Gradients of more than 16 KC panels (n = 4608: 18 panels) take the descent form that folds
+    the per-panel chains 32 at a time; 2 passes, act-order, against the live oracle."""
+    w, x, h, _ = synth_layer(71, 96, 4608, 5000)
+    assert_same(*run_both(ctx, w, h, bits=4, group=128, block=128, act_order=True, passes=2, row_chunk=32),
+                label="descent fold of 18 panels")
+
+
 @pytest.mark.parametrize("block,group,sub_block,mse", [(2048, 128, 1280, False), (1536, 1536, 1100, True),
                                                        (4096, 0, 64, False)])
 def test_quantize_blocks_wider_than_1024(ctx, block, group, sub_block, mse):
