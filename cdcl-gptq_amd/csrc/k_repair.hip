@@ -26,6 +26,7 @@ namespace {
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 typedef float v32f __attribute__((ext_vector_type(32)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int PR = 128;  // rows per panel-GEMM workgroup (32 per wave)
 constexpr int PC = 64;   // cols per panel-GEMM workgroup
@@ -739,21 +740,59 @@ __global__ __launch_bounds__(256) void k_refit_mfma(int rows, int n, int ng, int
   }
   __syncthreads();
   if (nlive == 0) return;
-  const bool vec = wd == 128 && (n & 3) == 0 && (c0 & 3) == 0;  // whole, 16-byte aligned rows
+  // Whole groups fold the GEMM's per-panel chains with 16-byte loads (below); the first batch of
+  // FB0 panels is issued here, so that its latency overlaps the H_CC staging and the hu chains
+  // (not in the 64-row form, whose registers would then allow one workgroup per CU).
+  constexpr int PER4 = RF_ROWS * 32 / 256;
+  constexpr int FB4 = PER4 == 2 ? 16 : (PER4 == 4 ? 8 : 4);
+  constexpr int FB0 = RF_ROWS == 64 ? 0 : FB4;
+  const bool fvec = P && wd == 128 && (reinterpret_cast<uintptr_t>(P) & 15) == 0;
+  const long pstride4 = (long)rows * 128;
+  v4f v0[FB0 ? FB0 : 1][PER4];
+  auto issue_v0 = [&]() {
+    if (FB0) {
+#pragma unroll
+      for (int u = 0; u < FB0; ++u) {
+        const long po = (long)min(u, np - 1) * pstride4;
+#pragma unroll
+        for (int i = 0; i < PER4; ++i) {
+          const int x = tid + 256 * i, rl = x >> 5, k4 = x & 31;
+          v0[u][i] = __builtin_nontemporal_load(
+              reinterpret_cast<const v4f*>(P + po + (long)min(r0 + rl, rows - 1) * 128 + 4 * k4));
+        }
+      }
+    }
+  };
+  // whole, 16-byte aligned rows, with chains to fold (the engine always passes them here)
+  const bool vec = fvec && (n & 3) == 0 && (c0 & 3) == 0;
   if (vec) {  // stage H_CC with 16-byte loads (16 per thread, all in flight) and the codes by words
+    // (issued before the fold's first batch, unconditionally in this branch: vector loads complete
+    // in order, so the LDS stores then wait for these loads only)
+    v4f hq[16];
+    uint32_t cw[RF_ROWS * 32 / 256];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       const int x = tid + 256 * u;  // float4 slot: row x >> 5, columns 4 (x & 31) ..
-      *reinterpret_cast<float4*>(&S[4 * x]) =
-          *reinterpret_cast<const float4*>(h32 + (long)(c0 + (x >> 5)) * n + c0 + 4 * (x & 31));
+      hq[u] = *reinterpret_cast<const v4f*>(h32 + (long)(c0 + (x >> 5)) * n + c0 + 4 * (x & 31));
     }
 #pragma unroll
     for (int u = 0; u < RF_ROWS * 32 / 256; ++u) {
       const int x = tid + 256 * u, rl = x >> 5, k4 = x & 31;
       const int r = min(r0 + rl, rows - 1);
-      CB[rl * (RF_CS / 4) + k4] = *reinterpret_cast<const uint32_t*>(codes + (long)r * n + c0 + 4 * k4);
+      cw[u] = *reinterpret_cast<const uint32_t*>(codes + (long)r * n + c0 + 4 * k4);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    issue_v0();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) *reinterpret_cast<v4f*>(&S[4 * (tid + 256 * u)]) = hq[u];
+#pragma unroll
+    for (int u = 0; u < RF_ROWS * 32 / 256; ++u) {
+      const int x = tid + 256 * u, rl = x >> 5, k4 = x & 31;
+      CB[rl * (RF_CS / 4) + k4] = cw[u];
     }
   } else {  // clamped scalar loads, zero padding outside wd
+    if (fvec) issue_v0();
     constexpr int PER = 128 * 128 / 256, BATCH = 16;
 #pragma unroll
     for (int b = 0; b < PER; b += BATCH) {
@@ -828,7 +867,57 @@ __global__ __launch_bounds__(256) void k_refit_mfma(int rows, int n, int ng, int
       PH[row * RF_PS + col] = u * __builtin_fmaf(1.0f, acc[r], 0.0f);
     }
   }
-  {  // u_k * g_k: all of a thread's G loads in flight at once (clamped addresses)
+  if (fvec) {
+    // u_k * g_k for whole groups: the same ordered fold with 16-byte loads. Slot x = tid + 256 i
+    // covers row x >> 5, columns 4 (x & 31) .. + 3, so a batch of FB4 panels is FB4 * PER4
+    // loads a thread (at most 40 in flight, below the wave's 63 outstanding vector loads) and the
+    // 56 panels of a 14336-wide input take 3 batches instead of 7.
+    const long pstride = pstride4;
+    v4f acc4[PER4];
+#pragma unroll
+    for (int i = 0; i < PER4; ++i) acc4[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < FB0; ++u) {
+      if (u < np) {  // uniform
+#pragma unroll
+        for (int i = 0; i < PER4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc4[i][j] = __builtin_fmaf(1.0f, v0[u][i][j], acc4[i][j]);
+      }
+    }
+    for (int p = FB0; p < np; p += FB4) {
+      v4f v[FB4][PER4];
+#pragma unroll
+      for (int u = 0; u < FB4; ++u) {
+        const long po = (long)min(p + u, np - 1) * pstride;
+#pragma unroll
+        for (int i = 0; i < PER4; ++i) {
+          const int x = tid + 256 * i, rl = x >> 5, k4 = x & 31;
+          v[u][i] = __builtin_nontemporal_load(
+              reinterpret_cast<const v4f*>(P + po + (long)min(r0 + rl, rows - 1) * 128 + 4 * k4));
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before the first add
+#pragma unroll
+      for (int u = 0; u < FB4; ++u) {
+        if (p + u < np) {  // uniform
+#pragma unroll
+          for (int i = 0; i < PER4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc4[i][j] = __builtin_fmaf(1.0f, v[u][i][j], acc4[i][j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PER4; ++i) {
+      const int x = tid + 256 * i, rl = x >> 5, k4 = x & 31;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = 4 * k4 + j;
+        PG[rl * RF_PS + k] = ((float)cb[rl * RF_CS + k] - zrow[rl]) * acc4[i][j];
+      }
+    }
+  } else {  // u_k * g_k: all of a thread's G loads in flight at once (clamped addresses)
     constexpr int PER = RF_ROWS * 128 / 256;
     float gv[PER];
     if (P) {
