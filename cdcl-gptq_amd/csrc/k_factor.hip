@@ -64,10 +64,17 @@ __global__ __launch_bounds__(256) void k_build_flipped_f64(int n, const double* 
 // end; the remaining steps run on with values that are discarded with the error.
 constexpr int DGL = 8;           // lane grid side
 constexpr int DSL = NBC / DGL;   // row / column slots per lane
+__device__ __forceinline__ double readlane_f64(double v, int l) {  // l uniform
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffLL), l);
+  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
 __global__ __launch_bounds__(64) void k_chol_diag(int n, double* __restrict__ a, int k, int kb, int* status,
                                                   double* pivot) {
   __shared__ double pre[NBC + 64];  // column t with all earlier columns applied; + a discard slot per lane
-  __shared__ double col[NBC];       // column t of L (zero above row t)
+  __shared__ double col[NBC + 32];  // column t of L (zero above row t); + discard slots for lanes 32..63
   if (*status) return;
   const int lane = threadIdx.x, tr = lane >> 3, tc = lane & 7;
   double v[DSL][DSL];
@@ -87,19 +94,21 @@ __global__ __launch_bounds__(64) void k_chol_diag(int n, double* __restrict__ a,
 #pragma unroll
     for (int r = ctn; r < DSL; ++r) pre[own ? DGL * r + tr : NBC + lane] = v[r][ctn];
   };
-  // pivot of column tn and the divided column of L into LDS (values past kb are computed from
+  // pivot d of column tn (read by the caller from the register of its owner lane, so that the
+  // square root starts without an LDS round trip), its square root and the divided column of L
+  // into LDS; both dividends are read before the square root (values past kb are computed from
   // clamped reads and never stored)
-  auto divide = [&](int tn) {
-    const double d = pre[tn];
+  auto divide = [&](int tn, double d) {
+    const double p0 = pre[lane], p1 = pre[min(lane + 64, NBC - 1)];
     const bool rec = (!(d > 0.0) || !isfinite(d)) && fail_t < 0 && tn < kb;
     fail_d = rec ? d : fail_d;
     fail_t = rec ? tn : fail_t;
     const double ltt = sqrt(d);
-    const double q0 = pre[lane] / ltt, q1 = pre[min(lane + 64, NBC - 1)] / ltt;
+    const double q0 = p0 / ltt, q1 = p1 / ltt;
     c0 = (lane == tn) ? ltt : ((lane > tn && lane < kb) ? q0 : 0.0);
     c1 = (lane + 64 == tn) ? ltt : ((lane + 64 > tn && lane + 64 < kb) ? q1 : 0.0);
     col[lane] = c0;
-    if (lane + 64 < NBC) col[lane + 64] = c1;
+    col[lane < 32 ? lane + 64 : NBC + lane - 32] = c1;
   };
   auto store_col = [&](int tn) {
     if (lane >= tn && lane < kb) a[(long)(k + lane) * n + k + tn] = c0;
@@ -107,7 +116,7 @@ __global__ __launch_bounds__(64) void k_chol_diag(int n, double* __restrict__ a,
   };
   double ci[DSL], cj[DSL];  // column t of L at rows DGL q + tr (ci) and DGL q + tc (cj)
   publish(0, 0);
-  divide(0);
+  divide(0, readlane_f64(v[0][0], 0));
   store_col(0);
 #pragma unroll
   for (int q = 0; q < DSL; ++q) {
@@ -123,7 +132,7 @@ __global__ __launch_bounds__(64) void k_chol_diag(int n, double* __restrict__ a,
 #pragma unroll
         for (int r = ct; r < DSL; ++r) v[r][ct] = v[r][ct] - ci[r] * cj[ct];
         publish(ct, lt + 1);
-        divide(t + 1);
+        divide(t + 1, readlane_f64(v[ct][ct], (DGL + 1) * (lt + 1)));  // l_{t+1,t+1}: lane 9 ((t + 1) % 8)
 #pragma unroll
         for (int r = ct + 1; r < DSL; ++r)
 #pragma unroll
@@ -138,7 +147,7 @@ __global__ __launch_bounds__(64) void k_chol_diag(int n, double* __restrict__ a,
 #pragma unroll
         for (int r = ct + 1; r < DSL; ++r) v[r][ct + 1] = v[r][ct + 1] - ci[r] * cj[ct + 1];
         publish(ct + 1, 0);
-        divide(t + 1);
+        divide(t + 1, readlane_f64(v[ct + 1][ct + 1], 0));
 #pragma unroll
         for (int r = ct + 2; r < DSL; ++r)
 #pragma unroll
