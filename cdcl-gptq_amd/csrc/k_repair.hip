@@ -295,7 +295,17 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
   int fc = 0;
   v32f acc = {};
   Unit pu = iu;  // without C: the unit whose chains acc holds
+  // Register r of the accumulator holds row (r & 3) + 8 ((r & 15) >> 2) + 4 (lane >> 5) of the
+  // wave's 32 rows and column 32 (r >> 4) + (lane & 31): relative to the lane's first element its
+  // offset is uniform, so a whole tile (the common case, a uniform test) needs one address per lane.
+  auto roff = [](int r, long ld) { return ((r & 3) + 8 * ((r & 15) >> 2)) * ld + 32 * (r >> 4); };
   auto store_p = [&](const Unit& t) {
+    if (t.r0 + PR <= m && t.cb + PC <= wd) {
+      float* q = P + ((long)t.p * m + t.r0 + 32 * wv + 4 * (lane >> 5)) * wd + t.cb + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 32; ++r) __builtin_nontemporal_store(acc[r], q + roff(r, wd));
+      return;
+    }
     // block b = r >> 4 (cols 32b..), row i = (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), col j = lane & 31
 #pragma unroll
     for (int r = 0; r < 32; ++r) {
@@ -321,11 +331,20 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
       // C is loaded before the stage after next, so the next stage's wait (everything but the
       // newest stage's loads) covers it rather than also holding back that stage.
       if (DIRECT && cs == 0) {
+        if (!beta_one) {
 #pragma unroll
-        for (int r = 0; r < 32; ++r) {  // clamped addresses; values outside m x wd are never used
-          const int row = min(cu.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), m - 1);
-          const int col = min(cu.cb + 32 * (r >> 4) + (lane & 31), wd - 1);
-          cv[r] = beta_one ? C[(long)row * ldc + col] : 0.0f;
+          for (int r = 0; r < 32; ++r) cv[r] = 0.0f;
+        } else if (cu.r0 + PR <= m && cu.cb + PC <= wd) {
+          const float* q = C + (long)(cu.r0 + 32 * wv + 4 * (lane >> 5)) * ldc + cu.cb + (lane & 31);
+#pragma unroll
+          for (int r = 0; r < 32; ++r) cv[r] = q[roff(r, ldc)];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 32; ++r) {  // clamped addresses; values outside m x wd are never used
+            const int row = min(cu.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), m - 1);
+            const int col = min(cu.cb + 32 * (r >> 4) + (lane & 31), wd - 1);
+            cv[r] = C[(long)row * ldc + col];
+          }
         }
       }
       if (!DIRECT || cs + 1 < cu.nst) issue_next();  // into the slot of stage fc - 1
@@ -348,11 +367,17 @@ __global__ __launch_bounds__(256) void k_panel_dma(int m, int wd, int k, const f
       }
     }
     if (DIRECT) {
+      if (cu.r0 + PR <= m && cu.cb + PC <= wd) {
+        float* q = C + (long)(cu.r0 + 32 * wv + 4 * (lane >> 5)) * ldc + cu.cb + (lane & 31);
 #pragma unroll
-      for (int r = 0; r < 32; ++r) {
-        const int row = cu.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
-        const int col = cu.cb + 32 * (r >> 4) + (lane & 31);
-        if (row < m && col < wd) C[(long)row * ldc + col] = __builtin_fmaf(alpha, acc[r], cv[r]);
+        for (int r = 0; r < 32; ++r) q[roff(r, ldc)] = __builtin_fmaf(alpha, acc[r], cv[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 32; ++r) {
+          const int row = cu.r0 + 32 * wv + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
+          const int col = cu.cb + 32 * (r >> 4) + (lane & 31);
+          if (row < m && col < wd) C[(long)row * ldc + col] = __builtin_fmaf(alpha, acc[r], cv[r]);
+        }
       }
       acc = v32f{};
       issue_next();  // the load deferred at the unit's last stage
@@ -461,7 +486,15 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
   int fc = 0;
   v32f acc = {};
   Unit pu = iu;
+  // as in k_panel_dma: a whole tile stores from one address per lane plus uniform offsets
+  auto roff = [](int r, long ld) { return ((r & 3) + 8 * ((r & 15) >> 2)) * ld + 32 * (r >> 4); };
   auto store_p = [&](const Unit& t) {
+    if (t.r0 + PR <= m && LPC <= wd) {
+      float* q = P + ((long)t.p * m + t.r0 + 32 * wr + 4 * (lane >> 5)) * wd + 64 * wc + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 32; ++r) __builtin_nontemporal_store(acc[r], q + roff(r, wd));
+      return;
+    }
 #pragma unroll
     for (int r = 0; r < 32; ++r) {
       const int row = t.r0 + 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
@@ -483,11 +516,17 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
         acc = v32f{};
       }
       if (DIRECT && cs == 0) {
+        if (cu.r0 + PR <= m && cu.cb + LPC <= wd) {
+          const float* q = C + (long)(cu.r0 + 32 * wr + 4 * (lane >> 5)) * ldc + cu.cb + 64 * wc + (lane & 31);
 #pragma unroll
-        for (int r = 0; r < 32; ++r) {
-          const int row = min(cu.r0 + 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), m - 1);
-          const int col = min(cu.cb + 64 * wc + 32 * (r >> 4) + (lane & 31), wd - 1);
-          cv[r] = C[(long)row * ldc + col];
+          for (int r = 0; r < 32; ++r) cv[r] = q[roff(r, ldc)];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 32; ++r) {
+            const int row = min(cu.r0 + 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5), m - 1);
+            const int col = min(cu.cb + 64 * wc + 32 * (r >> 4) + (lane & 31), wd - 1);
+            cv[r] = C[(long)row * ldc + col];
+          }
         }
       }
       issue_next();
@@ -510,11 +549,17 @@ __global__ __launch_bounds__(512) void k_lazy_wide(int m, int wd, int k, const f
       }
     }
     if (DIRECT) {
+      if (cu.r0 + PR <= m && cu.cb + LPC <= wd) {
+        float* q = C + (long)(cu.r0 + 32 * wr + 4 * (lane >> 5)) * ldc + cu.cb + 64 * wc + (lane & 31);
 #pragma unroll
-      for (int r = 0; r < 32; ++r) {
-        const int row = cu.r0 + 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
-        const int col = cu.cb + 64 * wc + 32 * (r >> 4) + (lane & 31);
-        if (row < m && col < wd) C[(long)row * ldc + col] = __builtin_fmaf(alpha, acc[r], cv[r]);
+        for (int r = 0; r < 32; ++r) q[roff(r, ldc)] = __builtin_fmaf(alpha, acc[r], cv[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 32; ++r) {
+          const int row = cu.r0 + 32 * wr + (r & 3) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5);
+          const int col = cu.cb + 64 * wc + 32 * (r >> 4) + (lane & 31);
+          if (row < m && col < wd) C[(long)row * ldc + col] = __builtin_fmaf(alpha, acc[r], cv[r]);
+        }
       }
       acc = v32f{};
     } else {
