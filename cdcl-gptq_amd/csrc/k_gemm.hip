@@ -398,17 +398,31 @@ __global__ __launch_bounds__(BM * 4) void k_dmm(int m, int n, int k, double alph
         cv[bi][bj][r] = 0.0;
       }
   for (int st = 0; st < DMS - 1 && st < nst; ++st) issue(st);
+  // Element (bi, bj, r) of a lane lies at a uniform offset from the lane's first one, so a whole
+  // tile (a uniform test) loads and stores C from one address per lane.
+  const bool whole = i0 + BM <= m && j0 + DMN <= n;
+  const long cbase = (long)(i0 + 32 * wr + (lane >> 4)) * ldc + j0 + 64 * wc + (lane & 15);
+  auto coff = [&](int bi, int bj, int r) { return (long)(16 * bi + 4 * r) * ldc + 16 * bj; };
   if (!SPLIT && beta != 0.0) {  // C' = beta * C; 1 * C is C itself
+    if (whole) {
 #pragma unroll
-    for (int bi = 0; bi < 2; ++bi)
+      for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
-      for (int bj = 0; bj < 4; ++bj)
+        for (int bj = 0; bj < 4; ++bj)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int gi = min(i0 + 32 * wr + 16 * bi + (lane >> 4) + 4 * r, m - 1);
-          const int gj = min(j0 + 64 * wc + 16 * bj + (lane & 15), n - 1);
-          cv[bi][bj][r] = C[(long)gi * ldc + gj];
-        }
+          for (int r = 0; r < 4; ++r) cv[bi][bj][r] = C[cbase + coff(bi, bj, r)];
+    } else {
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int gi = min(i0 + 32 * wr + 16 * bi + (lane >> 4) + 4 * r, m - 1);
+            const int gj = min(j0 + 64 * wc + 16 * bj + (lane & 15), n - 1);
+            cv[bi][bj][r] = C[(long)gi * ldc + gj];
+          }
+    }
     // one wait here (with the first stages in flight) instead of one the compiler would place at
     // every fold inside the loop, where it would also drain the stage ring
     wait_vmcnt<0>();
@@ -480,6 +494,15 @@ __global__ __launch_bounds__(BM * 4) void k_dmm(int m, int n, int k, double alph
             }
       }
     }
+  }
+  if (!SPLIT && whole) {
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+      for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) C[cbase + coff(bi, bj, r)] = cv[bi][bj][r];
+    return;
   }
 #pragma unroll
   for (int bi = 0; bi < 2; ++bi)
