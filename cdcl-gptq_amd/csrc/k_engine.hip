@@ -378,7 +378,21 @@ __global__ __launch_bounds__(64 * W) void k_gptq_rows(int rows, int n, int i1, i
 #pragma unroll
         for (int t2 = 0; t2 < VPL; ++t2) uv[t2] = ub[i * 128 + VPL * ll + t2];
         const float di = idv[i];
-        const float xv = __shfl(x[t], base + oi, 64);
+        float xv;  // column i of the row: lane base + oi's x[t]
+        if constexpr (L >= 32) {
+          // read from each row group's owner lane (uniform lane indices) and selected by row group:
+          // a few cycles, against a cross-lane permute through the LDS unit on the step's chain
+          // (with four or more row groups per wavefront the extra instructions cost more than the
+          // permute's latency in these issue-bound sweeps)
+          xv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x[t]), oi));
+#pragma unroll
+          for (int q = 1; q < R; ++q) {
+            const float sq = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x[t]), q * L + oi));
+            xv = rr == q ? sq : xv;
+          }
+        } else {
+          xv = __shfl(x[t], base + oi, 64);
+        }
         float q;
         const float dq = quant_dq(xv, sc, zr, maxq, &q);
         if (ll == 0) near_codes += near_midpoint(xv, sc, zr, maxq) ? 1u : 0u;
