@@ -56,14 +56,17 @@ __global__ __launch_bounds__(256) void k_build_flipped_f64(int n, const double* 
 // that column to its slots. LDS accesses of one wavefront complete in order, so a read issued
 // after a write sees it. Slot columns left of t's are skipped; the registers of finished columns
 // (and of the upper triangle) that are still updated are never read again.
-// The steps are software-pipelined: step t first updates the slot column that holds column t + 1
-// and publishes it, then runs column t + 1's pivot, square root and divisions while it applies
-// column t to the rest of its slots (no branch between them, so the two interleave), then stores
-// column t + 1 of L and reads it back for step t + 1. Every element still receives the same
-// operations in the same order. A failing pivot is recorded (the first one) and reported at the
-// end; the remaining steps run on with values that are discarded with the error.
+// Step t first updates the slot column that holds column t + 1 and publishes it, then runs
+// column t + 1's pivot (read from the register of the lane that holds it), square root and
+// divisions, applies column t to the rest of its slots, and stores column t + 1 of L and reads it
+// back for step t + 1. Every element still receives the same operations in the same order. The
+// block's time is this per-column chain (the square root, the divisions, two LDS round trips):
+// spreading the slots over four wavefronts measured no faster. A failing pivot is recorded (the
+// first one) and reported at the end; the remaining steps run on with values that are discarded
+// with the error.
 constexpr int DGL = 8;           // lane grid side
 constexpr int DSL = NBC / DGL;   // row / column slots per lane
+
 __device__ __forceinline__ double readlane_f64(double v, int l) {  // l uniform
   const long long b = __double_as_longlong(v);
   const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffLL), l);
