@@ -335,7 +335,14 @@ __global__ __launch_bounds__(64 * W) void k_gptq_rows(int rows, int n, int i1, i
     }
   }
   float sc = 0.0f, zr = 0.0f, maxq = 0.0f;
-  unsigned near_codes = 0, near_zeros = 0;  // counted once per row, by its lane 0
+  unsigned near_codes = 0, near_zeros = 0;  // zero points: counted once per row, by its lane 0
+  // With at most 8 columns per lane (the launcher keeps g a multiple of 8 here) a lane's columns lie
+  // in one group, so each lane tests its own columns' code decisions for a near midpoint after the
+  // sweep, from the value each had when it was decided (xs) and its group's grid (gsc, gzr, gmq),
+  // instead of the row's lane 0 testing every column inside the sweep's dependent chain.
+  constexpr bool DEFER = VPL <= 8;
+  float xs[DEFER ? VPL : 1];
+  float gsc = 0.0f, gzr = 0.0f, gmq = 0.0f;
   const int base = rr * L;                  // the row group's first lane
   for (int oi = 0; oi < L; ++oi) {          // owner lane of the columns VPL oi .. +VPL - 1
 #pragma unroll
@@ -366,6 +373,13 @@ __global__ __launch_bounds__(64 * W) void k_gptq_rows(int rows, int n, int i1, i
             xmax = 1.0f;
           }
           grid_mk(xmin, xmax, maxq, &sc, &zr);
+          if constexpr (DEFER) {
+            if (VPL * ll >= i && VPL * ll < i + g) {  // this lane's columns are in the group
+              gsc = sc;
+              gzr = zr;
+              gmq = maxq;
+            }
+          }
           if (ll == 0) {
             near_zeros += near_midpoint(-xmin, sc, 0.0f, maxq) ? 1u : 0u;
             if (live) {
@@ -395,9 +409,12 @@ __global__ __launch_bounds__(64 * W) void k_gptq_rows(int rows, int n, int i1, i
         }
         float q;
         const float dq = quant_dq(xv, sc, zr, maxq, &q);
-        if (ll == 0) near_codes += near_midpoint(xv, sc, zr, maxq) ? 1u : 0u;
+        if constexpr (!DEFER) {
+          if (ll == 0) near_codes += near_midpoint(xv, sc, zr, maxq) ? 1u : 0u;
+        }
         const float e = (xv - dq) * di;
         if (ll == oi) {
+          if constexpr (DEFER) xs[t] = xv;
           if constexpr (PACK)
             mcode[t >> 2] = (mcode[t >> 2] & ~(0xffu << (8 * (t & 3)))) | ((uint32_t)code_of(q) << (8 * (t & 3)));
           else
@@ -422,6 +439,7 @@ __global__ __launch_bounds__(64 * W) void k_gptq_rows(int rows, int n, int i1, i
           codes[o] = code_of(mq[t]);
         wq[o] = mwq[t];
         err[o] = me[t];
+        if constexpr (DEFER) near_codes += near_midpoint(xs[t], gsc, gzr, gmq) ? 1u : 0u;
       }
     }
     if (near_codes) atomicAdd(&mid[MID_CODE_NEAR], (unsigned long long)near_codes);
@@ -777,8 +795,10 @@ hipError_t gptq_block(hipStream_t st, int rows, int n, int i1, int cnt, int g, i
   // Lanes per row: as few as keep about two wavefronts per SIMD busy (1024 SIMDs), at least 8.
   // Two 64 KB workgroups per CU, every row resident at once up to 32768 rows: 32 lanes per row
   // and 4 wavefronts per workgroup up to 4096 rows (at most 2 wavefronts per SIMD), 16 lanes and
-  // 8 wavefronts up to 16384 (at most 4 per SIMD), 8 lanes and 8 wavefronts above.
-  if (groups_in_block && !mse && cnt <= 128 && i1 % g == 0 && rows >= 2048) {
+  // 8 wavefronts up to 16384 (at most 4 per SIMD), 8 lanes and 8 wavefronts above. With 32 or 16
+  // lanes a lane's 4 or 8 columns must lie in one group (g a multiple of 8), for the deferred
+  // near-midpoint test; other groups take k_gptq_block.
+  if (groups_in_block && !mse && cnt <= 128 && i1 % g == 0 && rows >= 2048 && (g % 8 == 0 || rows > 16384)) {
     if (rows > 16384)
       hipLaunchKernelGGL((k_gptq_rows<8, 8>), dim3((rows + 63) / 64), dim3(512), 0, st, rows, n, i1, cnt, g, ng, w, u,
                          invd, gbits, scales, zeros, codes, wq, err, mid);
