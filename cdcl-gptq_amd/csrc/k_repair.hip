@@ -1054,8 +1054,38 @@ __global__ __launch_bounds__(256) void k_refit_mfma(int rows, int n, int ng, int
     snew[lane] = s_new;
   }
   __syncthreads();
-  // e += W_hat - ndq, W_hat = ndq on the accepted rows, in two halves of 16 elements per thread
-  // with all of a half's loads in flight at once
+  // e += W_hat - ndq, W_hat = ndq on the accepted rows. Whole, aligned groups: 16-byte accesses,
+  // slot x = tid + 256 i covering row x >> 5, columns 4 (x & 31) .. + 3, all loads in flight.
+  if (vec && ((reinterpret_cast<uintptr_t>(e) | reinterpret_cast<uintptr_t>(wq)) & 15) == 0) {
+    v4f ev[PER4], qv[PER4];
+#pragma unroll
+    for (int i = 0; i < PER4; ++i) {
+      const int x = tid + 256 * i, rl = x >> 5, k4 = x & 31;
+      if (mv[rl]) {
+        const long o = (long)(r0 + rl) * n + c0 + 4 * k4;
+        ev[i] = *reinterpret_cast<const v4f*>(e + o);
+        qv[i] = *reinterpret_cast<const v4f*>(wq + o);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PER4; ++i) {
+      const int x = tid + 256 * i, rl = x >> 5, k4 = x & 31;
+      if (mv[rl]) {
+        const long o = (long)(r0 + rl) * n + c0 + 4 * k4;
+        const uint32_t cw = *reinterpret_cast<const uint32_t*>(cb + rl * RF_CS + 4 * k4);
+        v4f ne, nq;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          nq[j] = snew[rl] * ((float)((cw >> (8 * j)) & 0xffu) - zrow[rl]);
+          ne[j] = ev[i][j] + (qv[i][j] - nq[j]);
+        }
+        *reinterpret_cast<v4f*>(e + o) = ne;
+        *reinterpret_cast<v4f*>(wq + o) = nq;
+      }
+    }
+    return;
+  }
+  // otherwise in two halves of 16 elements per thread with all of a half's loads in flight at once
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     constexpr int PER = RF_ROWS * 128 / 256 / 2;
